@@ -1,0 +1,180 @@
+/*
+ * lrnnx_scan.h -- C ABI of the MI355X (gfx950) scan hot path of lrnnx.
+ *
+ * The library (lrnnx_amd/liblrnnx_scan.so) replaces the two pybind11 torch
+ * extensions of the reference, `selective_scan_cuda` and
+ * `simplified_scan_cuda` (reference csrc/selective_scan/bindings.cpp:5-8,
+ * csrc/simplified_scan/bindings.cpp:5-8), and the Triton decode kernel
+ * `_selective_scan_update_kernel`
+ * (lrnnx/ops/triton/selective_state_update.py:17-297).
+ *
+ * Conventions
+ *  - Plain pointers and sizes only.  Every buffer (inputs, outputs and the
+ *    workspace) is allocated by the caller; the library never allocates, so
+ *    every entry point may be captured in a HIP graph.
+ *  - Sequence tensors have unit stride along L; their batch / channel
+ *    strides are given in ELEMENTS (int64).  Complex tensors are interleaved
+ *    (re, im) float pairs and their strides count complex elements.
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream of
+ *    the current device).  No host synchronisation happens inside.
+ *  - Return 0 on success.  Non-zero means the arguments were rejected or a
+ *    launch failed; `lrnnx_last_error()` then returns the message
+ *    (thread-local).  This mirrors the reference's TORCH_CHECK failures
+ *    (selective_scan_cpu.cpp:271-367) and C10_CUDA_KERNEL_LAUNCH_CHECK.
+ */
+#ifndef LRNNX_SCAN_H
+#define LRNNX_SCAN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (reference accepts u in {f32, f16, bf16}, weights in {f32, c64};
+ * selective_scan_cpu.cpp:268-270). */
+enum lrnnx_dtype { LRNNX_F32 = 0, LRNNX_F16 = 1, LRNNX_BF16 = 2, LRNNX_C64 = 3 };
+
+/* Discretisation methods, same numbering as the reference enum
+ * DiscretizationMethod (csrc/selective_scan/selective_scan.h:14-21). */
+enum lrnnx_method {
+  LRNNX_ZOH = 0, LRNNX_BILINEAR = 1, LRNNX_DIRAC = 2,
+  LRNNX_MAMBA = 3, LRNNX_S7 = 4, LRNNX_RGLRU = 5
+};
+
+/* A 1-to-4-D tensor view: pointer + element strides of the leading dims.
+ * For (b, d, l) sequences: s0 = batch stride, s1 = channel stride.
+ * For variable B/C (b, g, n, l): s0 = batch, s1 = group, s2 = state.
+ * For (d, n) weights: s0 = channel stride, s1 = state stride.
+ * For (d) vectors: s0 = channel stride. */
+typedef struct lrnnx_view {
+  void *ptr;
+  int64_t s0, s1, s2;
+} lrnnx_view;
+
+/*
+ * Selective scan (S6 / Mamba and the other discretisations).
+ * One struct serves forward and backward; fields unused by a call are ignored.
+ *
+ * Replaces selective_scan_cuda.fwd / .bwd
+ *   (reference csrc/selective_scan/selective_scan.h:114-136,
+ *    host code csrc/selective_scan/selective_scan_cpu.cpp:263-632).
+ */
+typedef struct lrnnx_selective_scan_args {
+  int64_t batch, dim, seqlen, dstate, n_groups;
+  int32_t itype;          /* dtype of u, delta, deltaA, z, out, out_z, dout, du, ddelta, ddeltaA, dz, variable B/C */
+  int32_t wtype;          /* LRNNX_F32 or LRNNX_C64: A and constant B/C */
+  int32_t method;         /* enum lrnnx_method */
+  int32_t var_B, var_C;   /* 1: (b, g, n, l) sequences (complex: real (.., 2l) interleaved); 0: (d, n) weights */
+  int32_t delta_softplus;
+  /* inputs (ptr == NULL means absent for D, z, delta_bias, deltaA) */
+  lrnnx_view u, delta, A, B, C, D, z, delta_bias, deltaA;
+  /* forward outputs */
+  lrnnx_view out;         /* y + D u before gating; may be NULL when z is given (then only out_z is written) */
+  lrnnx_view out_z;       /* out * silu(z); required iff z is given */
+  void *x;                /* chunk carries (b, d, ceil(l/2048), 2n) contiguous, weight dtype; may be NULL */
+  void *ckpt;             /* fine state checkpoints (fp32) for the backward; may be NULL in forward */
+  /* backward inputs/outputs */
+  lrnnx_view dout;        /* gradient of out_z (or of out when z is absent) */
+  lrnnx_view out_saved;   /* forward `out` (pre-gating); required by backward when z is given */
+  lrnnx_view du, ddelta, dA, dB, dC, dD, ddelta_bias, ddeltaA, dz;
+  /* scratch: at least lrnnx_selective_scan_workspace_size() bytes, 256-byte aligned */
+  void *workspace;
+  int64_t workspace_bytes;
+} lrnnx_selective_scan_args;
+
+/* Bytes of fp32 state checkpoints `ckpt` written by the forward for a later
+ * backward (0 if the shape needs none). */
+int64_t lrnnx_selective_scan_ckpt_size(const lrnnx_selective_scan_args *a);
+
+/* Bytes of workspace the call needs (bwd = 0: forward, 1: backward). */
+int64_t lrnnx_selective_scan_workspace_size(const lrnnx_selective_scan_args *a, int bwd);
+
+/* Forward.  Writes out / out_z / x and, if ckpt != NULL, the checkpoints.
+ * Replaces selective_scan_fwd (selective_scan_cpu.cpp:263-421). */
+int lrnnx_selective_scan_fwd(const lrnnx_selective_scan_args *a, void *stream);
+
+/* Backward.  Needs `ckpt` from a forward over the same inputs; when
+ * ckpt == NULL the checkpoints are rebuilt into the workspace first (the
+ * reference re-runs its chunk scan from `x`, selective_scan_backward.cuh:330).
+ * Writes du, ddelta, dA, dB, dC, dD, ddelta_bias, ddeltaA (if deltaA), dz
+ * (if z).  Variable dB/dC are written in the input dtype (the reference
+ * accumulates them in fp32 and casts, selective_scan_cpu.cpp:627); constant
+ * dB/dC and dA in the weight dtype; dD, ddelta_bias in f32.
+ * Replaces selective_scan_bwd (selective_scan_cpu.cpp:423-632). */
+int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args *a, void *stream);
+
+/*
+ * Simplified complex diagonal scan (S5 / LRU), complex64 only.
+ * u, out, du, dout: (b, p, l) complex; delta, deltaA, ddelta, ddeltaA:
+ * (b, p, l) real f32.  For delta / deltaA the view's s2 is the L stride and
+ * may be 0 (value constant along L; then A_bar is computed once per channel).
+ * A, B, C, dA, dB, dC: (p, ds) complex.  The forward writes `ckpt` (chunk
+ * start states) that the backward reuses; without it the backward rebuilds
+ * them in the workspace.
+ * Replaces simplified_scan_cuda.fwd / .bwd
+ *   (reference csrc/simplified_scan/simplified_scan.h:98-109,
+ *    host code csrc/simplified_scan/simplified_scan_cpu.cpp:160-331).
+ */
+typedef struct lrnnx_simplified_scan_args {
+  int64_t batch, dim, seqlen, dstate;
+  int32_t method;          /* LRNNX_ZOH, LRNNX_BILINEAR or LRNNX_DIRAC */
+  int32_t need_ddelta;     /* backward: 0 skips ddelta/ddeltaA (they are not written) */
+  lrnnx_view u, delta, A, B, C, deltaA;
+  lrnnx_view out;
+  void *x;                 /* (b, p, ceil(l/2048), 2 ds) complex, may be NULL */
+  void *ckpt;              /* per-chunk start states written by the forward (complex); may be NULL */
+  lrnnx_view dout;
+  lrnnx_view du, ddelta, dA, dB, dC, ddeltaA;
+  void *workspace;
+  int64_t workspace_bytes;
+} lrnnx_simplified_scan_args;
+
+/* Bytes of the forward's chunk-start states `ckpt` (complex64). */
+int64_t lrnnx_simplified_scan_ckpt_size(const lrnnx_simplified_scan_args *a);
+int64_t lrnnx_simplified_scan_workspace_size(const lrnnx_simplified_scan_args *a, int bwd);
+int lrnnx_simplified_scan_fwd(const lrnnx_simplified_scan_args *a, void *stream);
+int lrnnx_simplified_scan_bwd(const lrnnx_simplified_scan_args *a, void *stream);
+
+/*
+ * One-token decode update, in place on `state`.
+ * state (b, h, d, n) in f32/f16/bf16 (math in fp32); x, dt, z, deltaA, out
+ * (b, h, d); A (h, d, n) f32; B, C (b, g, n); D, dt_bias (h, d) f32.
+ * state_batch_indices (b) int32 or NULL.
+ * Replaces selective_state_update
+ *   (reference lrnnx/ops/triton/selective_state_update.py:300-476).
+ */
+typedef struct lrnnx_state_update_args {
+  int64_t batch, nheads, dim, dstate, ngroups;
+  int32_t state_type, x_type, bc_type;   /* enum lrnnx_dtype (not C64) */
+  int32_t method;
+  int32_t dt_softplus;
+  void *state; int64_t state_s0, state_s1, state_s2, state_s3;
+  const void *x; int64_t x_s0, x_s1, x_s2;
+  const void *dt; int64_t dt_s0, dt_s1, dt_s2;
+  const void *A; int64_t A_s0, A_s1, A_s2;
+  const void *B; int64_t B_s0, B_s1, B_s2;
+  const void *C; int64_t C_s0, C_s1, C_s2;
+  const void *D; int64_t D_s0, D_s1;
+  const void *z; int64_t z_s0, z_s1, z_s2;
+  const void *dt_bias; int64_t dtb_s0, dtb_s1;
+  const void *deltaA; int64_t dA_s0, dA_s1, dA_s2;
+  const int32_t *state_batch_indices;
+  void *out; int64_t out_s0, out_s1, out_s2;
+} lrnnx_state_update_args;
+
+int lrnnx_selective_state_update(const lrnnx_state_update_args *a, void *stream);
+
+/* Last error message of this thread ("" if none). */
+const char *lrnnx_last_error(void);
+
+/* ABI version of this header (bumped on any struct change). */
+int lrnnx_abi_version(void);
+
+#define LRNNX_ABI_VERSION 1
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LRNNX_SCAN_H */

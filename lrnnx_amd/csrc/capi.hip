@@ -1,0 +1,229 @@
+// extern "C" entry points of liblrnnx_scan.so: argument checks, workspace
+// sizing and dispatch to the gfx950 kernels.
+//
+// The checks mirror the reference host code (TORCH_CHECKs of
+// csrc/selective_scan/selective_scan_cpu.cpp:263-632 and
+// csrc/simplified_scan/simplified_scan_cpu.cpp:160-331); a failed check
+// returns 1 and leaves the message in lrnnx_last_error().
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "ss_common.h"
+
+namespace lrnnx {
+hipError_t ss_fwd_mamba_f32(const lrnnx_selective_scan_args&, hipStream_t);
+hipError_t ss_fwd_mamba_bf16(const lrnnx_selective_scan_args&, hipStream_t);
+hipError_t ss_fwd_mamba_f16(const lrnnx_selective_scan_args&, hipStream_t);
+hipError_t ss_fwd_other_f32(const lrnnx_selective_scan_args&, hipStream_t);
+hipError_t ss_bwd_mamba_f32(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
+hipError_t ss_bwd_mamba_bf16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
+hipError_t ss_bwd_mamba_f16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
+hipError_t ss_bwd_other_f32(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
+hipError_t ssc_fwd_launch(const lrnnx_selective_scan_args&, hipStream_t);
+hipError_t ssc_bwd_launch(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
+int64_t ssc_ckpt_bytes(const lrnnx_selective_scan_args&);
+int64_t ssc_bwd_ws_bytes(const lrnnx_selective_scan_args&);
+hipError_t simp_fwd_launch(const lrnnx_simplified_scan_args&, hipStream_t);
+hipError_t simp_bwd_launch(const lrnnx_simplified_scan_args&, hipStream_t);
+int64_t simp_ckpt_bytes(const lrnnx_simplified_scan_args&);
+int64_t simp_ws_bytes(const lrnnx_simplified_scan_args&, int);
+hipError_t state_update_launch(const lrnnx_state_update_args&, hipStream_t);
+
+// defined in ss_bwd_layout.hip (shares ss_bwd_ws with the backward units)
+int64_t ss_bwd_ws_bytes(const lrnnx_selective_scan_args&);
+int64_t ss_bwd_ckpt_offset_bytes(const lrnnx_selective_scan_args&);
+}  // namespace lrnnx
+
+using namespace lrnnx;
+
+namespace {
+thread_local std::string g_err;
+
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return 1;
+}
+
+int from_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return 0;
+  return fail("%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+const char* method_name(int m) {
+  switch (m) {
+    case LRNNX_ZOH: return "zoh";
+    case LRNNX_BILINEAR: return "bilinear";
+    case LRNNX_DIRAC: return "dirac";
+    case LRNNX_MAMBA: return "mamba";
+    case LRNNX_S7: return "s7";
+    case LRNNX_RGLRU: return "rglru";
+  }
+  return "?";
+}
+
+int check_ss(const lrnnx_selective_scan_args* a, bool bwd) {
+  if (!a) return fail("null argument struct");
+  if (a->itype != LRNNX_F32 && a->itype != LRNNX_F16 && a->itype != LRNNX_BF16)
+    return fail("input dtype must be float32, float16 or bfloat16");
+  if (a->wtype != LRNNX_F32 && a->wtype != LRNNX_C64) return fail("weight dtype must be float32 or complex64");
+  if (a->method < LRNNX_ZOH || a->method > LRNNX_RGLRU) return fail("Discretization method not supported");
+  if (a->method == LRNNX_S7 && a->wtype != LRNNX_F32)
+    return fail("S7 discretization only supports real (float) weights, not complex");
+  if (a->method == LRNNX_RGLRU && a->wtype != LRNNX_F32)
+    return fail("RGLRU discretization only supports real (float) weights, not complex");
+  if (a->method != LRNNX_MAMBA && a->itype != LRNNX_F32)
+    return fail("discretization '%s' supports float32 input only (as the reference kernels)", method_name(a->method));
+  if (a->wtype == LRNNX_C64 && a->itype != LRNNX_F32)
+    return fail("complex weights support float32 input only (as the reference kernels)");
+  if (a->batch <= 0 || a->dim <= 0 || a->seqlen <= 0 || a->dstate <= 0)
+    return fail("empty or negative shape (batch=%lld dim=%lld seqlen=%lld dstate=%lld)", (long long)a->batch,
+                (long long)a->dim, (long long)a->seqlen, (long long)a->dstate);
+  if (a->dstate > 256) return fail("selective_scan only supports state dimension <= 256");
+  if ((a->var_B || a->var_C) && (a->n_groups <= 0 || a->dim % a->n_groups != 0))
+    return fail("dim (%lld) must be a multiple of the number of B/C groups (%lld)", (long long)a->dim,
+                (long long)a->n_groups);
+  if (!a->u.ptr || !a->delta.ptr || !a->A.ptr || !a->B.ptr || !a->C.ptr) return fail("u, delta, A, B, C are required");
+  if (a->z.ptr && !bwd && !a->out_z.ptr) return fail("out_z is required when z is given");
+  if (!bwd && !a->z.ptr && !a->out.ptr && !a->ckpt && !a->x) return fail("nothing to compute: no outputs given");
+  if (bwd) {
+    if (!a->dout.ptr) return fail("dout is required");
+    if (a->z.ptr && !a->out_saved.ptr) return fail("out is required by the backward when z is given");
+    if (a->z.ptr && !a->dz.ptr) return fail("dz is required when z is given");
+    if (!a->du.ptr || !a->ddelta.ptr || !a->dA.ptr || !a->dB.ptr || !a->dC.ptr) return fail("du, ddelta, dA, dB, dC are required");
+    if (a->deltaA.ptr && !a->ddeltaA.ptr) return fail("ddeltaA is required when deltaA is given");
+  }
+  return 0;
+}
+}  // namespace
+
+extern "C" {
+
+const char* lrnnx_last_error(void) { return g_err.c_str(); }
+
+int lrnnx_abi_version(void) { return LRNNX_ABI_VERSION; }
+
+int64_t lrnnx_selective_scan_ckpt_size(const lrnnx_selective_scan_args* a) {
+  if (!a) return -1;
+  if (a->wtype == LRNNX_C64) return ssc_ckpt_bytes(*a);
+  const SSGeom g = ss_geom(*a);
+  return a->batch * g.n_ck * a->dstate * a->dim * (int64_t)sizeof(float);
+}
+
+int64_t lrnnx_selective_scan_workspace_size(const lrnnx_selective_scan_args* a, int bwd) {
+  if (!a) return -1;
+  if (!bwd) return 0;
+  if (a->wtype == LRNNX_C64) return ssc_bwd_ws_bytes(*a);
+  return ss_bwd_ws_bytes(*a);
+}
+
+int lrnnx_selective_scan_fwd(const lrnnx_selective_scan_args* a, void* stream) {
+  if (check_ss(a, false)) return 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->wtype == LRNNX_C64) return from_hip(ssc_fwd_launch(*a, st), "selective_scan_fwd (complex)");
+  hipError_t e;
+  if (a->method == LRNNX_MAMBA) {
+    switch (a->itype) {
+      case LRNNX_F32: e = ss_fwd_mamba_f32(*a, st); break;
+      case LRNNX_BF16: e = ss_fwd_mamba_bf16(*a, st); break;
+      default: e = ss_fwd_mamba_f16(*a, st); break;
+    }
+  } else {
+    e = ss_fwd_other_f32(*a, st);
+  }
+  return from_hip(e, "selective_scan_fwd");
+}
+
+int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args* a, void* stream) {
+  if (check_ss(a, true)) return 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t need = lrnnx_selective_scan_workspace_size(a, 1);
+  if (need > 0 && (!a->workspace || a->workspace_bytes < need))
+    return fail("workspace too small: %lld bytes given, %lld needed", (long long)a->workspace_bytes, (long long)need);
+  if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0) return fail("workspace must be 256-byte aligned");
+  float* ws = static_cast<float*>(a->workspace);
+  if (a->wtype == LRNNX_C64) return from_hip(ssc_bwd_launch(*a, ws, static_cast<const float*>(a->ckpt), st),
+                                             "selective_scan_bwd (complex)");
+  const float* ckp = static_cast<const float*>(a->ckpt);
+  if (!ckp) {
+    // rebuild the fine checkpoints with a forward pass that writes nothing else
+    lrnnx_selective_scan_args f = *a;
+    f.out.ptr = nullptr;
+    f.out_z.ptr = nullptr;
+    f.z.ptr = nullptr;
+    f.x = nullptr;
+    f.ckpt = reinterpret_cast<char*>(a->workspace) + ss_bwd_ckpt_offset_bytes(*a);
+    hipError_t e = a->method == LRNNX_MAMBA
+                       ? (a->itype == LRNNX_F32 ? ss_fwd_mamba_f32(f, st)
+                          : a->itype == LRNNX_BF16 ? ss_fwd_mamba_bf16(f, st) : ss_fwd_mamba_f16(f, st))
+                       : ss_fwd_other_f32(f, st);
+    if (from_hip(e, "selective_scan_bwd (checkpoint rebuild)")) return 1;
+    ckp = static_cast<const float*>(f.ckpt);
+  }
+  hipError_t e;
+  if (a->method == LRNNX_MAMBA) {
+    switch (a->itype) {
+      case LRNNX_F32: e = ss_bwd_mamba_f32(*a, ws, ckp, st); break;
+      case LRNNX_BF16: e = ss_bwd_mamba_bf16(*a, ws, ckp, st); break;
+      default: e = ss_bwd_mamba_f16(*a, ws, ckp, st); break;
+    }
+  } else {
+    e = ss_bwd_other_f32(*a, ws, ckp, st);
+  }
+  return from_hip(e, "selective_scan_bwd");
+}
+
+int64_t lrnnx_simplified_scan_ckpt_size(const lrnnx_simplified_scan_args* a) {
+  return a ? simp_ckpt_bytes(*a) : -1;
+}
+
+int64_t lrnnx_simplified_scan_workspace_size(const lrnnx_simplified_scan_args* a, int bwd) {
+  return a ? simp_ws_bytes(*a, bwd) : -1;
+}
+
+static int check_simp(const lrnnx_simplified_scan_args* a, bool bwd) {
+  if (!a) return fail("null argument struct");
+  if (a->method != LRNNX_ZOH && a->method != LRNNX_BILINEAR && a->method != LRNNX_DIRAC)
+    return fail("Discretization method not supported (simplified scan: zoh, bilinear, dirac)");
+  if (a->batch <= 0 || a->dim <= 0 || a->seqlen <= 0 || a->dstate <= 0) return fail("empty or negative shape");
+  if (a->dstate > 256) return fail("simplified_scan only supports state dimension <= 256");
+  if (!a->u.ptr || !a->delta.ptr || !a->A.ptr || !a->B.ptr || !a->C.ptr) return fail("u, delta, A, B, C are required");
+  if (!a->workspace && simp_ws_bytes(*a, bwd) > 0) return fail("workspace is required");
+  if (a->workspace_bytes < simp_ws_bytes(*a, bwd))
+    return fail("workspace too small: %lld bytes given, %lld needed", (long long)a->workspace_bytes,
+                (long long)simp_ws_bytes(*a, bwd));
+  if (bwd) {
+    if (!a->dout.ptr || !a->du.ptr || !a->dA.ptr || !a->dB.ptr || !a->dC.ptr) return fail("dout, du, dA, dB, dC are required");
+    if (a->need_ddelta && !a->ddelta.ptr) return fail("ddelta is required");
+    if (a->need_ddelta && a->deltaA.ptr && !a->ddeltaA.ptr) return fail("ddeltaA is required when deltaA is given");
+  }
+  return 0;
+}
+
+int lrnnx_simplified_scan_fwd(const lrnnx_simplified_scan_args* a, void* stream) {
+  if (check_simp(a, false)) return 1;
+  return from_hip(simp_fwd_launch(*a, static_cast<hipStream_t>(stream)), "simplified_scan_fwd");
+}
+
+int lrnnx_simplified_scan_bwd(const lrnnx_simplified_scan_args* a, void* stream) {
+  if (check_simp(a, true)) return 1;
+  return from_hip(simp_bwd_launch(*a, static_cast<hipStream_t>(stream)), "simplified_scan_bwd");
+}
+
+int lrnnx_selective_state_update(const lrnnx_state_update_args* a, void* stream) {
+  if (!a) return fail("null argument struct");
+  if (a->method < LRNNX_ZOH || a->method > LRNNX_RGLRU) return fail("Discretization method not supported");
+  if (a->batch <= 0 || a->nheads <= 0 || a->dim <= 0 || a->dstate <= 0) return fail("empty or negative shape");
+  if (a->ngroups <= 0 || a->nheads % a->ngroups != 0) return fail("nheads must be divisible by ngroups");
+  if (!a->state || !a->x || !a->dt || !a->A || !a->B || !a->C || !a->out) return fail("state, x, dt, A, B, C, out are required");
+  for (int t : {a->state_type, a->x_type, a->bc_type})
+    if (t != LRNNX_F32 && t != LRNNX_F16 && t != LRNNX_BF16) return fail("unsupported dtype code %d", t);
+  return from_hip(state_update_launch(*a, static_cast<hipStream_t>(stream)), "selective_state_update");
+}
+
+}  // extern "C"

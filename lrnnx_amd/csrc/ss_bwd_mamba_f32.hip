@@ -1,0 +1,8 @@
+// Selective scan backward, method "mamba", f32 I/O (instantiation unit).
+#include "ss_bwd_impl.h"
+namespace lrnnx {
+hipError_t ss_bwd_mamba_f32(const lrnnx_selective_scan_args& a, float* ws, const float* ckp, hipStream_t st) {
+  const SSGeom g = ss_geom(a);
+  return launch_bwd_s<float, LRNNX_MAMBA>(a, g, ws, ss_bwd_ws(a, g, a.ckpt == nullptr), ckp, st);
+}
+}  // namespace lrnnx

@@ -1,0 +1,120 @@
+// Shared pieces of the selective-scan forward and backward kernels.
+//
+// Work decomposition (both directions):
+//   * one workgroup = one batch row b and a block of CB <= 64 channels that
+//     lie in a single B/C group (so B/C are wave-uniform);
+//   * lane l of every wave owns channel d0 + l;
+//   * wave w owns states [w*kS, w*kS + kS) and keeps their fp32 h in VGPRs;
+//   * L is walked sequentially in tiles of kT steps staged through LDS
+//     (coalesced 16-byte loads of u, delta, deltaA, z; B/C rows of the group).
+// The sum over states (y, du, ddelta) crosses waves through LDS; the sum over
+// channels (dB, dC) is a wave reduce-scatter followed by a deterministic
+// second-stage reduction over channel blocks.
+#pragma once
+
+#include "common.h"
+
+namespace lrnnx {
+
+// States per wave by d_state; the backward stores kS * kCk values of A_bar
+// and h per lane, so kS * kCk <= 64 keeps that at <= 128 VGPRs and fits the
+// per-lane dB/dC block into one 64-value reduce-scatter.
+__host__ __device__ constexpr int ck_for(int kS) { return kS == 1 ? 16 : 64 / kS; }
+// backward tile length along L (a whole number of checkpoint intervals) and
+// forward tile length, sized so that every instantiation fits 160 KB of LDS
+__host__ __device__ constexpr int tb_for(int kS) { return kS >= 8 ? 8 : 16; }
+__host__ __device__ constexpr int tf_for(int kS) { return kS >= 32 ? 16 : 32; }
+constexpr size_t kMaxLds = 160 * 1024;
+
+inline int pick_kS(int64_t N) {
+  if (N <= 4) return 1;
+  if (N <= 16) return 4;
+  if (N <= 64) return 8;
+  return 32;
+}
+
+// Per-(t, n) discretisation of a real state.  `dtA` is the step used for
+// A_bar (deltaA or delta'), `dl` the post-bias/softplus delta', `a2` the
+// per-(d, n) prepared eigenvalue:
+//   exp-based methods: A * log2(e);  bilinear, zoh: A;  rglru: log2(A);  s7: unused.
+// Returns A_bar; writes the input factor beta so that the increment is
+// beta * B_in * u (selective_scan.cuh:272-302).
+template <int kMethod>
+__device__ __forceinline__ float disc_real(float dtA, float dl, float a2, float Araw, float& beta) {
+  if constexpr (kMethod == LRNNX_MAMBA) {
+    beta = dl;
+    return fast_exp2(dtA * a2);
+  } else if constexpr (kMethod == LRNNX_DIRAC) {
+    beta = 1.f;
+    return fast_exp2(dtA * a2);
+  } else if constexpr (kMethod == LRNNX_ZOH) {
+    beta = expm1f(dl * Araw) / Araw;
+    return expf(dtA * Araw);
+  } else if constexpr (kMethod == LRNNX_BILINEAR) {
+    const float vA = 0.5f * dtA * Araw;
+    const float vB = 0.5f * dl * Araw;
+    beta = dl / (1.f - vB);
+    return (1.f + vA) / (1.f - vA);
+  } else if constexpr (kMethod == LRNNX_S7) {
+    beta = 1.f;
+    return 1.f - 1.f / (dl * dl + 0.5f);
+  } else {  // RGLRU: A_bar = A^delta, beta = sqrt(1 - A_bar^2)
+    const float ab = fast_exp2(dl * a2);
+    beta = sqrtf(-expm1f(dl * a2 * kLn2) * (1.f + ab));  // 1 - ab^2 without cancellation
+    return ab;
+  }
+}
+
+template <int kMethod>
+__device__ __forceinline__ float prep_a2(float A) {
+  if constexpr (kMethod == LRNNX_MAMBA || kMethod == LRNNX_DIRAC) return A * kLog2e;
+  else if constexpr (kMethod == LRNNX_RGLRU) return __log2f(A);
+  else return A;
+}
+
+// Whether A_bar of this method is exp(dtA * A) (then the running product of
+// A_bar over a chunk is exp(A * sum dtA) and needs no per-step multiply).
+template <int kMethod>
+__host__ __device__ constexpr bool exp_family() {
+  return kMethod == LRNNX_MAMBA || kMethod == LRNNX_DIRAC || kMethod == LRNNX_ZOH;
+}
+
+// Whether B (variable or constant) multiplies the input term
+// (rglru ignores B on the input side, selective_scan.cuh:296-302).
+template <int kMethod>
+__host__ __device__ constexpr bool uses_B_input() { return kMethod != LRNNX_RGLRU; }
+
+// Whether deltaA (when given) drives A_bar (s7 and rglru ignore it).
+template <int kMethod>
+__host__ __device__ constexpr bool uses_deltaA() {
+  return kMethod != LRNNX_S7 && kMethod != LRNNX_RGLRU;
+}
+
+// Launch geometry shared by forward and backward.
+struct SSGeom {
+  int CB;        // channels per workgroup (<= 64, divides D/G when G > 1)
+  int n_cb;      // channel blocks
+  int kS, nW;    // states per wave, waves per workgroup
+  int ck;        // checkpoint interval (steps)
+  int64_t n_ck;  // checkpoints per (b, d)
+};
+
+inline SSGeom ss_geom(const lrnnx_selective_scan_args& a) {
+  SSGeom g;
+  const int64_t ratio = a.var_B || a.var_C ? a.dim / a.n_groups : a.dim;
+  if (a.n_groups <= 1 || !(a.var_B || a.var_C)) {
+    g.CB = 64;
+  } else {
+    int cb = 64;
+    while (cb > 1 && ratio % cb != 0) --cb;
+    g.CB = cb;
+  }
+  g.n_cb = (int)((a.dim + g.CB - 1) / g.CB);
+  g.kS = pick_kS(a.dstate);
+  g.nW = (int)((a.dstate + g.kS - 1) / g.kS);
+  g.ck = ck_for(g.kS);
+  g.n_ck = (a.seqlen + g.ck - 1) / g.ck;
+  return g;
+}
+
+}  // namespace lrnnx

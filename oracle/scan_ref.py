@@ -1,0 +1,466 @@
+"""PyTorch (CPU) restatement of the reference scans.  TEST INFRASTRUCTURE ONLY.
+
+Each function follows a reference function line by line in *semantics* (same
+discretisation formulas, same order of broadcast/grouping, same output
+casting) and adds a ``compute_dtype`` argument: ``None`` reproduces the
+reference's float32 arithmetic, ``torch.float64`` runs the same algorithm in
+double precision (complex128 for complex weights) for pinning and parity.
+
+Reference anchors (paths relative to the reference checkout):
+  selective_scan_ref ........ lrnnx/ops/selective_scan.py:200-360
+  softplus threshold ........ csrc/selective_scan/selective_scan.cuh:172-174 (F.softplus, threshold 20)
+  s7 / rglru discretisation . csrc/selective_scan/selective_scan.cuh:287-302
+  x chunk carries ........... csrc/selective_scan/selective_scan_cpu.cpp:380-386, selective_scan.cuh:326-334
+  simplified_scan_ref ....... lrnnx/ops/simplified_scan.py:233-340
+  simplified kernel (B*C out) csrc/simplified_scan/simplified_scan.cuh:172-246
+  s5_inner_ref .............. lrnnx/ops/simplified_scan.py:586-640
+  selective_state_update_ref  lrnnx/ops/triton/selective_state_update.py:479-599
+  s7_scan_ref ............... lrnnx/ops/s7_scan.py:179-233
+  rglru_scan_ref ............ lrnnx/ops/rglru_scan.py:148-203
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+CHUNK = 2048  # reference L-chunk for the x carries (selective_scan_cpu.cpp:380)
+
+METHODS = ("zoh", "bilinear", "dirac", "mamba", "s7", "rglru")
+
+
+def _real(dt):
+    return torch.float32 if dt is None else dt
+
+
+def _cplx(dt):
+    return torch.complex64 if (dt is None or dt == torch.float32) else torch.complex128
+
+
+def _group_expand(X, dim):
+    """(b, g, n, l) -> (b, dim, n, l): channel d uses group d // (dim // g)
+    (reference ``repeat(B, "B G N L -> B (G H) N L")``, selective_scan.py:265-267)."""
+    g = X.shape[1]
+    return X.repeat_interleave(dim // g, dim=1)
+
+
+def _as_complex_seq(X, cdt):
+    """Variable complex B/C arrive as real (..., 2L) interleaved (re, im) pairs
+    (selective_scan.py:233-241; selective_scan_cpu.cpp:335)."""
+    Xr = X.to(_real(None) if cdt == torch.complex64 else torch.float64)
+    return torch.view_as_complex(Xr.reshape(*Xr.shape[:-1], Xr.shape[-1] // 2, 2).contiguous())
+
+
+def discretize(method, delta, deltaA, A, u, Bseq=None):
+    """Per-element (A_bar, B_bar * u) for one discretisation.
+
+    delta, deltaA, u: (b, d, l, 1) in the compute dtype; A: (1, d, 1, n).
+    ``Bseq`` is the input-side B factor broadcast to (b, d, l, n) or None (=1).
+    Returns (A_bar, Bu) of shape (b, d, l, n).
+
+    Formulas: selective_scan.py:249-323 (mamba, zoh, bilinear, dirac) and
+    selective_scan.cuh:287-302 (s7: A_bar = 1 - 1/(delta^2 + 1/2), B_bar = 1;
+    rglru: A_bar = A**delta, B_bar = sqrt(1 - A_bar^2) and B is not used on
+    the input side).
+    """
+    dA_ = deltaA if deltaA is not None else delta
+    one = torch.ones((), dtype=A.dtype)
+    if method == "mamba":
+        Abar = torch.exp(dA_ * A)
+        Bbar = delta.expand_as(Abar)
+    elif method == "zoh":
+        Abar = torch.exp(dA_ * A)
+        Bbar = torch.expm1(delta * A) / A
+    elif method == "bilinear":
+        vA = 0.5 * dA_ * A
+        Abar = (one + vA) / (one - vA)
+        Bbar = delta / (one - 0.5 * delta * A)
+    elif method == "dirac":
+        Abar = torch.exp(dA_ * A)
+        Bbar = torch.ones_like(Abar)
+    elif method == "s7":
+        Abar = (1.0 - 1.0 / (delta * delta + 0.5)).expand(-1, -1, -1, A.shape[-1])
+        Bbar = torch.ones_like(Abar)
+    elif method == "rglru":
+        Abar = torch.exp(delta * torch.log(A))
+        Bbar = torch.sqrt(1.0 - Abar * Abar)
+        Bseq = None
+    else:
+        raise ValueError(f"Unknown discretization method: {method}")
+    Bu = Bbar * u
+    if Bseq is not None:
+        Bu = Bu * Bseq
+    return Abar, Bu
+
+
+def _prep_delta(delta, delta_bias, delta_softplus, rdt):
+    d = delta.to(rdt)
+    if delta_bias is not None:
+        d = d + delta_bias[..., None].to(rdt)
+    if delta_softplus:
+        d = F.softplus(d)  # threshold=20 => identity above 20, as selective_scan.cuh:173
+    return d
+
+
+def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, deltaA=None,
+                       delta_softplus=False, return_last_state=False, discretization="mamba",
+                       compute_dtype=None):
+    """Restatement of ``selective_scan_ref`` (selective_scan.py:200-360).
+
+    u, delta, z, deltaA: (b, d, l).  A: (d, n) real or complex.
+    B, C: (d, n) constant, (b, n, l) or (b, g, n, l) variable (complex variable
+    B/C are real (..., 2l) interleaved).  D, delta_bias: (d,).
+    Also implements the kernel-only methods "s7" and "rglru".
+    Returns out (input dtype) or (out, last_state (b, d, n)).
+    """
+    dtype_in = u.dtype
+    rdt = _real(compute_dtype)
+    is_complex = A.is_complex()
+    cdt = _cplx(compute_dtype)
+    wdt = cdt if is_complex else rdt
+    uu = u.to(rdt)
+    dl = _prep_delta(delta, delta_bias, delta_softplus, rdt)
+    dA_ = deltaA.to(rdt) if deltaA is not None else None
+    batch, dim, L = u.shape
+    n = A.shape[1]
+    Aw = A.to(wdt)
+    varB, varC = B.dim() >= 3, C.dim() >= 3
+
+    def seq(X):  # -> (b, d, l, n)
+        if is_complex:
+            X = _as_complex_seq(X, cdt)
+        else:
+            X = X.to(rdt)
+        if X.dim() == 3:
+            X = X.unsqueeze(1)
+        return _group_expand(X, dim).permute(0, 1, 3, 2)
+
+    Bseq = seq(B) if varB else Aw.new_ones(()) * B.to(wdt)[None, :, None, :]
+    Cseq = seq(C) if varC else C.to(wdt)[None, :, None, :]
+    if discretization == "rglru" and not varB:
+        # rglru never uses B on the input side; a constant B is folded into the
+        # output weight as the kernel does (selective_scan.cuh:208-214, :296-302)
+        Cseq = Cseq * B.to(wdt)[None, :, None, :]
+    Abar, Bu = discretize(discretization, dl[..., None], dA_[..., None] if dA_ is not None else None,
+                          Aw[None, :, None, :], uu[..., None], Bseq)
+    h = torch.zeros((batch, dim, n), dtype=wdt)
+    ys = []
+    for t in range(L):
+        h = Abar[:, :, t] * h + Bu[:, :, t]
+        y = (h * Cseq[:, :, min(t, Cseq.shape[2] - 1)]).sum(-1)
+        if is_complex:
+            y = 2 * y.real
+        ys.append(y)
+    y = torch.stack(ys, dim=2)
+    out = y if D is None else y + uu * D.to(rdt)[:, None]
+    if z is not None:
+        zz = z if compute_dtype is None else z.to(rdt)
+        out = out * F.silu(zz)
+    out = out.to(dtype_in)
+    return (out, h) if return_last_state else out
+
+
+def selective_scan_fwd_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, deltaA=None,
+                           delta_softplus=False, discretization="mamba", compute_dtype=None):
+    """Kernel-boundary semantics of ``selective_scan_cuda.fwd``
+    (selective_scan.h:114-121; selective_scan_cpu.cpp:263-421).
+
+    Returns ``[out, x]`` (+ ``out_z`` if z).  ``out`` = y + D*u before gating,
+    in the input dtype.  ``x`` is (b, d, n_chunks, 2n) in the weight dtype with
+    x[..., 2k] = prod_{s<=t_end} A_bar_s and x[..., 2k+1] = h_{t_end} at the end
+    of each 2048-step chunk.  With a *constant* B the kernel folds B into the
+    output weight, so the stored h excludes B (the wrapper multiplies it back,
+    selective_scan.py:88-92).  With "rglru" B never enters the input term.
+    """
+    rdt = _real(compute_dtype)
+    is_complex = A.is_complex()
+    cdt = _cplx(compute_dtype)
+    wdt = cdt if is_complex else rdt
+    batch, dim, L = u.shape
+    n = A.shape[1]
+    uu = u.to(rdt)
+    dl = _prep_delta(delta, delta_bias, delta_softplus, rdt)
+    dA_ = deltaA.to(rdt) if deltaA is not None else None
+    Aw = A.to(wdt)
+    varB, varC = B.dim() >= 3, C.dim() >= 3
+
+    def seq(X):
+        X = _as_complex_seq(X, cdt) if is_complex else X.to(rdt)
+        if X.dim() == 3:
+            X = X.unsqueeze(1)
+        return _group_expand(X, dim).permute(0, 1, 3, 2)
+
+    Bin = seq(B) if varB else None
+    Cout = seq(C) if varC else C.to(wdt)[None, :, None, :]
+    if not varB:
+        Cout = Cout * B.to(wdt)[None, :, None, :]
+    Abar, Bu = discretize(discretization, dl[..., None], dA_[..., None] if dA_ is not None else None,
+                          Aw[None, :, None, :], uu[..., None], Bin)
+    n_chunks = (L + CHUNK - 1) // CHUNK
+    x = torch.zeros((batch, dim, n_chunks, 2 * n), dtype=wdt)
+    h = torch.zeros((batch, dim, n), dtype=wdt)
+    a = torch.ones((batch, dim, n), dtype=wdt)
+    ys = []
+    for t in range(L):
+        h = Abar[:, :, t] * h + Bu[:, :, t]
+        a = a * Abar[:, :, t]
+        y = (h * Cout[:, :, min(t, Cout.shape[2] - 1)]).sum(-1)
+        ys.append(2 * y.real if is_complex else y)
+        if t == L - 1 or (t + 1) % CHUNK == 0:
+            c = t // CHUNK
+            x[:, :, c, 0::2] = a
+            x[:, :, c, 1::2] = h
+    y = torch.stack(ys, dim=2)
+    out = y if D is None else y + uu * D.to(rdt)[:, None]
+    res = [out.to(u.dtype), x]
+    if z is not None:
+        res.append((out * F.silu(z.to(rdt))).to(u.dtype))
+    return res
+
+
+# ----------------------------------------------------------------------------
+# Simplified (S5) scan
+# ----------------------------------------------------------------------------
+
+def simplified_scan_kernel_ref(u, delta, A, B, C, deltaA=None, discretization="bilinear",
+                               compute_dtype=None):
+    """Kernel-boundary semantics of ``simplified_scan_cuda.fwd``
+    (simplified_scan.h:98-109; simplified_scan.cuh:85-262).
+
+    u (b, p, l) complex, delta/deltaA (b, p, l) real, A/B/C (p, ds) complex.
+    h_{t,s} = A_bar h + B_bar(delta, A) * u_t (B does not enter the input term,
+    simplified_scan.cuh:204-223); out_t = sum_s (B_s C_s) h_{t,s}.
+    Returns [out (b,p,l) complex, x (b,p,n_chunks,2ds) complex].
+    """
+    rdt = _real(compute_dtype)
+    cdt = _cplx(compute_dtype)
+    batch, P, L = u.shape
+    ds = A.shape[1]
+    uu = u.to(cdt)[..., None]
+    dl = delta.to(rdt)[..., None]
+    dA_ = deltaA.to(rdt)[..., None] if deltaA is not None else None
+    Aw = A.to(cdt)[None, :, None, :]
+    if discretization not in ("zoh", "bilinear", "dirac"):
+        raise ValueError(f"Unknown discretization method: {discretization}")
+    Abar, Bu = discretize(discretization, dl, dA_, Aw, uu, None)
+    BC = (B.to(cdt) * C.to(cdt))[None, :, :]
+    n_chunks = (L + CHUNK - 1) // CHUNK
+    x = torch.zeros((batch, P, n_chunks, 2 * ds), dtype=cdt)
+    h = torch.zeros((batch, P, ds), dtype=cdt)
+    a = torch.ones((batch, P, ds), dtype=cdt)
+    outs = []
+    for t in range(L):
+        h = Abar[:, :, t] * h + Bu[:, :, t]
+        a = a * Abar[:, :, t]
+        outs.append((h * BC).sum(-1))
+        if t == L - 1 or (t + 1) % CHUNK == 0:
+            c = t // CHUNK
+            x[:, :, c, 0::2] = a
+            x[:, :, c, 1::2] = h
+    return [torch.stack(outs, dim=2), x]
+
+
+def simplified_scan_ref(u, delta, A, B, C, deltaA=None, return_last_state=False,
+                        discretization="bilinear", compute_dtype=None):
+    """Restatement of ``simplified_scan_ref`` (simplified_scan.py:233-340).
+
+    u (b, h, l) complex; delta (b, p, l) real; A (p,) or (p, 1) complex;
+    B (p, h) complex; C (h, p) complex.  y = C @ scan(B @ u).
+    """
+    assert u.is_complex() and A.is_complex() and not delta.is_complex()
+    rdt = _real(compute_dtype)
+    cdt = _cplx(compute_dtype)
+    dtype_in = u.dtype
+    if A.dim() == 2:
+        A = A.squeeze(-1)
+    Bu = torch.einsum("ph,bhl->bpl", B.to(cdt), u.to(cdt))
+    dl = delta.to(rdt)[..., None]
+    dA_ = deltaA.to(rdt)[..., None] if deltaA is not None else None
+    if discretization not in ("zoh", "bilinear", "dirac"):
+        raise ValueError(f"Unknown discretization method: {discretization}")
+    Abar, dBu = discretize(discretization, dl, dA_, A.to(cdt)[None, :, None, None], Bu[..., None], None)
+    batch, P, L = Bu.shape
+    x = torch.zeros((batch, P, 1), dtype=cdt)
+    xs = []
+    for i in range(L):
+        x = Abar[:, :, i] * x + dBu[:, :, i]
+        xs.append(x.squeeze(-1))
+    last_state = x.squeeze(-1)
+    y = torch.einsum("hp,bpl->bhl", C.to(cdt), torch.stack(xs, dim=2))
+    out = y.to(dtype_in) if compute_dtype is None else y
+    return (out, last_state) if return_last_state else out
+
+
+def s5_inner_ref(u, delta, A, B, C, D, deltaA=None, discretization="bilinear", conj_sym=True,
+                 compute_dtype=None):
+    """Restatement of ``s5_inner_ref`` (simplified_scan.py:586-640)."""
+    y = simplified_scan_ref(u, delta, A, B, C, deltaA=deltaA, discretization=discretization,
+                            compute_dtype=compute_dtype)
+    y_real = 2 * y.real if conj_sym else y.real
+    u_real = u.real if u.is_complex() else u
+    rdt = _real(compute_dtype)
+    return y_real + D.to(rdt)[None, :, None] * u_real.to(rdt)
+
+
+# ----------------------------------------------------------------------------
+# One-step decode update
+# ----------------------------------------------------------------------------
+
+def selective_state_update_ref(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
+                               dt_softplus=False, deltaA=None, discretization="mamba",
+                               compute_dtype=None):
+    """Restatement of ``selective_state_update_ref``
+    (selective_state_update.py:479-599).  Updates ``state`` in place (stored in
+    its own dtype) and returns out (x dtype).
+
+    Note the reference's A discretisation: exp(dt*A) for every method except
+    rglru (A**dt) and s7 (1 - 1/(dt^2+1/2)); deltaA (if given) replaces dt in
+    the exp.  zoh/bilinear change only the B factor.
+    """
+    rdt = _real(compute_dtype)
+    has_heads = state.dim() > 3
+    st = state if state.dim() == 4 else state.unsqueeze(1)
+    x_ = x if x.dim() == 3 else x.unsqueeze(1)
+    dt_ = dt if dt.dim() == 3 else dt.unsqueeze(1)
+    A_ = A if A.dim() == 3 else A.unsqueeze(0)
+    B_ = B if B.dim() == 3 else B.unsqueeze(1)
+    C_ = C if C.dim() == 3 else C.unsqueeze(1)
+    D_ = None if D is None else (D if D.dim() == 2 else D.unsqueeze(0))
+    z_ = None if z is None else (z if z.dim() == 3 else z.unsqueeze(1))
+    db_ = None if dt_bias is None else (dt_bias if dt_bias.dim() == 2 else dt_bias.unsqueeze(0))
+    dA_in = None if deltaA is None else (deltaA if deltaA.dim() == 3 else deltaA.unsqueeze(1))
+    batch, nheads, dim, dstate = st.shape
+    ngroups = B_.shape[1]
+    dtv = dt_.to(rdt)
+    if db_ is not None:
+        dtv = dtv + db_.to(rdt)
+    if dt_softplus:
+        dtv = F.softplus(dtv)
+    Af = A_.to(rdt)
+    disc = discretization.lower()
+    if disc == "rglru":
+        gate = (dA_in.to(rdt) if dA_in is not None else dtv)[..., None]
+        dA = Af ** gate
+    elif disc == "s7":
+        e = dtv[..., None]
+        dA = (1.0 - 1.0 / (e * e + 0.5)).expand(-1, -1, -1, dstate)
+    elif dA_in is not None:
+        dA = torch.exp(dA_in.to(rdt)[..., None] * Af)
+    else:
+        dA = torch.exp(dtv[..., None] * Af)
+    Bf = B_.to(rdt).repeat_interleave(nheads // ngroups, dim=1)
+    Cf = C_.to(rdt).repeat_interleave(nheads // ngroups, dim=1)
+    dte = dtv[..., None]
+    Be = Bf[:, :, None, :]
+    if disc == "zoh":
+        dB = Be * (torch.exp(dte * Af) - 1.0) / Af
+    elif disc == "bilinear":
+        dB = Be * (1.0 / (1.0 - 0.5 * dte * Af)) * dte
+    elif disc in ("dirac", "s7"):
+        dB = Be.expand_as(dA)
+    elif disc == "rglru":
+        dB = Be * torch.sqrt(1.0 - dA * dA)
+    else:
+        dB = dte * Be
+    new = st.to(rdt) * dA + dB * x_.to(rdt)[..., None]
+    st.copy_(new.to(st.dtype))
+    stv = st.to(rdt) if compute_dtype is None else new
+    out = torch.einsum("bhdn,bhn->bhd", stv, Cf)
+    if D_ is not None:
+        out = out + x_.to(rdt) * D_.to(rdt)
+    if z_ is not None:
+        out = out * F.silu(z_.to(rdt))
+    out = out.to(x.dtype) if compute_dtype is None else out
+    return out if has_heads else out.squeeze(1)
+
+
+# ----------------------------------------------------------------------------
+# S7 / RG-LRU wrappers (they call selective_scan_cuda with "s7"/"rglru")
+# ----------------------------------------------------------------------------
+
+def s7_scan_ref(u, A, B, C, bias=None, return_last_state=False, compute_dtype=None):
+    """Restatement of ``s7_scan_ref`` (s7_scan.py:179-233)."""
+    rdt = _real(compute_dtype)
+    uu, Af, Bf, Cf = u.to(rdt), A.to(rdt), B.to(rdt), C.to(rdt)
+    Abar = 1.0 - 1.0 / (Af * Af + 0.5)
+    Bu = torch.einsum("bnhl,bhl->bnl", Bf, uu)
+    if bias is not None:
+        Bu = Bu + bias.to(rdt)
+    x = torch.zeros(u.shape[0], A.shape[1], dtype=rdt)
+    xs = []
+    for t in range(u.shape[2]):
+        x = Abar[:, :, t] * x + Bu[:, :, t]
+        xs.append(x)
+    y = torch.einsum("bhnl,bnl->bhl", Cf, torch.stack(xs, dim=-1))
+    out = y.to(u.dtype) if compute_dtype is None else y
+    return (out, x) if return_last_state else out
+
+
+def rglru_scan_ref(u, delta, A, return_last_state=False, compute_dtype=None):
+    """Restatement of ``rglru_scan_ref`` (rglru_scan.py:148-203)."""
+    rdt = _real(compute_dtype)
+    uu, dl, Af = u.to(rdt), delta.to(rdt), A.to(rdt)
+    Abar = torch.exp(dl.unsqueeze(2) * torch.log(Af).unsqueeze(0).unsqueeze(-1))
+    Bu = torch.sqrt(1.0 - Abar * Abar) * uu.unsqueeze(2)
+    h = torch.zeros(u.shape[0], u.shape[1], A.shape[1], dtype=rdt)
+    hs = []
+    for t in range(u.shape[2]):
+        h = Abar[..., t] * h + Bu[..., t]
+        hs.append(h)
+    y = torch.stack(hs, dim=-1).sum(dim=2)
+    out = y.to(u.dtype) if compute_dtype is None else y
+    return (out, h) if return_last_state else out
+
+
+# ----------------------------------------------------------------------------
+# Synthetic inputs of the BASELINE configurations
+# ----------------------------------------------------------------------------
+
+def make_selective_inputs(batch, dim, L, N, *, seed, itype=torch.float32, groups=None,
+                          varB=True, varC=True, has_z=True, has_D=True, has_bias=True,
+                          complex_A=False, device="cpu"):
+    """Inputs of the BASELINE selective-scan configs: u, z ~ N(0,1); delta ~
+    0.5 N(0,1); delta_bias = log(expm1(dt)), dt log-uniform in [1e-3, 1e-1];
+    A = -(1..N) (S4D-real); B, C ~ N(0,1); D = ones.  Generation order is
+    fixed here: u, delta, z, dt, B, C (all on the CPU generator)."""
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(batch, dim, L, generator=g)
+    delta = 0.5 * torch.randn(batch, dim, L, generator=g)
+    z = torch.randn(batch, dim, L, generator=g) if has_z else None
+    dt = torch.exp(torch.rand(dim, generator=g) * (math.log(1e-1) - math.log(1e-3)) + math.log(1e-3))
+    delta_bias = torch.log(torch.expm1(dt)) if has_bias else None
+    A = -torch.arange(1, N + 1, dtype=torch.float32).repeat(dim, 1)
+    if complex_A:
+        A = torch.complex(A, torch.randn(dim, N, generator=g))
+    shp = (batch, N, L) if groups is None else (batch, groups, N, L)
+    if complex_A:
+        shp = shp[:-1] + (2 * L,)
+    B = torch.randn(*shp, generator=g) if varB else (
+        torch.randn(dim, N, generator=g) if not complex_A else torch.randn(dim, N, dtype=torch.complex64, generator=g))
+    C = torch.randn(*shp, generator=g) if varC else (
+        torch.randn(dim, N, generator=g) if not complex_A else torch.randn(dim, N, dtype=torch.complex64, generator=g))
+    D = torch.ones(dim) if has_D else None
+    cast = lambda t: None if t is None else t.to(itype)
+    u, delta, z = cast(u), cast(delta), cast(z)
+    if varB:
+        B = B.to(itype)
+    if varC:
+        C = C.to(itype)
+    out = dict(u=u, delta=delta, A=A, B=B, C=C, D=D, z=z, delta_bias=delta_bias)
+    return {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in out.items()}
+
+
+def make_lru_inputs(batch, L, P, *, seed, device="cpu"):
+    """Config-1 inputs: Lambda = r e^{i theta}, r ~ U[0.9, 0.999], theta ~
+    U[0, pi/10]; Bu = (N(0,1) + i N(0,1))/sqrt(2) laid out (b, P, L) (the
+    kernel's layout; the config's (b, L, P) is the same values transposed)."""
+    g = torch.Generator().manual_seed(seed)
+    r = 0.9 + 0.099 * torch.rand(P, generator=g)
+    theta = (math.pi / 10) * torch.rand(P, generator=g)
+    lam = torch.polar(r, theta)
+    re = torch.randn(batch, P, L, generator=g)
+    im = torch.randn(batch, P, L, generator=g)
+    Bu = torch.complex(re, im) / math.sqrt(2.0)
+    return {"Lambda": lam.to(device), "Bu": Bu.to(device)}

@@ -1,0 +1,126 @@
+"""CPU tests of the drop-in boundary: the C ABI library loads, exports every
+symbol include/lrnnx_scan.h declares, its structs have the layout the
+Python binding assumes, argument checks fail with the reference's messages
+(host code only, no GPU call), and the Python API refuses CPU tensors
+(there is no CPU fallback)."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+import torch
+
+from lrnnx_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lrnnx_scan.h")
+
+
+def _declared_functions():
+    src = open(HEADER).read()
+    decl = re.compile(r"^\s*(?:const\s+)?(?:int|int64_t|char|void)\s*\*?\s*(lrnnx_[a-z0-9_]+)\s*\(", re.M)
+    return sorted(set(decl.findall(src)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = _declared_functions()
+    assert len(names) >= 11
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in lrnnx_scan.h but not exported"
+    assert set(_lib.EXPORTS) <= set(names)
+    assert L.lrnnx_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layout_matches_c():
+    prog = r'''
+#include <stdio.h>
+#include <stddef.h>
+#include "lrnnx_scan.h"
+int main(void) {
+  printf("%zu %zu %zu %zu\n", sizeof(lrnnx_view), sizeof(lrnnx_selective_scan_args),
+         sizeof(lrnnx_simplified_scan_args), sizeof(lrnnx_state_update_args));
+  printf("%zu %zu %zu %zu %zu\n", offsetof(lrnnx_selective_scan_args, u), offsetof(lrnnx_selective_scan_args, x),
+         offsetof(lrnnx_selective_scan_args, dout), offsetof(lrnnx_selective_scan_args, workspace),
+         offsetof(lrnnx_selective_scan_args, dz));
+  printf("%zu %zu %zu\n", offsetof(lrnnx_simplified_scan_args, x), offsetof(lrnnx_simplified_scan_args, dout),
+         offsetof(lrnnx_simplified_scan_args, workspace_bytes));
+  printf("%zu %zu %zu\n", offsetof(lrnnx_state_update_args, state), offsetof(lrnnx_state_update_args, deltaA),
+         offsetof(lrnnx_state_update_args, out_s2));
+  return 0;
+}
+'''
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "t.c")
+        open(c, "w").write(prog)
+        exe = os.path.join(d, "t")
+        subprocess.check_call(["gcc", "-std=c99", "-I", os.path.dirname(HEADER), c, "-o", exe])
+        got = subprocess.check_output([exe]).decode().split("\n")
+    S, M, U = _lib.SelectiveScanArgs, _lib.SimplifiedScanArgs, _lib.StateUpdateArgs
+    assert got[0].split() == [str(ctypes.sizeof(t)) for t in (_lib.View, S, M, U)]
+    assert got[1].split() == [str(getattr(S, f).offset) for f in ("u", "x", "dout", "workspace", "dz")]
+    assert got[2].split() == [str(getattr(M, f).offset) for f in ("x", "dout", "workspace_bytes")]
+    assert got[3].split() == [str(getattr(U, f).offset) for f in ("state", "deltaA", "out_s2")]
+
+
+def _err():
+    return _lib.lib().lrnnx_last_error().decode()
+
+
+def test_argument_checks_mirror_reference_messages():
+    L = _lib.lib()
+    a = _lib.SelectiveScanArgs()
+    a.batch, a.dim, a.seqlen, a.dstate, a.n_groups = 1, 4, 8, 4, 1
+    a.itype, a.wtype, a.method = _lib.F32, _lib.F32, 99
+    assert L.lrnnx_selective_scan_fwd(a, None) != 0
+    assert "Discretization method not supported" in _err()
+    a.method = _lib.METHODS["mamba"]
+    a.dstate = 300
+    assert L.lrnnx_selective_scan_fwd(a, None) != 0
+    assert "state dimension <= 256" in _err()
+    a.dstate = 4
+    a.method, a.wtype = _lib.METHODS["s7"], _lib.C64
+    assert L.lrnnx_selective_scan_fwd(a, None) != 0
+    assert "S7 discretization only supports real" in _err()
+    a.method, a.wtype, a.itype = _lib.METHODS["zoh"], _lib.F32, _lib.BF16
+    assert L.lrnnx_selective_scan_fwd(a, None) != 0
+    assert "float32 input only" in _err()
+    a.itype = _lib.F32
+    assert L.lrnnx_selective_scan_fwd(a, None) != 0   # null tensors
+    assert "required" in _err()
+    assert L.lrnnx_selective_scan_fwd(None, None) != 0
+    m = _lib.SimplifiedScanArgs()
+    m.batch, m.dim, m.seqlen, m.dstate, m.method = 1, 2, 3, 1, _lib.METHODS["mamba"]
+    assert L.lrnnx_simplified_scan_fwd(m, None) != 0
+    assert "Discretization method not supported" in _err()
+    u = _lib.StateUpdateArgs()
+    u.batch, u.nheads, u.dim, u.dstate, u.ngroups, u.method = 1, 3, 4, 4, 2, 3
+    assert L.lrnnx_selective_state_update(u, None) != 0
+    assert "divisible" in _err()
+
+
+def test_python_api_refuses_cpu_tensors():
+    from lrnnx_amd import selective_scan_cuda, selective_scan_fn
+
+    u = torch.randn(1, 4, 8)
+    A = -torch.ones(4, 2)
+    B = torch.randn(1, 2, 8)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        selective_scan_fn(u, u.clone(), A, B, B.clone())
+    with pytest.raises(RuntimeError, match="GPU only"):
+        selective_scan_cuda.fwd(u, u.clone(), A, B[:, None], B[:, None].clone(), None, None, None, None, False,
+                                "mamba")
+
+
+def test_workspace_queries_are_host_only():
+    L = _lib.lib()
+    a = _lib.SelectiveScanArgs()
+    a.batch, a.dim, a.seqlen, a.dstate, a.n_groups = 8, 4096, 4096, 16, 1
+    a.itype, a.wtype, a.method, a.var_B, a.var_C = _lib.BF16, _lib.F32, 3, 1, 1
+    ck = L.lrnnx_selective_scan_ckpt_size(a)
+    assert ck == 8 * (4096 // 16) * 16 * 4096 * 4
+    assert L.lrnnx_selective_scan_workspace_size(a, 0) == 0
+    assert L.lrnnx_selective_scan_workspace_size(a, 1) > 0

@@ -1,0 +1,261 @@
+"""CPU tests that pin the oracle (oracle/scan_ref.py) before it is trusted as
+the parity reference.  Every check here is independent of the vectorised
+recurrence it tests: an O(L^2) scalar brute force, closed forms, library
+routines (scipy.signal.lfilter), invariants of the reference's API, and
+finite differences (gradcheck).  The reference holds no golden vectors for
+this path (its tests compare the CUDA op with *_ref at run time)."""
+
+import math
+
+import numpy as np
+import pytest
+import scipy.signal
+import torch
+import torch.nn.functional as F
+
+from oracle import brute
+from oracle import scan_ref as R
+
+torch.manual_seed(0)
+D64 = torch.float64
+
+
+def _tolist_seq(X, cplx):
+    if cplx:
+        Xc = torch.view_as_complex(X.reshape(*X.shape[:-1], X.shape[-1] // 2, 2).contiguous())
+        return [[[[complex(v) for v in row] for row in g] for g in bb] for bb in Xc]
+    return X.tolist()
+
+
+@pytest.mark.parametrize("method", R.METHODS)
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("varB,varC", [(False, False), (True, False), (False, True), (True, True)])
+def test_selective_ref_vs_bruteforce(method, cplx, varB, varC):
+    if cplx and method in ("s7", "rglru"):
+        pytest.skip("s7 / rglru are real-only (selective_scan_cpu.cpp:299-305)")
+    g = torch.Generator().manual_seed(hash((method, cplx, varB, varC)) % 1000)
+    b, d, L, n, G = 2, 4, 5, 3, 2
+    u = torch.randn(b, d, L, generator=g, dtype=D64)
+    delta = 0.5 * torch.randn(b, d, L, generator=g, dtype=D64)
+    z = torch.randn(b, d, L, generator=g, dtype=D64)
+    Dv = torch.randn(d, generator=g, dtype=D64)
+    bias = 0.3 * torch.randn(d, generator=g, dtype=D64)
+    A = (torch.rand(d, n, generator=g, dtype=D64) * 0.5 + 0.4) if method == "rglru" else \
+        (-torch.rand(d, n, generator=g, dtype=D64) - 0.2)
+    if cplx:
+        A = torch.complex(A, torch.randn(d, n, generator=g, dtype=D64))
+    Lb = 2 * L if cplx else L
+    B = torch.randn(b, G, n, Lb, generator=g, dtype=D64) if varB else torch.randn(d, n, dtype=A.dtype, generator=g)
+    C = torch.randn(b, G, n, Lb, generator=g, dtype=D64) if varC else torch.randn(d, n, dtype=A.dtype, generator=g)
+    out, last = R.selective_scan_ref(u, delta, A, B, C, Dv, z, bias, None, True, True, method, compute_dtype=D64)
+    cl = (lambda M: [[complex(v) for v in r] for r in M]) if cplx else (lambda M: M.tolist())
+    Bl = _tolist_seq(B, cplx) if varB else cl(B)
+    Cl = _tolist_seq(C, cplx) if varC else cl(C)
+    ob, lb = brute.selective_scan(u.tolist(), delta.tolist(), cl(A), Bl, Cl, Dv.tolist(), z.tolist(), bias.tolist(),
+                                  None, True, method)
+    assert torch.allclose(out, torch.tensor(ob, dtype=D64), rtol=1e-12, atol=1e-12)
+    assert torch.allclose(last, torch.tensor(lb, dtype=last.dtype), rtol=1e-12, atol=1e-12)
+    # kernel-boundary form: x carries hold h (without a constant B) and prod A_bar
+    o2, x, oz = R.selective_scan_fwd_ref(u, delta, A, B, C, Dv, z, bias, None, True, method, compute_dtype=D64)
+    assert torch.allclose(oz, out, rtol=1e-12, atol=1e-12)
+    hl = x[:, :, -1, 1::2]
+    if not varB and method != "rglru":
+        hl = hl * B
+    assert torch.allclose(hl, last, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("method", ["mamba", "zoh", "bilinear", "dirac"])
+def test_selective_ref_deltaA_vs_bruteforce(method):
+    g = torch.Generator().manual_seed(11)
+    b, d, L, n = 1, 3, 6, 2
+    u, delta = torch.randn(b, d, L, generator=g, dtype=D64), torch.rand(b, d, L, generator=g, dtype=D64)
+    dA = torch.rand(b, d, L, generator=g, dtype=D64)
+    A = -torch.rand(d, n, generator=g, dtype=D64) - 0.1
+    B = torch.randn(b, 1, n, L, generator=g, dtype=D64)
+    C = torch.randn(b, 1, n, L, generator=g, dtype=D64)
+    out = R.selective_scan_ref(u, delta, A, B, C, deltaA=dA, discretization=method, compute_dtype=D64)
+    ob, _ = brute.selective_scan(u.tolist(), delta.tolist(), A.tolist(), B.tolist(), C.tolist(), deltaA=dA.tolist(),
+                                 method=method)
+    assert torch.allclose(out, torch.tensor(ob, dtype=D64), rtol=1e-12, atol=1e-12)
+
+
+def test_closed_form_geometric_series():
+    # dirac with constant delta: A_bar = exp(delta A) = a, increment b = B u constant
+    L, dl, Av, Bv, uv = 50, 0.3, -0.7, 1.3, 0.8
+    u = torch.full((1, 1, L), uv, dtype=D64)
+    delta = torch.full((1, 1, L), dl, dtype=D64)
+    A = torch.tensor([[Av]], dtype=D64)
+    out = R.selective_scan_ref(u, delta, A, torch.tensor([[Bv]], dtype=D64), torch.ones(1, 1, dtype=D64),
+                               discretization="dirac", compute_dtype=D64)
+    a, b = math.exp(dl * Av), Bv * uv
+    t = torch.arange(L, dtype=D64)
+    ref = b * (1 - a ** (t + 1)) / (1 - a)
+    assert torch.allclose(out[0, 0], ref, rtol=1e-13, atol=1e-13)
+
+
+def test_closed_form_A_zero_is_cumsum():
+    g = torch.Generator().manual_seed(2)
+    b, d, L, n = 2, 3, 40, 4
+    u, delta = torch.randn(b, d, L, generator=g, dtype=D64), torch.randn(b, d, L, generator=g, dtype=D64)
+    B, C = torch.randn(b, n, L, generator=g, dtype=D64), torch.randn(b, n, L, generator=g, dtype=D64)
+    A = torch.zeros(d, n, dtype=D64)
+    out = R.selective_scan_ref(u, delta, A, B, C, delta_softplus=True, compute_dtype=D64)
+    dl = F.softplus(delta)
+    h = torch.cumsum((dl * u)[:, :, :, None] * B.permute(0, 2, 1)[:, None], dim=2)  # (b, d, l, n)
+    ref = (h * C.permute(0, 2, 1)[:, None]).sum(-1)
+    assert torch.allclose(out, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_closed_form_zero_delta_gives_Du():
+    g = torch.Generator().manual_seed(3)
+    u = torch.randn(2, 5, 17, generator=g, dtype=D64)
+    Dv = torch.randn(5, generator=g, dtype=D64)
+    out = R.selective_scan_ref(u, torch.zeros_like(u), -torch.rand(5, 4, dtype=D64), torch.randn(2, 4, 17, dtype=D64),
+                               torch.randn(2, 4, 17, dtype=D64), D=Dv, compute_dtype=D64)
+    assert torch.allclose(out, Dv[:, None] * u, rtol=0, atol=0)
+
+
+def test_closed_form_L1():
+    g = torch.Generator().manual_seed(4)
+    u, delta = torch.randn(2, 3, 1, generator=g, dtype=D64), torch.rand(2, 3, 1, generator=g, dtype=D64)
+    A, B, C = -torch.rand(3, 5, dtype=D64), torch.randn(2, 5, 1, dtype=D64), torch.randn(2, 5, 1, dtype=D64)
+    Dv = torch.randn(3, dtype=D64)
+    out = R.selective_scan_ref(u, delta, A, B, C, D=Dv, compute_dtype=D64)
+    ref = ((delta * u)[..., 0, None] * B[:, None, :, 0] * C[:, None, :, 0]).sum(-1) + Dv * u[..., 0]
+    assert torch.allclose(out[..., 0], ref, rtol=1e-13, atol=1e-13)
+
+
+@pytest.mark.parametrize("method", ["mamba", "dirac", "zoh", "bilinear"])
+def test_iir_filter_lfilter(method):
+    # N = 1, constant delta: first-order IIR y_t = a y_{t-1} + beta B u_t, checked with scipy
+    g = np.random.default_rng(5)
+    L, dl, Av, Bv, Cv = 300, 0.2, -1.7, 0.9, 1.1
+    x = g.standard_normal(L)
+    out = R.selective_scan_ref(torch.tensor(x)[None, None], torch.full((1, 1, L), dl, dtype=D64),
+                               torch.tensor([[Av]], dtype=D64), torch.tensor([[Bv]], dtype=D64),
+                               torch.tensor([[Cv]], dtype=D64), discretization=method, compute_dtype=D64)[0, 0]
+    if method == "bilinear":
+        a, beta = (1 + dl * Av / 2) / (1 - dl * Av / 2), dl / (1 - dl * Av / 2)
+    else:
+        a = math.exp(dl * Av)
+        beta = {"mamba": dl, "dirac": 1.0, "zoh": math.expm1(dl * Av) / Av}[method]
+    ref = Cv * scipy.signal.lfilter([beta * Bv], [1.0, -a], x)
+    assert np.allclose(out.numpy(), ref, rtol=1e-12, atol=1e-12)
+
+
+def test_lru_complex_iir_lfilter():
+    # config 1 at the boundary: dirac, delta = 1, A = log(Lambda) -> h_t = Lambda h_{t-1} + Bu_t
+    d = R.make_lru_inputs(2, 500, 3, seed=1)
+    lam, Bu = d["Lambda"].to(torch.complex128), d["Bu"].to(torch.complex128)
+    A = torch.log(lam).unsqueeze(-1)
+    ones = torch.ones(3, 1, dtype=torch.complex128)
+    out, x = R.simplified_scan_kernel_ref(Bu, torch.ones(2, 3, 500, dtype=D64), A, ones, ones, None, "dirac",
+                                          compute_dtype=D64)
+    for b in range(2):
+        for p in range(3):
+            ref = scipy.signal.lfilter([1.0], [1.0, -lam[p].item()], Bu[b, p].numpy())
+            assert np.allclose(out[b, p].numpy(), ref, rtol=1e-11, atol=1e-11)
+
+
+@pytest.mark.parametrize("method", ["bilinear", "zoh", "dirac"])
+def test_simplified_ref_vs_bruteforce(method):
+    g = torch.Generator().manual_seed(6)
+    b, H, P, L = 2, 3, 4, 7
+    u = torch.complex(torch.randn(b, H, L, generator=g, dtype=D64), torch.randn(b, H, L, generator=g, dtype=D64))
+    delta, deltaA = torch.rand(b, P, L, generator=g, dtype=D64), torch.rand(b, P, L, generator=g, dtype=D64)
+    A = torch.complex(-torch.rand(P, generator=g, dtype=D64), torch.randn(P, generator=g, dtype=D64))
+    Bm = torch.complex(torch.randn(P, H, generator=g, dtype=D64), torch.randn(P, H, generator=g, dtype=D64))
+    Cm = torch.complex(torch.randn(H, P, generator=g, dtype=D64), torch.randn(H, P, generator=g, dtype=D64))
+    for dA in (None, deltaA):
+        y, last = R.simplified_scan_ref(u, delta, A, Bm, Cm, deltaA=dA, return_last_state=True,
+                                        discretization=method, compute_dtype=D64)
+        Bu = torch.einsum("ph,bhl->bpl", Bm, u)
+        hb = brute.simplified_scan_states(Bu.tolist(), delta.tolist(), [complex(a) for a in A],
+                                          None if dA is None else dA.tolist(), method)
+        hb = torch.tensor(hb, dtype=torch.complex128)
+        assert torch.allclose(y, torch.einsum("hp,bpl->bhl", Cm, hb), rtol=1e-12, atol=1e-12)
+        assert torch.allclose(last, hb[:, :, -1], rtol=1e-12, atol=1e-12)
+        # kernel-level form with identity B/C is the state sequence
+        out_k, _ = R.simplified_scan_kernel_ref(Bu, delta, A[:, None], torch.ones(P, 1, dtype=A.dtype),
+                                                torch.ones(P, 1, dtype=A.dtype), dA, method, compute_dtype=D64)
+        assert torch.allclose(out_k, hb, rtol=1e-12, atol=1e-12)
+
+
+def test_invariants_selective():
+    inp = R.make_selective_inputs(2, 8, 30, 4, seed=7)
+    i64 = {k: (v.double() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    f = lambda **kw: R.selective_scan_ref(**{**dict(u=i64["u"], delta=i64["delta"], A=i64["A"], B=i64["B"],
+                                                     C=i64["C"], delta_bias=i64["delta_bias"], delta_softplus=True,
+                                                     compute_dtype=D64), **kw})
+    base = f()
+    # z gating: out(z) == out(z=None) * silu(z)
+    assert torch.allclose(f(z=i64["z"]), base * F.silu(i64["z"]), rtol=1e-13, atol=1e-13)
+    # D skip: out(D) - out(D=None) == D u
+    Dv = torch.randn(8, dtype=D64)
+    assert torch.allclose(f(D=Dv) - base, Dv[:, None] * i64["u"], rtol=1e-12, atol=1e-12)
+    # G = 1 4-D B/C == 3-D B/C
+    assert torch.allclose(f(B=i64["B"][:, None], C=i64["C"][:, None]), base, rtol=0, atol=0)
+    # deltaA equal to the processed delta reproduces the plain scan (reference test_simplified_scan_async.py:285)
+    dproc = F.softplus(i64["delta"] + i64["delta_bias"][:, None])
+    assert torch.allclose(f(deltaA=dproc), base, rtol=1e-13, atol=1e-13)
+    # the x carry at the 2048 boundary equals the state of the prefix run
+    inp2 = R.make_selective_inputs(1, 2, 2050, 2, seed=8, has_z=False)
+    a = {k: (v.double() if isinstance(v, torch.Tensor) else v) for k, v in inp2.items()}
+    _, x = R.selective_scan_fwd_ref(a["u"], a["delta"], a["A"], a["B"], a["C"], a["D"], None, a["delta_bias"], None,
+                                    True, "mamba", compute_dtype=D64)
+    _, last = R.selective_scan_ref(a["u"][..., :2048], a["delta"][..., :2048], a["A"], a["B"][..., :2048],
+                                   a["C"][..., :2048], a["D"], None, a["delta_bias"], None, True, True,
+                                   compute_dtype=D64)
+    assert torch.allclose(x[:, :, 0, 1::2], last, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("method", ["mamba", "zoh", "bilinear", "dirac", "s7", "rglru"])
+def test_gradcheck_selective(method):
+    g = torch.Generator().manual_seed(9)
+    b, d, L, n = 1, 2, 4, 2
+    u = torch.randn(b, d, L, generator=g, dtype=D64, requires_grad=True)
+    delta = (0.3 * torch.rand(b, d, L, generator=g, dtype=D64) + 0.1).requires_grad_(True)
+    A = ((torch.rand(d, n, generator=g, dtype=D64) * 0.5 + 0.4) if method == "rglru"
+         else (-torch.rand(d, n, generator=g, dtype=D64) - 0.2)).requires_grad_(True)
+    B = torch.randn(b, 1, n, L, generator=g, dtype=D64, requires_grad=True)
+    C = torch.randn(b, 1, n, L, generator=g, dtype=D64, requires_grad=True)
+    Dv = torch.randn(d, generator=g, dtype=D64, requires_grad=True)
+    z = torch.randn(b, d, L, generator=g, dtype=D64, requires_grad=True)
+    fn = lambda *t: R.selective_scan_ref(*t, discretization=method, compute_dtype=D64)
+    assert torch.autograd.gradcheck(fn, (u, delta, A, B, C, Dv, z), eps=1e-6, atol=1e-7)
+
+
+def test_state_update_equals_one_scan_step():
+    # decode step from the zero state == first step of the scan; a decode loop == the full scan
+    inp = R.make_selective_inputs(2, 6, 12, 4, seed=10)
+    a = {k: (v.double() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    full = R.selective_scan_ref(a["u"], a["delta"], a["A"], a["B"], a["C"], a["D"], a["z"], a["delta_bias"], None,
+                                True, compute_dtype=D64)
+    state = torch.zeros(2, 6, 4, dtype=D64)
+    outs = []
+    for t in range(12):
+        outs.append(R.selective_state_update_ref(state, a["u"][..., t], a["delta"][..., t], a["A"], a["B"][..., t],
+                                                 a["C"][..., t], a["D"], a["z"][..., t], a["delta_bias"], True,
+                                                 compute_dtype=D64))
+    assert torch.allclose(torch.stack(outs, -1), full, rtol=1e-12, atol=1e-12)
+
+
+def test_s7_and_rglru_wrapper_refs_match_kernel_semantics():
+    g = torch.Generator().manual_seed(12)
+    b, H, n, L = 2, 3, 4, 9
+    u = torch.randn(b, H, L, generator=g, dtype=D64)
+    A = torch.randn(b, n, L, generator=g, dtype=D64)
+    B = torch.randn(b, n, H, L, generator=g, dtype=D64)
+    C = torch.randn(b, H, n, L, generator=g, dtype=D64)
+    y = R.s7_scan_ref(u, A, B, C, compute_dtype=D64)
+    Bu = torch.einsum("bnhl,bhl->bnl", B, u)
+    ones = torch.ones(n, 1, dtype=D64)
+    states = R.selective_scan_ref(Bu, A, torch.zeros(n, 1, dtype=D64), ones, ones, discretization="s7",
+                                  compute_dtype=D64)
+    assert torch.allclose(y, torch.einsum("bhnl,bnl->bhl", C, states), rtol=1e-12, atol=1e-12)
+    u2, dl = torch.randn(b, H, L, generator=g, dtype=D64), torch.rand(b, H, L, generator=g, dtype=D64)
+    Ar = torch.rand(H, n, generator=g, dtype=D64) * 0.5 + 0.4
+    y2 = R.rglru_scan_ref(u2, dl, Ar, compute_dtype=D64)
+    onesH = torch.ones(H, n, dtype=D64)
+    y2k = R.selective_scan_ref(u2, dl, Ar, onesH, onesH, discretization="rglru", compute_dtype=D64)
+    assert torch.allclose(y2, y2k, rtol=1e-12, atol=1e-12)

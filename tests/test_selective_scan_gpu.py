@@ -1,0 +1,122 @@
+"""GPU parity of the selective scan (HIP kernels through the C ABI) against the
+float64 CPU oracle (oracle/scan_ref.py, a restatement of the reference's
+selective_scan_ref, lrnnx/ops/selective_scan.py:200-360).
+
+Tolerances (elementwise |got-ref| <= atol + rtol |ref|, atol relative to the
+tensor's max magnitude):
+  fp32 I/O  : outputs rtol 1e-4, atol 1e-5 * max|ref|; gradients the same,
+              except reductions over batch*length (dA, dD, ddelta_bias,
+              constant dB/dC) rtol 1e-4, atol 1e-4 * max|ref|.
+  bf16 I/O  : rtol 2e-2, atol 1e-2 * max|ref| (fp32 state; inputs are the
+              bf16-rounded values given to both sides).
+"""
+
+import pytest
+import torch
+
+from lrnnx_amd import selective_scan_fn
+from oracle import scan_ref as R
+from tests.parity import close, oracle_selective, to_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: (1e-4, 1e-5, 1e-4), torch.bfloat16: (2e-2, 1e-2, 1e-2), torch.float16: (1e-2, 5e-3, 5e-3)}
+
+
+def _run(dev, B, D, L, N, itype=torch.float32, method="mamba", varB=True, varC=True, has_z=True, has_D=True,
+         has_bias=True, softplus=True, groups=None, seed=0, with_deltaA=False, A_override=None):
+    inp = R.make_selective_inputs(B, D, L, N, seed=seed, itype=itype, groups=groups, varB=varB, varC=varC,
+                                  has_z=has_z, has_D=has_D, has_bias=has_bias)
+    if A_override is not None:
+        inp["A"] = A_override
+    if not softplus:
+        # without softplus the time step must already be positive (as the callers guarantee)
+        inp["delta"] = (inp["delta"].float().abs() * 0.2 + 1e-3).to(itype)
+    g = torch.Generator().manual_seed(seed + 100)
+    dout = torch.randn(B, D, L, generator=g).to(itype)
+    deltaA = (0.5 * torch.rand(B, D, L, generator=g)).to(itype) if with_deltaA else None
+    ref_out, ref_last, ref_g = oracle_selective(inp, method, softplus, deltaA, True, dout)
+    d = to_dev(inp, dev)
+    leaves = {}
+    for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias"):
+        if d.get(k) is not None:
+            leaves[k] = d[k].clone().requires_grad_(True)
+    dA_dev = deltaA.to(dev).requires_grad_(True) if deltaA is not None else None
+    out, last = selective_scan_fn(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"],
+                                  leaves.get("D"), leaves.get("z"), leaves.get("delta_bias"), dA_dev, softplus,
+                                  True, method)
+    out.backward(dout.to(dev))
+    torch.cuda.synchronize()
+    rt, at, atr = TOL[itype]
+    close("out", out, ref_out, rt, at)
+    close("last_state", last, ref_last, rt, at)
+    for k, v in leaves.items():
+        red = k in ("A", "D", "delta_bias") or (k == "B" and not varB) or (k == "C" and not varC)
+        close(f"d{k}", v.grad, ref_g[k], rt, atr if red else at)
+    if dA_dev is not None:
+        close("ddeltaA", dA_dev.grad, ref_g["deltaA"], rt, at)
+
+
+@pytest.mark.parametrize("L", [1, 7, 32, 100, 256, 511])
+def test_mamba_fp32_lengths(dev, L):
+    _run(dev, 2, 64, L, 16)
+
+
+@pytest.mark.parametrize("varB,varC", [(True, True), (True, False), (False, True), (False, False)])
+def test_mamba_fp32_var_const(dev, varB, varC):
+    _run(dev, 2, 70, 96, 16, varB=varB, varC=varC)
+
+
+@pytest.mark.parametrize("N", [1, 3, 8, 16, 33, 64])
+def test_mamba_fp32_dstate(dev, N):
+    _run(dev, 1, 64, 80, N)
+
+
+@pytest.mark.parametrize("flags", [dict(has_z=False), dict(has_D=False), dict(has_bias=False), dict(softplus=False)])
+def test_mamba_fp32_options(dev, flags):
+    _run(dev, 2, 64, 64, 16, **flags)
+
+
+def test_mamba_fp32_groups(dev):
+    _run(dev, 2, 128, 64, 16, groups=2)
+
+
+def test_mamba_fp32_deltaA(dev):
+    _run(dev, 2, 64, 64, 16, with_deltaA=True)
+
+
+@pytest.mark.parametrize("method", ["zoh", "bilinear", "dirac"])
+@pytest.mark.parametrize("varB,varC", [(True, True), (False, False)])
+def test_other_methods_fp32(dev, method, varB, varC):
+    _run(dev, 2, 64, 72, 8, method=method, varB=varB, varC=varC)
+
+
+@pytest.mark.parametrize("method", ["zoh", "bilinear", "dirac"])
+def test_other_methods_deltaA(dev, method):
+    _run(dev, 2, 64, 48, 8, method=method, with_deltaA=True)
+
+
+def test_s7_fp32(dev):
+    _run(dev, 2, 64, 64, 1, method="s7", varB=False, varC=False, has_z=False, has_D=False, has_bias=False,
+         softplus=False)
+
+
+def test_rglru_fp32(dev):
+    A = torch.rand(64, 1) * 0.5 + 0.45
+    _run(dev, 2, 64, 64, 1, method="rglru", varB=False, varC=False, has_z=False, has_D=False, has_bias=False,
+         softplus=False, A_override=A)
+
+
+@pytest.mark.parametrize("itype", [torch.bfloat16, torch.float16])
+def test_mamba_low_precision(dev, itype):
+    _run(dev, 2, 64, 128, 16, itype=itype)
+
+
+def test_mamba_bf16_cfg2_slice(dev):
+    # config-2 distributions on a channel slice (the full shape is timed by bench.py)
+    _run(dev, 2, 64, 2048, 16, itype=torch.bfloat16, seed=2)
+
+
+def test_mamba_fp32_long_chunks(dev):
+    # crosses the 2048-step chunk of the reference x carries
+    _run(dev, 1, 64, 4100, 16, seed=5)
