@@ -223,6 +223,61 @@ def other_configs(torch, ss, L_, dev):
     return res
 
 
+COPY_CALIB_BYTES = 1 << 30
+
+
+def traffic_from_counters(fetch_csv, write_csv):
+    """HBM bytes per launch of the headline kernels from rocprofv3 --pmc runs.
+
+    FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are scaled by what the same
+    counter reads for the plain copy of --copy-calib (COPY_CALIB_BYTES read and
+    written), so the result is in bytes of HBM traffic.
+    """
+    import csv
+    import re
+
+    def load(path, counter):
+        per = {}
+        with open(path) as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row.get("Kernel_Name", "")
+                per.setdefault(name, []).append(float(row["Counter_Value"]))
+        return per
+
+    out = {}
+    for key, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
+        per = load(path, counter)
+        copy = [v for k, vs in per.items() if re.search(r"copy|elementwise", k, re.I) for v in vs]
+        if not copy:
+            raise SystemExit(f"no copy kernel in {path}")
+        scale = COPY_CALIB_BYTES / (max(copy) * 1024.0)
+        for k, vs in per.items():
+            for tag in ("ss_bwd_kernel", "ss_fwd_kernel", "ss_reduce_bc_kernel", "ss_reduce_batch_kernel"):
+                if tag in k:
+                    ent = out.setdefault(tag, {})
+                    ent.setdefault(key, []).extend(v * 1024.0 * scale for v in vs)
+        out.setdefault("calibration", {})[key] = {"copy_counter_kib": max(copy), "scale": scale}
+    summary = {"calibration": out.pop("calibration")}
+    for tag, ent in out.items():
+        f = ent.get("fetch", [])
+        w = ent.get("write", [])
+        summary[tag] = {"fetch_bytes_per_launch": sum(f) / len(f) if f else None,
+                        "write_bytes_per_launch": sum(w) / len(w) if w else None, "launches": len(f)}
+    bwd = [summary.get(t) for t in ("ss_bwd_kernel",)]
+    if bwd[0] and bwd[0]["fetch_bytes_per_launch"] is not None:
+        red = summary.get("ss_reduce_bc_kernel", {})
+        tot = bwd[0]["fetch_bytes_per_launch"] + bwd[0]["write_bytes_per_launch"]
+        if red.get("fetch_bytes_per_launch") is not None:
+            tot += 2 * (red["fetch_bytes_per_launch"] + red["write_bytes_per_launch"])  # dB and dC launches
+        summary["bwd_bytes_per_launch"] = tot
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_cfg3.json")
+    with open(path, "w") as fh:
+        json.dump(summary, fh, indent=1)
+    print(json.dumps(summary, indent=1))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -230,7 +285,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1 and 2")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="first run a plain 1 GiB device copy (reference kernel for HBM byte counters)")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic_cfg3.json from two rocprofv3 --pmc counter_collection.csv "
+                         "files (FETCH_SIZE, WRITE_SIZE) of a --copy-calib run, then exit")
     args = ap.parse_args()
+    if args.traffic_from:
+        traffic_from_counters(*args.traffic_from)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the scan path needs no collectives; "
               "multi-GPU sharding is described in DESIGN.md but not built). Use --gpus 1.", file=sys.stderr)
@@ -247,6 +310,14 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     L_.lib()
+    if args.copy_calib:
+        _log(f"copy calibration: {COPY_CALIB_BYTES} bytes read + written")
+        src = torch.ones(COPY_CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(2):  # an elementwise kernel, not a DMA-engine copy
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     _log("building config-3 inputs on the GPU")
     Bt, D, L, N, G = 8, 4096, 4096, 16, 1
     inp = make_cfg3(dev, torch, None, Bt, D, L, N)

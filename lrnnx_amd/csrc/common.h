@@ -28,12 +28,9 @@ template <typename T> __device__ __forceinline__ T from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return static_cast<f16>(v); }
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
-  // round to nearest even; NaN stays a quiet NaN
-  uint32_t u = __float_as_uint(v);
+  // round to nearest even (gfx950 v_cvt_pk_bf16_f32; NaN stays NaN)
   bf16 r;
-  if ((u & 0x7fffffffu) > 0x7f800000u) { r.bits = 0x7fc0; return r; }
-  u += 0x7fffu + ((u >> 16) & 1u);
-  r.bits = static_cast<uint16_t>(u >> 16);
+  r.bits = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
   return r;
 }
 

@@ -1,26 +1,42 @@
 // Selective scan backward (real weights), gfx950.
 //
 // Semantics: reference kernel csrc/selective_scan/selective_scan_backward.cuh:86-845
-// (gradients of the forward defined in ss_fwd_impl.h; softplus backward =
-// sigmoid, :797-799; dz = dout * out * sigma(z) (1 + z (1 - sigma(z))), :218-219).
+// (gradients of the forward in ss_fwd_impl.h; softplus backward = sigmoid,
+// :797-799; dz = dout * out * sigma(z) (1 + z (1 - sigma(z))), :218-219).
 //
-// Per workgroup (b, channel block), tiles of kTB steps are processed from the
-// end of the sequence to the start; each tile holds kTB / kCk checkpoint
-// intervals ("sub-chunks").  Per sub-chunk a wave
-//   1. reloads h at the sub-chunk start from the forward's fp32 checkpoints,
-//   2. recomputes A_bar and h for the kCk steps and keeps them in VGPRs,
-//   3. walks the steps backwards: dh_t = A_bar_{t+1} dh_{t+1} + C_t dy_t, and
-//      accumulates the per-step partials of du / ddelta / ddeltaA (summed
-//      over its kS states; crossed over waves in LDS), dA (per lane), and the
-//      kS * kCk per-lane values of dB / dC,
-//   4. reduce-scatters the dB / dC values over the 64 channels of the wave
-//      and writes one fp32 partial per (channel block, b, n, t) to the
-//      workspace.  A second kernel sums the partials over channel blocks in
-//      a fixed order, so the result is deterministic (the reference uses one
-//      global atomic per element and channel block,
-//      selective_scan_backward.cuh:483-502).
+// Same decomposition as the forward (lane = channel, wave = kS states).
+// Tiles of kTB steps are processed from the end of the sequence to the start;
+// a tile holds kTB / kCk checkpoint intervals ("sub-chunks").  Per sub-chunk a
+// wave takes h at the sub-chunk start from the forward's fp32 checkpoints,
+// recomputes A_bar and h for the kCk steps into VGPRs, then walks the steps
+// backwards:
+//   dh_t = A_bar_{t+1} dh_{t+1} + C_t dy_t
+// accumulating the per-step partials of du / ddelta / ddeltaA (summed over
+// its kS states; crossed over waves in LDS), dA (per lane) and the values of
+// dB / dC.  dB / dC are reduce-scattered over the 64 channels of the wave
+// (the two cross-half steps right after each step, so only 16 values per
+// quantity stay live) and one fp32 partial per (channel block, b, n, t) goes
+// to the workspace; a second kernel sums the partials over channel blocks in
+// a fixed order, so the result is deterministic (the reference uses one
+// global atomic per element and channel block, selective_scan_backward.cuh:483-502).
+//
+// Phases per tile k, as in the forward:
+//   compute(k)  issue the asynchronous LDS fetch of raw tile k-1 (u, delta,
+//               dout, z, out, deltaA, B/C rows and, when a tile is one
+//               checkpoint interval, the checkpoint rows), then the
+//               sub-chunks of tile k;
+//   finish(k)   wait + barrier; epilogue of tile k (du, ddelta, ddeltaA and
+//               the per-element dD / ddelta_bias terms) and conversion of raw
+//               tile k-1 (delta' = softplus(delta + bias), dy = dout silu(z),
+//               dz written here, B/C to fp32).
+// The fp32 operands of a tile (delta', u, dy) are double buffered because the
+// epilogue of tile k and the conversion of tile k-1 share a phase.
 #pragma once
+#include <type_traits>
+
 #include "ss_common.h"
+#include "ss_fwd_impl.h"
+#include "tile_io.h"
 
 namespace lrnnx {
 
@@ -28,7 +44,6 @@ template <int kMethod>
 __host__ __device__ constexpr bool needs_p3() {
   return kMethod == LRNNX_ZOH || kMethod == LRNNX_BILINEAR || kMethod == LRNNX_RGLRU;
 }
-inline bool needs_p3_rt(int m) { return m == LRNNX_ZOH || m == LRNNX_BILINEAR || m == LRNNX_RGLRU; }
 
 struct SSBwdWs {  // fp32 workspace sections (element offsets)
   int64_t dBv, dCv, dA, dBc, dCc, dD, dbias, ckpt, total;
@@ -52,181 +67,398 @@ inline SSBwdWs ss_bwd_ws(const lrnnx_selective_scan_args& a, const SSGeom& g, bo
   return w;
 }
 
-template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC>
+// kV consecutive floats from LDS (kV = 4 or 2, naturally aligned)
+template <int kV>
+__device__ __forceinline__ void lds_ldv(const float* p, float* o) {
+  if constexpr (kV == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  } else {
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    o[0] = v.x; o[1] = v.y;
+  }
+}
+template <int kV>
+__device__ __forceinline__ void lds_stv(float* p, const float* o) {
+  if constexpr (kV == 4) *reinterpret_cast<float4*>(p) = make_float4(o[0], o[1], o[2], o[3]);
+  else *reinterpret_cast<float2*>(p) = make_float2(o[0], o[1]);
+}
+
+// Scheduling fence between groups of steps: keeps the compiler from hoisting
+// the LDS operand loads of later steps above the arithmetic of earlier ones
+// (which raises register pressure past 256 VGPRs and forces spills).
+__device__ __forceinline__ void kSchedFence() { __builtin_amdgcn_sched_barrier(0); }
+
+// the kS consecutive floats of a wave's states (16-byte aligned when kS >= 4)
+template <int kS>
+__device__ __forceinline__ void lds_states(const float* p, float* o) {
+  if constexpr (kS == 1) {
+    o[0] = p[0];
+  } else {
+#pragma unroll
+    for (int k = 0; k < kS; k += 4) lds_ldv<4>(p + k, o + k);
+  }
+}
+
+template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
 __global__ void __launch_bounds__(512)
 ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_ck, float* __restrict__ ws,
-              const SSBwdWs wo, const float* __restrict__ ckp) {
+              const SSBwdWs wo, const float* __restrict__ ckp, const int flags) {
   constexpr int kCk = ck_for(kS);
   constexpr int kTB = tb_for(kS);
-  constexpr int kP = kTB + 4;
-  constexpr int V = Vec<IT>::n;
-  constexpr int kNV = kS * kCk;       // dB/dC values per lane per sub-chunk (<= 64)
+  constexpr int kEl = 16 / sizeof(IT);  // elements per 16-byte block
+  constexpr int kQ = kTB / kEl;         // 16-byte blocks per raw row
+  constexpr int kG = kTB / 4;           // groups of 4 steps
+  constexpr int kNV = kS * kCk;         // dB/dC values per lane per sub-chunk (<= 64)
+  constexpr int kV = kCk < 4 ? kCk : 4; // steps per LDS vector access
   constexpr bool kP3 = needs_p3<kMethod>();
-  extern __shared__ float smem[];
+  constexpr int kNWmax = fwd_nw_max(kS);
+  constexpr int kNPmax = kNWmax * kS;
+  constexpr int kRawArr = kWave * kTB * (int)sizeof(IT);
+  constexpr int kRawBC = kNPmax * kTB * (int)sizeof(IT);
+  constexpr bool kCkLds = kTB == kCk;   // one checkpoint interval per tile: stage its rows in LDS
+  static_assert(kTB % kCk == 0, "tile must hold whole checkpoint intervals");
+  static_assert(kCk % kV == 0 && kTB % 4 == 0, "vector access must not straddle groups");
+
+  // separate LDS objects (see the forward): the asynchronous fetches write
+  // only s_raw_* and s_ck
+  __shared__ __attribute__((aligned(16))) char s_raw_u[kRawArr];
+  __shared__ __attribute__((aligned(16))) char s_raw_d[kRawArr];
+  __shared__ __attribute__((aligned(16))) char s_raw_do[kRawArr];
+  __shared__ __attribute__((aligned(16))) char s_raw_z[kRawArr];
+  __shared__ __attribute__((aligned(16))) char s_raw_os[kRawArr];
+  __shared__ __attribute__((aligned(16))) char s_raw_dA[kDA ? kRawArr : 16];
+  __shared__ __attribute__((aligned(16))) char s_raw_bc[(kVarB || kVarC) ? 2 * kRawBC : 16];
+  __shared__ __attribute__((aligned(16))) float s_ck[kCkLds ? 2 * kNPmax * kWave : 4];  // [buf][NP][64]
+  __shared__ __attribute__((aligned(16))) float s_dl[2][kWave * kTB];  // [buf][kG][64][4] delta'
+  __shared__ __attribute__((aligned(16))) float s_u[2][kWave * kTB];   // u
+  __shared__ __attribute__((aligned(16))) float s_dy[2][kWave * kTB];  // dout * silu(z)
+  __shared__ __attribute__((aligned(16))) float s_dt[kDA ? kWave * kTB : 4];  // deltaA
+  __shared__ __attribute__((aligned(16))) float s_B[kVarB ? kTB * kNPmax : 4];  // [kTB][NPmax] (step-major)
+  __shared__ __attribute__((aligned(16))) float s_C[kVarC ? kTB * kNPmax : 4];
+  __shared__ __attribute__((aligned(16))) float s_P1[kNWmax * kWave * kTB];  // [w][kG][64][4]
+  __shared__ __attribute__((aligned(16))) float s_P2[kNWmax * kWave * kTB];
+  __shared__ __attribute__((aligned(16))) float s_P3[kP3 ? kNWmax * kWave * kTB : 4];
+  __shared__ float s_Dv[kWave], s_bias[kWave];
 
   const int nW = blockDim.x / kWave;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int64_t b = blockIdx.y;
-  const int64_t D = a.dim, L = a.seqlen, N = a.dstate;
+  const int64_t D = a.dim, L = a.seqlen;
+  const int N = (int)a.dstate;
   const int64_t cb = blockIdx.x;
   const int64_t d0 = cb * CB;
+  const int rows = (int)((D - d0) < CB ? (D - d0) : CB);
   const int64_t d = d0 + lane;
-  const bool lane_ok = lane < CB && d < D;
+  const bool lane_ok = lane < rows;
   const int64_t grp = (a.var_B || a.var_C) ? d0 / (D / a.n_groups) : 0;
   const int n0 = w * kS;
+  const int NP = nW * kS;
   const bool has_dA_in = a.deltaA.ptr != nullptr;
-  const bool has_dA = has_dA_in && uses_deltaA<kMethod>();
   const bool has_bias = a.delta_bias.ptr != nullptr;
   const bool has_D = a.D.ptr != nullptr;
   const bool has_z = a.z.ptr != nullptr;
+  const bool async_ok = flags & kFlagAsyncIn;   // fetched tensors allow 16-byte LDS-DMA rows
+  const bool out_al = flags & kFlagAlignedOut;  // du / ddelta / ddeltaA / dz rows are 16-byte aligned
 
-  float* sDl = smem;               // [64][kP] delta'
-  float* sU = sDl + kWave * kP;    // [64][kP] u
-  float* sDy = sU + kWave * kP;    // [64][kP] dy = dout * silu(z)
-  float* sDt = sDy + kWave * kP;   // [64][kP] deltaA
-  float* sB = sDt + kWave * kP;    // [nW*kS][kTB] (rows >= N are zero)
-  float* sC = sB + nW * kS * kTB;  // [nW*kS][kTB]
-  float* sP1 = sC + nW * kS * kTB;       // [nW][64][kP]
-  float* sP2 = sP1 + nW * kWave * kP;
-  float* sP3 = sP2 + nW * kWave * kP;  // only if kP3
-  if (!has_dA) sDt = sDl;
+  const IT* gu = static_cast<const IT*>(a.u.ptr) + b * a.u.s0 + d0 * a.u.s1;
+  const IT* gd = static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d0 * a.delta.s1;
+  const IT* gdo = static_cast<const IT*>(a.dout.ptr) + b * a.dout.s0 + d0 * a.dout.s1;
+  const IT* gz = has_z ? static_cast<const IT*>(a.z.ptr) + b * a.z.s0 + d0 * a.z.s1 : nullptr;
+  const IT* gos =
+      has_z ? static_cast<const IT*>(a.out_saved.ptr) + b * a.out_saved.s0 + d0 * a.out_saved.s1 : nullptr;
+  const IT* gdA = kDA ? static_cast<const IT*>(a.deltaA.ptr) + b * a.deltaA.s0 + d0 * a.deltaA.s1 : nullptr;
+  const IT* gB = kVarB ? static_cast<const IT*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1 : nullptr;
+  const IT* gC = kVarC ? static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1 : nullptr;
+  IT* gdu = static_cast<IT*>(a.du.ptr) + b * a.du.s0 + d0 * a.du.s1;
+  IT* gddl = static_cast<IT*>(a.ddelta.ptr) + b * a.ddelta.s0 + d0 * a.ddelta.s1;
+  IT* gddA = has_dA_in ? static_cast<IT*>(a.ddeltaA.ptr) + b * a.ddeltaA.s0 + d0 * a.ddeltaA.s1 : nullptr;
+  IT* gdz = has_z ? static_cast<IT*>(a.dz.ptr) + b * a.dz.s0 + d0 * a.dz.s1 : nullptr;
+  const uint32_t su = (uint32_t)a.u.s1, sd = (uint32_t)a.delta.s1, sdo = (uint32_t)a.dout.s1;
+  const uint32_t sz = (uint32_t)a.z.s1, sos = (uint32_t)a.out_saved.s1, sdA = (uint32_t)a.deltaA.s1;
+  const uint32_t sBn = (uint32_t)a.B.s2, sCn = (uint32_t)a.C.s2;
+  const uint32_t sdu = (uint32_t)a.du.s1, sddl = (uint32_t)a.ddelta.s1, sddA = (uint32_t)a.ddeltaA.s1;
+  const uint32_t sdz = (uint32_t)a.dz.s1;
+  // checkpoint rows: state n of interval kk at ckp[((b * n_ck + kk) * N + n) * D + d]
+  const float* gck = ckp + b * n_ck * N * D + d0;
 
   float a2[kS], Araw[kS], bcst[kS], ccst[kS], cout_c[kS];
-  float dh[kS], Anext[kS], dA_acc[kS], dBc_acc[kS], dCc_acc[kS];
-  const float* Ap = static_cast<const float*>(a.A.ptr);
-  const float* Bp = static_cast<const float*>(a.B.ptr);
-  const float* Cp = static_cast<const float*>(a.C.ptr);
+  // dh: gradient of the state at the current step; gn: A_bar_{t+1} dh_{t+1}
+  float dh[kS], gn[kS], dA_acc[kS], dBc_acc[kS], dCc_acc[kS];
+  {
+    const float* Ap = static_cast<const float*>(a.A.ptr);
+    const float* Bp = static_cast<const float*>(a.B.ptr);
+    const float* Cp = static_cast<const float*>(a.C.ptr);
 #pragma unroll
-  for (int k = 0; k < kS; ++k) {
-    const int n = n0 + k;
-    const bool ok = lane_ok && n < N;
-    const float Av = ok ? Ap[d * a.A.s0 + n * a.A.s1] : (kMethod == LRNNX_RGLRU ? 0.5f : -1.f);
-    Araw[k] = Av;
-    a2[k] = prep_a2<kMethod>(Av);
-    bcst[k] = (!kVarB && ok) ? Bp[d * a.B.s0 + n * a.B.s1] : 1.f;
-    ccst[k] = (!kVarC && ok) ? Cp[d * a.C.s0 + n * a.C.s1] : 1.f;
-    cout_c[k] = ok ? (kVarB ? 1.f : bcst[k]) * (kVarC ? 1.f : ccst[k]) : 0.f;
-    dh[k] = 0.f; Anext[k] = 0.f; dA_acc[k] = 0.f; dBc_acc[k] = 0.f; dCc_acc[k] = 0.f;
+    for (int k = 0; k < kS; ++k) {
+      const int n = n0 + k;
+      const bool ok = lane_ok && n < N;
+      const float Av = ok ? Ap[d * a.A.s0 + n * a.A.s1] : (kMethod == LRNNX_RGLRU ? 0.5f : -1.f);
+      Araw[k] = Av;
+      a2[k] = prep_a2<kMethod>(Av);
+      bcst[k] = (!kVarB && ok) ? Bp[d * a.B.s0 + n * a.B.s1] : 1.f;
+      ccst[k] = (!kVarC && ok) ? Cp[d * a.C.s0 + n * a.C.s1] : 1.f;
+      cout_c[k] = ok ? (kVarB ? 1.f : bcst[k]) * (kVarC ? 1.f : ccst[k]) : 0.f;
+      dh[k] = 0.f; gn[k] = 0.f; dA_acc[k] = 0.f; dBc_acc[k] = 0.f; dCc_acc[k] = 0.f;
+    }
   }
   float dD_acc = 0.f, dbias_acc = 0.f;  // wave 0, per channel
+  if (tid < kWave) {
+    s_Dv[tid] = (has_D && tid < rows) ? static_cast<const float*>(a.D.ptr)[(d0 + tid) * a.D.s0] : 0.f;
+    s_bias[tid] = (has_bias && tid < rows) ? static_cast<const float*>(a.delta_bias.ptr)[(d0 + tid) * a.delta_bias.s0]
+                                           : 0.f;
+  }
 
-  const IT* Pu = static_cast<const IT*>(a.u.ptr);
-  const IT* Pd = static_cast<const IT*>(a.delta.ptr);
-  const IT* PdA = static_cast<const IT*>(a.deltaA.ptr);
-  const IT* Pz = static_cast<const IT*>(a.z.ptr);
-  const IT* Pdo = static_cast<const IT*>(a.dout.ptr);
-  const IT* Pos = static_cast<const IT*>(a.out_saved.ptr);
-  const IT* VBp = static_cast<const IT*>(a.B.ptr);
-  const IT* VCp = static_cast<const IT*>(a.C.ptr);
-  IT* Pdu = static_cast<IT*>(a.du.ptr);
-  IT* Pddl = static_cast<IT*>(a.ddelta.ptr);
-  IT* PddA = static_cast<IT*>(a.ddeltaA.ptr);
-  IT* Pdz = static_cast<IT*>(a.dz.ptr);
-
-  const int vpr = kTB / V;
-  const int rows = CB;
   const int64_t n_tiles = (L + kTB - 1) / kTB;
-  for (int64_t tile = n_tiles - 1; tile >= 0; --tile) {
+
+  // ---- fetch of raw tile `tile` (checkpoint rows into buffer `buf`).  As in
+  // the forward, the synchronous form runs in the finish phase only.
+  auto async_tile = [&](int64_t tile) __attribute__((always_inline)) {
+    return async_ok && (L - tile * kTB) >= kTB && rows == CB && CB == kWave;
+  };
+  auto fetch_async = [&](int64_t tile, int buf) __attribute__((always_inline)) {
     const int64_t t0 = tile * kTB;
-    const int Tv = (int)((L - t0) < kTB ? (L - t0) : kTB);
-    __syncthreads();
-    // ---- tile load; dz is finished here (it needs only dout, out, z)
-    for (int e = tid; e < rows * vpr; e += blockDim.x) {
-      const int r = e / vpr, c = (e % vpr) * V;
-      const int64_t dr = d0 + r;
-      const int nv = Tv - c;
-      float vu[V], vd[V], vdy[V], va[V];
-      if (dr < D && nv > 0) {
-        const int n_ = nv < V ? nv : V;
-        load_vec(Pu + b * a.u.s0 + dr * a.u.s1 + t0 + c, n_, vu);
-        load_vec(Pd + b * a.delta.s0 + dr * a.delta.s1 + t0 + c, n_, vd);
-        load_vec(Pdo + b * a.dout.s0 + dr * a.dout.s1 + t0 + c, n_, vdy);
-        const float bias = has_bias ? static_cast<const float*>(a.delta_bias.ptr)[dr * a.delta_bias.s0] : 0.f;
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-          const float x = vd[i] + bias;
-          vd[i] = a.delta_softplus ? softplus20(x) : x;
+    tile_fetch_async<IT, kQ>(gu + t0, su, CB, s_raw_u, w, nW, lane);
+    tile_fetch_async<IT, kQ>(gd + t0, sd, CB, s_raw_d, w, nW, lane);
+    tile_fetch_async<IT, kQ>(gdo + t0, sdo, CB, s_raw_do, w, nW, lane);
+    if (has_z) {
+      tile_fetch_async<IT, kQ>(gz + t0, sz, CB, s_raw_z, w, nW, lane);
+      tile_fetch_async<IT, kQ>(gos + t0, sos, CB, s_raw_os, w, nW, lane);
+    }
+    if constexpr (kDA) tile_fetch_async<IT, kQ>(gdA + t0, sdA, CB, s_raw_dA, w, nW, lane);
+    if constexpr (kVarB) tile_fetch_async<IT, kQ>(gB + t0, sBn, N, s_raw_bc, w, nW, lane);
+    if constexpr (kVarC) tile_fetch_async<IT, kQ>(gC + t0, sCn, N, s_raw_bc + kRawBC, w, nW, lane);
+    if constexpr (kCkLds) {
+      if (tile > 0)  // h at the tile start = checkpoint of interval tile - 1 (64 channels x N states)
+        tile_fetch_async<float, kWave * 4 / 16>(gck + (tile - 1) * N * D, (uint32_t)D, N,
+                                                 reinterpret_cast<char*>(s_ck + buf * kNPmax * kWave), w, nW, lane);
+    }
+  };
+  auto fetch_sync = [&](int64_t tile, int buf) __attribute__((always_inline)) {
+    const int64_t t0 = tile * kTB;
+    const int nt = (int)((L - t0) < kTB ? (L - t0) : kTB);
+    tile_fetch_sync<IT, kQ>(gu + t0, su, kWave, rows, nt, s_raw_u, tid, blockDim.x);
+    tile_fetch_sync<IT, kQ>(gd + t0, sd, kWave, rows, nt, s_raw_d, tid, blockDim.x);
+    tile_fetch_sync<IT, kQ>(gdo + t0, sdo, kWave, rows, nt, s_raw_do, tid, blockDim.x);
+    if (has_z) {
+      tile_fetch_sync<IT, kQ>(gz + t0, sz, kWave, rows, nt, s_raw_z, tid, blockDim.x);
+      tile_fetch_sync<IT, kQ>(gos + t0, sos, kWave, rows, nt, s_raw_os, tid, blockDim.x);
+    }
+    if constexpr (kDA) tile_fetch_sync<IT, kQ>(gdA + t0, sdA, kWave, rows, nt, s_raw_dA, tid, blockDim.x);
+    if constexpr (kVarB) tile_fetch_sync<IT, kQ>(gB + t0, sBn, NP, N, nt, s_raw_bc, tid, blockDim.x);
+    if constexpr (kVarC) tile_fetch_sync<IT, kQ>(gC + t0, sCn, NP, N, nt, s_raw_bc + kRawBC, tid, blockDim.x);
+    if constexpr (kCkLds) {
+      if (tile > 0) {
+        const float* src = gck + (tile - 1) * N * D;
+        float* dst = s_ck + buf * kNPmax * kWave;
+        for (int j = tid; j < N * kWave; j += blockDim.x) {
+          const int n = j / kWave, c = j % kWave;
+          dst[j] = c < rows ? src[(int64_t)n * D + c] : 0.f;
         }
-        if (has_z) {
-          float vz[V], vo[V], dzv[V];
-          load_vec(Pz + b * a.z.s0 + dr * a.z.s1 + t0 + c, n_, vz);
-          load_vec(Pos + b * a.out_saved.s0 + dr * a.out_saved.s1 + t0 + c, n_, vo);
-#pragma unroll
-          for (int i = 0; i < V; ++i) {
-            const float sg = 1.f / (1.f + expf(-vz[i]));
-            dzv[i] = vdy[i] * vo[i] * sg * (1.f + vz[i] * (1.f - sg));
-            vdy[i] = vdy[i] * vz[i] * sg;
-          }
-          store_vec(Pdz + b * a.dz.s0 + dr * a.dz.s1 + t0 + c, n_, dzv);
-        }
-        if (has_dA) load_vec(PdA + b * a.deltaA.s0 + dr * a.deltaA.s1 + t0 + c, n_, va);
-      } else {
-#pragma unroll
-        for (int i = 0; i < V; ++i) { vu[i] = 0.f; vd[i] = 0.f; vdy[i] = 0.f; va[i] = 0.f; }
       }
+    }
+  };
+
+  // a tile whose kTB steps and 64 channels are all valid
+  auto full_tile = [&](int64_t tile) __attribute__((always_inline)) {
+    return (L - tile * kTB) >= kTB && rows == kWave;
+  };
+
+  // ---- raw tile -> fp32 operands of buffer `p`; dz is finished here
+  auto convert = [&](auto full_tag, int64_t tile, int p) __attribute__((always_inline)) {
+    constexpr bool kFull = decltype(full_tag)::value;
+    const int64_t t0 = tile * kTB;
+    const int nt = (int)((L - t0) < kTB ? (L - t0) : kTB);
+    for (int j = tid; j < kWave * kQ; j += blockDim.x) {
+      const int r = j / kQ, q = j % kQ;
+      float vu[kEl], vd[kEl], vdo[kEl], vz[kEl], vo[kEl], vda[kEl], dzv[kEl];
+      raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_u + 16 * j), vu);
+      raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_d + 16 * j), vd);
+      raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_do + 16 * j), vdo);
+      if constexpr (kDA) raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_dA + 16 * j), vda);
+      if (has_z) {
+        raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_z + 16 * j), vz);
+        raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_os + 16 * j), vo);
+      }
+      const float bias = s_bias[r];
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        sU[r * kP + c + i] = vu[i];
-        sDl[r * kP + c + i] = vd[i];
-        sDy[r * kP + c + i] = vdy[i];
-        if (has_dA) sDt[r * kP + c + i] = va[i];
+      for (int i = 0; i < kEl; ++i) {
+        const bool valid = kFull || (r < rows && q * kEl + i < nt);
+        const float x = vd[i] + bias;
+        const float dl = a.delta_softplus ? softplus_fast(x) : x;
+        float dy = vdo[i];
+        if (has_z) {
+          const float sg = sigmoid_fast(vz[i]);
+          dzv[i] = dy * vo[i] * sg * (1.f + vz[i] * (1.f - sg));
+          dy = dy * vz[i] * sg;
+        }
+        vd[i] = valid ? dl : 0.f;
+        vu[i] = valid ? vu[i] : 0.f;
+        vdo[i] = valid ? dy : 0.f;
+        if constexpr (kDA) vda[i] = valid ? vda[i] : 0.f;
+      }
+      const int n_ = kFull ? kEl : nt - q * kEl;
+      if (has_z && (kFull || (r < rows && n_ > 0))) {
+        IT* pz = gdz + r * sdz + t0 + q * kEl;
+        if ((kFull && out_al) || (n_ >= kEl && (reinterpret_cast<uintptr_t>(pz) & 15u) == 0))
+          *reinterpret_cast<uint4*>(pz) = f32_to_raw<IT>(dzv);
+        else
+          for (int i = 0; i < (n_ < kEl ? n_ : kEl); ++i) pz[i] = from_f32<IT>(dzv[i]);
+      }
+      // step s = q * kEl + i goes to group s / 4, slot s % 4 of row r
+#pragma unroll
+      for (int i = 0; i < kEl; i += 4) {
+        const int o = (((q * kEl + i) / 4) * kWave + r) * 4;
+        lds_stv<4>(&s_dl[p][o], vd + i);
+        lds_stv<4>(&s_u[p][o], vu + i);
+        lds_stv<4>(&s_dy[p][o], vdo + i);
+        if constexpr (kDA) lds_stv<4>(&s_dt[o], vda + i);
       }
     }
     if constexpr (kVarB || kVarC) {
-      for (int e = tid; e < nW * kS * vpr; e += blockDim.x) {
-        const int n = e / vpr, c = (e % vpr) * V;
-        const int nv = n < N ? Tv - c : 0;  // padded states get B = C = 0
-        const int n_ = nv < V ? (nv > 0 ? nv : 0) : V;
-        float vb[V], vc[V];
+      for (int j = tid; j < NP * kQ; j += blockDim.x) {
+        const bool st_ok = j / kQ < N;  // padded states read B = C = 0
+        float v[kEl];
+        const int n = j / kQ, s0 = (j % kQ) * kEl;
         if constexpr (kVarB) {
-          load_vec(VBp + b * a.B.s0 + grp * a.B.s1 + n * a.B.s2 + t0 + c, n_, vb);
+          raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_bc + 16 * j), v);
 #pragma unroll
-          for (int i = 0; i < V; ++i) sB[n * kTB + c + i] = vb[i];
+          for (int i = 0; i < kEl; ++i) s_B[(s0 + i) * kNPmax + n] = st_ok ? v[i] : 0.f;
         }
         if constexpr (kVarC) {
-          load_vec(VCp + b * a.C.s0 + grp * a.C.s1 + n * a.C.s2 + t0 + c, n_, vc);
+          raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_bc + kRawBC + 16 * j), v);
 #pragma unroll
-          for (int i = 0; i < V; ++i) sC[n * kTB + c + i] = vc[i];
+          for (int i = 0; i < kEl; ++i) s_C[(s0 + i) * kNPmax + n] = st_ok ? v[i] : 0.f;
         }
       }
     }
-    __syncthreads();
+  };
 
-    // ---- sub-chunks of this tile, last first
-    const int n_sub = (Tv + kCk - 1) / kCk;
-    for (int s = n_sub - 1; s >= 0; --s) {
-      const int ts = s * kCk;                       // tile-local start
-      const int Ls = (Tv - ts) < kCk ? (Tv - ts) : kCk;
-      const int64_t kk = (t0 + ts) / kCk;           // global checkpoint interval index
-      float h0[kS];
+  // ---- epilogue of tile `tile` (fp32 buffer p): cross-wave sums -> du, ddelta,
+  // ddeltaA; the per-element terms of dD (dy u) and ddelta_bias (ddelta) are
+  // left in wave 0's partial slots
+  auto epilogue = [&](auto full_tag, int64_t tile, int p) __attribute__((always_inline)) {
+    constexpr bool kFull = decltype(full_tag)::value;
+    const int64_t t0 = tile * kTB;
+    const int nt = (int)((L - t0) < kTB ? (L - t0) : kTB);
+    for (int j = tid; j < kWave * kQ; j += blockDim.x) {
+      const int r = j / kQ, q = j % kQ;
+      const float Dv = s_Dv[r];
+      float vdu[kEl], vdd[kEl], vda[kEl];
 #pragma unroll
-      for (int k = 0; k < kS; ++k)
+      for (int i = 0; i < kEl; i += 4) {
+        const int g = (q * kEl + i) / 4;
+        const int o = (g * kWave + r) * 4;
+        float P1[4], P2[4], P3[4] = {0.f, 0.f, 0.f, 0.f}, x[4];
+        lds_ldv<4>(&s_P1[o], P1);
+        lds_ldv<4>(&s_P2[o], P2);
+        if constexpr (kP3) lds_ldv<4>(&s_P3[o], P3);
+        for (int ww = 1; ww < nW; ++ww) {
+          const int ow = ((ww * kG + g) * kWave + r) * 4;
+          lds_ldv<4>(&s_P1[ow], x);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) P1[m] += x[m];
+          lds_ldv<4>(&s_P2[ow], x);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) P2[m] += x[m];
+          if constexpr (kP3) {
+            lds_ldv<4>(&s_P3[ow], x);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) P3[m] += x[m];
+          }
+        }
+        float dlv[4], uv[4], dyv[4], q1[4], q2[4];
+        lds_ldv<4>(&s_dl[p][o], dlv);
+        lds_ldv<4>(&s_u[p][o], uv);
+        lds_ldv<4>(&s_dy[p][o], dyv);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          float ddl;
+          if constexpr (kMethod == LRNNX_MAMBA) {
+            vdu[i + m] = fmaf(dlv[m], P1[m], Dv * dyv[m]);
+            ddl = uv[m] * P1[m];
+          } else {
+            vdu[i + m] = fmaf(Dv, dyv[m], P1[m]);
+            ddl = P3[m];
+          }
+          if constexpr (kDA) {
+            vda[i + m] = P2[m];
+          } else {
+            ddl += P2[m];
+            vda[i + m] = 0.f;
+          }
+          // d softplus(x)/dx = sigmoid(x) = 1 - exp(-softplus(x))
+          const float dd = a.delta_softplus ? ddl * one_minus_exp_neg(dlv[m]) : ddl;
+          vdd[i + m] = dd;
+          q1[m] = dyv[m] * uv[m];
+          q2[m] = dd;
+        }
+        lds_stv<4>(&s_P1[o], q1);
+        lds_stv<4>(&s_P2[o], q2);
+      }
+      const int n_ = kFull ? kEl : nt - q * kEl;
+      if (!kFull && (r >= rows || n_ <= 0)) continue;
+      auto put = [&](IT* pp, const float* v) __attribute__((always_inline)) {
+        if ((kFull && out_al) || (n_ >= kEl && (reinterpret_cast<uintptr_t>(pp) & 15u) == 0))
+          *reinterpret_cast<uint4*>(pp) = f32_to_raw<IT>(v);
+        else
+          for (int i = 0; i < (n_ < kEl ? n_ : kEl); ++i) pp[i] = from_f32<IT>(v[i]);
+      };
+      put(gdu + r * sdu + t0 + q * kEl, vdu);
+      put(gddl + r * sddl + t0 + q * kEl, vdd);
+      if (has_dA_in) put(gddA + r * sddA + t0 + q * kEl, vda);
+    }
+  };
+
+  // ---- one checkpoint interval: steps [ts, ts + Ls) of tile `tile` (fp32 buffer p).
+  // kFull: Ls == kCk, no per-step guards.  Steps past Ls hold zero operands
+  // and are skipped; their partial slots are written as zero.
+  auto sub_chunk = [&](auto full_tag, int64_t tile, int p, int ts, int Ls) __attribute__((always_inline)) {
+    constexpr bool kFull = decltype(full_tag)::value;
+    const int64_t kk = (tile * kTB + ts) / kCk;  // global checkpoint interval
+    float h0[kS];
+#pragma unroll
+    for (int k = 0; k < kS; ++k) {
+      if constexpr (kCkLds) {
+        h0[k] = (kk > 0 && n0 + k < N) ? s_ck[(p * kNPmax + n0 + k) * kWave + lane] : 0.f;
+      } else {
         h0[k] = (kk > 0 && lane_ok && n0 + k < N) ? ckp[((b * n_ck + kk - 1) * N + n0 + k) * D + d] : 0.f;
-
-      float Ab[kCk][kS], H[kCk][kS];
-      // recompute
-      {
-        float hc[kS];
+      }
+    }
+    // recompute A_bar and h over the interval
+    float Ab[kCk][kS], H[kCk][kS];
+    {
+      float hc[kS];
 #pragma unroll
-        for (int k = 0; k < kS; ++k) hc[k] = h0[k];
+      for (int k = 0; k < kS; ++k) hc[k] = h0[k];
 #pragma unroll
-        for (int j = 0; j < kCk; ++j) {
-          if (j < Ls) {
-            const int t = ts + j;
-            const float dl = sDl[lane * kP + t], uu = sU[lane * kP + t], dt = sDt[lane * kP + t];
-            const float du_ = dl * uu;
+      for (int jg = 0; jg < kCk; jg += kV) {
+        kSchedFence();
+        const int t = ts + jg;
+        const int o = ((t >> 2) * kWave + lane) * 4 + (t & 3);
+        float dlv[kV], uvv[kV], dtv[kV];
+        lds_ldv<kV>(&s_dl[p][o], dlv);
+        lds_ldv<kV>(&s_u[p][o], uvv);
+        if constexpr (kDA) lds_ldv<kV>(&s_dt[o], dtv);
+#pragma unroll
+        for (int i = 0; i < kV; ++i) {
+          const int j = jg + i;
+          if (kFull || j < Ls) {
+            const float dt = kDA ? dtv[i] : dlv[i];
+            const float du_ = dlv[i] * uvv[i];
+            float bv[kS];
+            if constexpr (kVarB) lds_states<kS>(&s_B[(t + i) * kNPmax + n0], bv);
 #pragma unroll
             for (int k = 0; k < kS; ++k) {
               float beta;
-              const float ab = disc_real<kMethod>(dt, dl, a2[k], Araw[k], beta);
-              float bin = 1.f;
-              if constexpr (kVarB) bin = sB[(n0 + k) * kTB + t];
+              const float ab = disc_real<kMethod>(dt, dlv[i], a2[k], Araw[k], beta);
+              const float bin = kVarB ? bv[k] : 1.f;
               float inc;
               if constexpr (kMethod == LRNNX_MAMBA) inc = du_ * bin;
-              else if constexpr (uses_B_input<kMethod>()) inc = beta * uu * bin;
-              else inc = beta * uu;
+              else if constexpr (uses_B_input<kMethod>()) inc = beta * uvv[i] * bin;
+              else inc = beta * uvv[i];
               hc[k] = fmaf(ab, hc[k], inc);
               Ab[j][k] = ab;
               H[j][k] = hc[k];
@@ -234,57 +466,71 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
           }
         }
       }
-      // reverse walk.  dB/dC: for kS >= 4 the two cross-half reduce-scatter
-      // steps (index bits 5, 4 = the top bits of k) are applied right after
-      // each step, leaving 16 values per quantity (index bits 3..0).
-      constexpr int kAcc = kS >= 4 ? 16 : kNV;
-      float accB[kAcc], accC[kAcc];
+    }
+    // reverse walk.  dB/dC: for kS >= 4 the two cross-half reduce-scatter
+    // steps (index bits 5, 4 = the top bits of k) are applied right after
+    // each step, leaving 16 values per quantity (index bits 3..0).
+    constexpr int kAcc = kS >= 4 ? 16 : kNV;
+    float accB[kAcc], accC[kAcc];
 #pragma unroll
-      for (int j = kCk - 1; j >= 0; --j) {
-        if (j < Ls) {
-          const int t = ts + j;
-          const float dl = sDl[lane * kP + t], uu = sU[lane * kP + t], dt = sDt[lane * kP + t];
-          const float dy = sDy[lane * kP + t];
+    for (int jg = kCk - kV; jg >= 0; jg -= kV) {
+      kSchedFence();
+      const int t = ts + jg;
+      const int o = ((t >> 2) * kWave + lane) * 4 + (t & 3);
+      float dlv[kV], uvv[kV], dtv[kV], dyv[kV];
+      float p1v[kV], p2v[kV], p3v[kV];
+      lds_ldv<kV>(&s_dl[p][o], dlv);
+      lds_ldv<kV>(&s_u[p][o], uvv);
+      lds_ldv<kV>(&s_dy[p][o], dyv);
+      if constexpr (kDA) lds_ldv<kV>(&s_dt[o], dtv);
+#pragma unroll
+      for (int i = kV - 1; i >= 0; --i) {
+        const int j = jg + i;
+        p1v[i] = 0.f; p2v[i] = 0.f; p3v[i] = 0.f;
+        if (kFull || j < Ls) {
+          const float dl = dlv[i], uu = uvv[i], dt = kDA ? dtv[i] : dlv[i], dy = dyv[i];
           const float du_ = dl * uu;
           float p1 = 0.f, p2 = 0.f, p3 = 0.f;
-          float vB[kS], vC[kS];
+          float vB[kS], vC[kS], bv[kS], cv[kS];
+          if constexpr (kVarB) lds_states<kS>(&s_B[(t + i) * kNPmax + n0], bv);
+          if constexpr (kVarC) lds_states<kS>(&s_C[(t + i) * kNPmax + n0], cv);
 #pragma unroll
           for (int k = 0; k < kS; ++k) {
             // effective output weight: (C_t or C_const) * (B_const when B is constant)
             float cvar = 0.f, cc = cout_c[k];
-            float bin = 1.f;
             if constexpr (kVarC) {
-              cvar = sC[(n0 + k) * kTB + t];
+              cvar = cv[k];
               cc = kVarB ? cvar : cvar * cout_c[k];
             }
-            if constexpr (kVarB) bin = sB[(n0 + k) * kTB + t];
-            dh[k] = fmaf(Anext[k], dh[k], dy * cc);
+            const float bin = kVarB ? bv[k] : 1.f;
+            dh[k] = fmaf(dy, cc, gn[k]);
             const float ab = Ab[j][k];
             const float hp = j > 0 ? H[j - 1][k] : h0[k];
             const float hcur = H[j][k];
-            Anext[k] = ab;
-            // contribution through A_bar: dh * hp * dA_bar/d(.)
+            const float gk = ab * dh[k];  // carried to step t-1
+            gn[k] = gk;
+            // through A_bar: dh * hp * dA_bar/d(.)
             if constexpr (kMethod == LRNNX_MAMBA || kMethod == LRNNX_DIRAC || kMethod == LRNNX_ZOH) {
-              const float wv = dh[k] * (ab * hp);
+              const float wv = gk * hp;
               p2 = fmaf(wv, Araw[k], p2);
               dA_acc[k] = fmaf(wv, dt, dA_acc[k]);
             } else if constexpr (kMethod == LRNNX_BILINEAR) {
               const float vA = 0.5f * dt * Araw[k];
-              const float q = dh[k] * hp / ((1.f - vA) * (1.f - vA));
-              p2 = fmaf(q, Araw[k], p2);
-              dA_acc[k] = fmaf(q, dt, dA_acc[k]);
+              const float qv = dh[k] * hp / ((1.f - vA) * (1.f - vA));
+              p2 = fmaf(qv, Araw[k], p2);
+              dA_acc[k] = fmaf(qv, dt, dA_acc[k]);
             } else if constexpr (kMethod == LRNNX_S7) {
               const float den = dl * dl + 0.5f;
               p2 = fmaf(dh[k] * hp, 2.f * dl / (den * den), p2);
             } else {  // RGLRU: dA_bar/ddelta = A_bar ln A, dA_bar/dA = delta A_bar / A
-              const float wv = dh[k] * (ab * hp);
+              const float wv = gk * hp;
               const float lnA = a2[k] * kLn2;
               p2 = fmaf(wv, lnA, p2);
               dA_acc[k] = fmaf(wv, dl / Araw[k], dA_acc[k]);
             }
-            // contribution through the input term
+            // through the input term
             if constexpr (kMethod == LRNNX_MAMBA) {
-              p1 = fmaf(dh[k], bin, p1);                 // du = delta' * p1, ddelta' += u * p1
+              p1 = fmaf(dh[k], bin, p1);  // du = delta' p1, ddelta' += u p1
               if constexpr (kVarB) vB[k] = dh[k] * du_;
             } else if constexpr (kMethod == LRNNX_DIRAC || kMethod == LRNNX_S7) {
               p1 = fmaf(dh[k], bin, p1);
@@ -322,14 +568,10 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
             if constexpr (!kVarB) dBc_acc[k] = fmaf(dyh, kVarC ? cvar : ccst[k], dBc_acc[k]);
             if constexpr (!kVarC) dCc_acc[k] = fmaf(dyh, kVarB ? 1.f : bcst[k], dCc_acc[k]);
           }
-          sP1[(w * kWave + lane) * kP + t] = p1;
-          sP2[(w * kWave + lane) * kP + t] = p2;
-          if constexpr (kP3) sP3[(w * kWave + lane) * kP + t] = p3;
+          p1v[i] = p1; p2v[i] = p2; p3v[i] = p3;
+          // lanes past the last channel hold zero operands (convert) and a zero
+          // checkpoint, so their dh and h, hence vB and vC, are exactly zero
           if constexpr (kVarB || kVarC) {
-            if (!lane_ok) {
-#pragma unroll
-              for (int k = 0; k < kS; ++k) { vB[k] = 0.f; vC[k] = 0.f; }
-            }
             if constexpr (kS >= 4) {
               if constexpr (kVarB) { rs_step32<kS / 2>(vB); rs_step16<kS / 4>(vB); }
               if constexpr (kVarC) { rs_step32<kS / 2>(vC); rs_step16<kS / 4>(vC); }
@@ -352,87 +594,107 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
           }
         }
       }
-      // dB / dC over the wave's channels -> one partial per (cb, b, n, t)
-      if constexpr (kVarB || kVarC) {
-        const int kq = lane / kCk, jq = lane % kCk;  // lane now owns index v = k * kCk + j
-        const bool wr = lane < kNV && n0 + kq < N && jq < Ls;
-        const int64_t tg = t0 + ts + jq;
-        if constexpr (kVarB) {
-          float r;
-          if constexpr (kS >= 4) { rs_tail16(accB, lane); r = accB[0]; }
-          else { float r64[64];
-#pragma unroll
-                 for (int i = 0; i < 64; ++i) r64[i] = i < kNV ? accB[i] : 0.f;
-                 r = reduce_scatter64(r64, lane); }
-          if (wr) ws[wo.dBv + ((cb * a.batch + b) * N + n0 + kq) * L + tg] = r;
-        }
-        if constexpr (kVarC) {
-          float r;
-          if constexpr (kS >= 4) { rs_tail16(accC, lane); r = accC[0]; }
-          else { float r64[64];
-#pragma unroll
-                 for (int i = 0; i < 64; ++i) r64[i] = i < kNV ? accC[i] : 0.f;
-                 r = reduce_scatter64(r64, lane); }
-          if (wr) ws[wo.dCv + ((cb * a.batch + b) * N + n0 + kq) * L + tg] = r;
-        }
-      }
+      const int op = ((w * kG + (t >> 2)) * kWave + lane) * 4 + (t & 3);
+      lds_stv<kV>(&s_P1[op], p1v);
+      lds_stv<kV>(&s_P2[op], p2v);
+      if constexpr (kP3) lds_stv<kV>(&s_P3[op], p3v);
     }
-    __syncthreads();
-
-    // ---- epilogue over the tile: cross-wave sums, du / ddelta / ddeltaA
-    for (int e = tid; e < rows * vpr; e += blockDim.x) {
-      const int r = e / vpr, c = (e % vpr) * V;
-      const int64_t dr = d0 + r;
-      const int nv = Tv - c;
-      if (dr >= D || nv <= 0) continue;
-      const int n_ = nv < V ? nv : V;
-      const float Dv = has_D ? static_cast<const float*>(a.D.ptr)[dr * a.D.s0] : 0.f;
-      float vdu[V], vdd[V], vda[V], q1[V], q2[V];
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const int t = c + i;
-        float P1 = 0.f, P2 = 0.f, P3 = 0.f;
-        for (int ww = 0; ww < nW; ++ww) {
-          P1 += sP1[(ww * kWave + r) * kP + t];
-          P2 += sP2[(ww * kWave + r) * kP + t];
-          if constexpr (kP3) P3 += sP3[(ww * kWave + r) * kP + t];
-        }
-        const float dl = sDl[r * kP + t], uu = sU[r * kP + t], dy = sDy[r * kP + t];
-        float ddl;
-        if constexpr (kMethod == LRNNX_MAMBA) {
-          vdu[i] = dl * P1 + Dv * dy;
-          ddl = uu * P1;
+    // dB / dC over the wave's channels -> one partial per (cb, b, n, t)
+    if constexpr (kVarB || kVarC) {
+      const int kq = lane / kCk, jq = lane % kCk;  // lane now owns index v = k * kCk + j
+      const bool wr = lane < kNV && n0 + kq < N && (kFull || jq < Ls);
+      const int64_t tg = tile * kTB + ts + jq;
+      if constexpr (kVarB) {
+        float r;
+        if constexpr (kS >= 4) {
+          rs_tail16(accB, lane);
+          r = accB[0];
         } else {
-          vdu[i] = P1 + Dv * dy;
-          ddl = P3;
-        }
-        if (has_dA) { vda[i] = P2; } else { ddl += P2; vda[i] = 0.f; }
-        // d softplus(x)/dx = sigmoid(x) = 1 - exp(-softplus(x))
-        const float dd = a.delta_softplus ? ddl * (-expm1f(-dl)) : ddl;
-        vdd[i] = dd;
-        q1[i] = dy * uu;
-        q2[i] = dd;
-      }
-      store_vec(Pdu + b * a.du.s0 + dr * a.du.s1 + t0 + c, n_, vdu);
-      store_vec(Pddl + b * a.ddelta.s0 + dr * a.ddelta.s1 + t0 + c, n_, vdd);
-      if (has_dA_in) store_vec(PddA + b * a.ddeltaA.s0 + dr * a.ddeltaA.s1 + t0 + c, n_, vda);
-      // per-element contributions to dD and ddelta_bias, summed below in t order
+          float r64[64];
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        sP1[r * kP + c + i] = i < n_ ? q1[i] : 0.f;
-        sP2[r * kP + c + i] = i < n_ ? q2[i] : 0.f;
+          for (int i = 0; i < 64; ++i) r64[i] = i < kNV ? accB[i] : 0.f;
+          r = reduce_scatter64(r64, lane);
+        }
+        if (wr) ws[wo.dBv + ((cb * a.batch + b) * N + n0 + kq) * L + tg] = r;
+      }
+      if constexpr (kVarC) {
+        float r;
+        if constexpr (kS >= 4) {
+          rs_tail16(accC, lane);
+          r = accC[0];
+        } else {
+          float r64[64];
+#pragma unroll
+          for (int i = 0; i < 64; ++i) r64[i] = i < kNV ? accC[i] : 0.f;
+          r = reduce_scatter64(r64, lane);
+        }
+        if (wr) ws[wo.dCv + ((cb * a.batch + b) * N + n0 + kq) * L + tg] = r;
       }
     }
+  };
+
+  // ---- prologue: last tile
+  {
+    const int64_t tl = n_tiles - 1;
+    if (async_tile(tl)) fetch_async(tl, (int)(tl & 1));
+    else fetch_sync(tl, (int)(tl & 1));
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
-    if (w == 0 && lane_ok) {
-      for (int t = 0; t < Tv; ++t) {
-        dD_acc += sP1[lane * kP + t];
-        dbias_acc += sP2[lane * kP + t];
+    if (full_tile(tl)) convert(std::true_type{}, tl, (int)(tl & 1));
+    else convert(std::false_type{}, tl, (int)(tl & 1));
+    __syncthreads();
+  }
+  for (int64_t tile = n_tiles - 1; tile >= 0; --tile) {
+    const int p = (int)(tile & 1);
+    const int64_t t0 = tile * kTB;
+    const int Tv = (int)((L - t0) < kTB ? (L - t0) : kTB);
+    const bool prev = tile > 0;
+    const bool prev_async = prev && async_tile(tile - 1);
+    if (prev_async) fetch_async(tile - 1, p ^ 1);
+
+    // ---- compute(tile): checkpoint intervals, last first
+    if (Tv == kTB) {
+#pragma unroll
+      for (int s = kTB / kCk - 1; s >= 0; --s) sub_chunk(std::true_type{}, tile, p, s * kCk, kCk);
+    } else {
+      for (int s = (Tv + kCk - 1) / kCk - 1; s >= 0; --s) {
+        const int ts = s * kCk;
+        sub_chunk(std::false_type{}, tile, p, ts, (Tv - ts) < kCk ? (Tv - ts) : kCk);
+      }
+    }
+
+    // ---- finish(tile): tile-1 in LDS, epilogue(tile), convert(tile-1)
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (prev && !prev_async) {
+      fetch_sync(tile - 1, p ^ 1);
+      __syncthreads();
+    }
+    if (full_tile(tile)) epilogue(std::true_type{}, tile, p);
+    else epilogue(std::false_type{}, tile, p);
+    if (prev) {
+      if (full_tile(tile - 1)) convert(std::true_type{}, tile - 1, p ^ 1);
+      else convert(std::false_type{}, tile - 1, p ^ 1);
+    }
+    __syncthreads();
+    if (w == 0) {  // dD / ddelta_bias terms of this tile, in step order
+#pragma unroll
+      for (int g = 0; g < kG; ++g) {
+        float q1[4], q2[4];
+        lds_ldv<4>(&s_P1[(g * kWave + lane) * 4], q1);
+        lds_ldv<4>(&s_P2[(g * kWave + lane) * 4], q2);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          if (4 * g + m < Tv) {
+            dD_acc += q1[m];
+            dbias_acc += q2[m];
+          }
+        }
       }
     }
   }
 
-  // per-(b, d, n) and per-(b, d) partials; summed over b by ss_reduce_kernel
+  // per-(b, d, n) and per-(b, d) partials; summed over b by ss_reduce_batch_kernel
 #pragma unroll
   for (int k = 0; k < kS; ++k) {
     if (lane_ok && n0 + k < N) {
@@ -446,12 +708,6 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
     ws[wo.dD + b * D + d] = dD_acc;
     ws[wo.dbias + b * D + d] = dbias_acc;
   }
-}
-
-inline size_t ss_bwd_smem_bytes(int kS, int kMethod, int64_t N, int nW) {
-  const int kTB = tb_for(kS), kP = kTB + 4;
-  const int np = needs_p3_rt(kMethod) ? 3 : 2;
-  return sizeof(float) * ((size_t)4 * kWave * kP + (size_t)2 * nW * kS * kTB + (size_t)np * nW * kWave * kP);
 }
 
 // Sum of the dB / dC partials over the channel blocks of each group, in
@@ -481,49 +737,76 @@ ss_reduce_batch_kernel(const float* __restrict__ part, lrnnx_view out, int64_t B
   static_cast<OT*>(out.ptr)[d * out.s0 + n * out.s1] = acc;
 }
 
-template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC>
+template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
 static hipError_t launch_bwd_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                                const float* ckp, hipStream_t st) {
   dim3 grid(g.n_cb, (unsigned)a.batch);
   dim3 block(g.nW * kWave);
-  const size_t sm = ss_bwd_smem_bytes(kS, kMethod, a.dstate, g.nW);
-  if (sm > kMaxLds) return hipErrorInvalidConfiguration;
-  auto kfn = ss_bwd_kernel<IT, kS, kMethod, kVarB, kVarC>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kfn, grid, block, sm, st, a, g.CB, g.n_ck, ws, wo, ckp);
-  e = hipGetLastError();
+  if (g.nW > fwd_nw_max(kS)) return hipErrorInvalidConfiguration;
+  // async LDS fetches need 16-byte aligned row starts for every fetched tensor
+  auto al = [](const void* p, int64_t s_batch, int64_t s_row) {
+    return p == nullptr || ((reinterpret_cast<uintptr_t>(p) & 15u) == 0 && ((s_batch * sizeof(IT)) & 15) == 0 &&
+                            ((s_row * sizeof(IT)) & 15) == 0);
+  };
+  const bool has_z = a.z.ptr != nullptr;
+  const bool in_ok = al(a.u.ptr, a.u.s0, a.u.s1) && al(a.delta.ptr, a.delta.s0, a.delta.s1) &&
+                     al(a.dout.ptr, a.dout.s0, a.dout.s1) && (!has_z || al(a.z.ptr, a.z.s0, a.z.s1)) &&
+                     (!has_z || al(a.out_saved.ptr, a.out_saved.s0, a.out_saved.s1)) &&
+                     (!kDA || al(a.deltaA.ptr, a.deltaA.s0, a.deltaA.s1)) &&
+                     (!kVarB || (al(a.B.ptr, a.B.s0, a.B.s2) && ((a.B.s1 * sizeof(IT)) & 15) == 0)) &&
+                     (!kVarC || (al(a.C.ptr, a.C.s0, a.C.s2) && ((a.C.s1 * sizeof(IT)) & 15) == 0)) &&
+                     (reinterpret_cast<uintptr_t>(ckp) & 15u) == 0 && (a.dim % 4) == 0;
+  const bool out_ok = al(a.du.ptr, a.du.s0, a.du.s1) && al(a.ddelta.ptr, a.ddelta.s0, a.ddelta.s1) &&
+                      al(a.ddeltaA.ptr, a.ddeltaA.s0, a.ddeltaA.s1) && (!has_z || al(a.dz.ptr, a.dz.s0, a.dz.s1));
+  const int flags = (in_ok ? kFlagAsyncIn : 0) | (out_ok ? kFlagAlignedOut : 0);
+  hipLaunchKernelGGL((ss_bwd_kernel<IT, kS, kMethod, kVarB, kVarC, kDA>), grid, block, 0, st, a, g.CB, g.n_ck, ws,
+                     wo, ckp, flags);
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t B = a.batch, D = a.dim, N = a.dstate, L = a.seqlen, G = a.n_groups;
   if constexpr (kVarB || kVarC) {
     const int64_t ncpg = g.n_cb / G;
     dim3 rg((unsigned)((L + 255) / 256), (unsigned)(B * G * N));
-    if constexpr (kVarB) hipLaunchKernelGGL(ss_reduce_bc_kernel<IT>, rg, dim3(256), 0, st, ws + wo.dBv, a.dB, B, G, N, L, ncpg);
-    if constexpr (kVarC) hipLaunchKernelGGL(ss_reduce_bc_kernel<IT>, rg, dim3(256), 0, st, ws + wo.dCv, a.dC, B, G, N, L, ncpg);
+    if constexpr (kVarB)
+      hipLaunchKernelGGL(ss_reduce_bc_kernel<IT>, rg, dim3(256), 0, st, ws + wo.dBv, a.dB, B, G, N, L, ncpg);
+    if constexpr (kVarC)
+      hipLaunchKernelGGL(ss_reduce_bc_kernel<IT>, rg, dim3(256), 0, st, ws + wo.dCv, a.dC, B, G, N, L, ncpg);
   }
   const unsigned gdn = (unsigned)((D * N + 255) / 256), gd = (unsigned)((D + 255) / 256);
   hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dA, a.dA, B, D, N);
-  if constexpr (!kVarB) hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dBc, a.dB, B, D, N);
-  if constexpr (!kVarC) hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dCc, a.dC, B, D, N);
+  if constexpr (!kVarB)
+    hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dBc, a.dB, B, D, N);
+  if constexpr (!kVarC)
+    hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dCc, a.dC, B, D, N);
   if (a.dD.ptr) {
-    lrnnx_view v = a.dD; v.s1 = 0;
+    lrnnx_view v = a.dD;
+    v.s1 = 0;
     hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gd), dim3(256), 0, st, ws + wo.dD, v, B, D, (int64_t)1);
   }
   if (a.ddelta_bias.ptr) {
-    lrnnx_view v = a.ddelta_bias; v.s1 = 0;
+    lrnnx_view v = a.ddelta_bias;
+    v.s1 = 0;
     hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gd), dim3(256), 0, st, ws + wo.dbias, v, B, D, (int64_t)1);
   }
   return hipGetLastError();
 }
 
+template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC>
+static hipError_t launch_bwd_da(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
+                                const float* ckp, hipStream_t st) {
+  if constexpr (uses_deltaA<kMethod>()) {
+    if (a.deltaA.ptr != nullptr) return launch_bwd_t<IT, kS, kMethod, kVarB, kVarC, true>(a, g, ws, wo, ckp, st);
+  }
+  return launch_bwd_t<IT, kS, kMethod, kVarB, kVarC, false>(a, g, ws, wo, ckp, st);
+}
+
 template <typename IT, int kS, int kMethod>
 static hipError_t launch_bwd_bc(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                                 const float* ckp, hipStream_t st) {
-  if (a.var_B && a.var_C) return launch_bwd_t<IT, kS, kMethod, true, true>(a, g, ws, wo, ckp, st);
-  if (a.var_B) return launch_bwd_t<IT, kS, kMethod, true, false>(a, g, ws, wo, ckp, st);
-  if (a.var_C) return launch_bwd_t<IT, kS, kMethod, false, true>(a, g, ws, wo, ckp, st);
-  return launch_bwd_t<IT, kS, kMethod, false, false>(a, g, ws, wo, ckp, st);
+  if (a.var_B && a.var_C) return launch_bwd_da<IT, kS, kMethod, true, true>(a, g, ws, wo, ckp, st);
+  if (a.var_B) return launch_bwd_da<IT, kS, kMethod, true, false>(a, g, ws, wo, ckp, st);
+  if (a.var_C) return launch_bwd_da<IT, kS, kMethod, false, true>(a, g, ws, wo, ckp, st);
+  return launch_bwd_da<IT, kS, kMethod, false, false>(a, g, ws, wo, ckp, st);
 }
 
 template <typename IT, int kMethod>

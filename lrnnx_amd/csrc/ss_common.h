@@ -26,6 +26,10 @@ __host__ __device__ constexpr int tb_for(int kS) { return kS >= 8 ? 8 : 16; }
 __host__ __device__ constexpr int tf_for(int kS) { return kS >= 32 ? 16 : 32; }
 constexpr size_t kMaxLds = 160 * 1024;
 
+// launch flags of the selective-scan kernels (computed on the host)
+constexpr int kFlagAsyncIn = 1;     // every fetched tensor has 16-byte aligned rows (LDS-DMA usable)
+constexpr int kFlagAlignedOut = 2;  // every written sequence tensor has 16-byte aligned rows
+
 inline int pick_kS(int64_t N) {
   if (N <= 4) return 1;
   if (N <= 16) return 4;

@@ -1,0 +1,9 @@
+// Selective scan forward, method "bilinear", fp32 I/O (instantiation unit; the
+// reference builds every method for fp32 input only,
+// csrc/selective_scan/forward_kernels/*.cu:3).
+#include "ss_fwd_impl.h"
+namespace lrnnx {
+hipError_t ss_fwd_bilinear_f32(const lrnnx_selective_scan_args& a, hipStream_t st) {
+  return launch_fwd_s<float, LRNNX_BILINEAR>(a, ss_geom(a), st);
+}
+}  // namespace lrnnx

@@ -95,7 +95,9 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None, deltaA=No
                     contrib = c * h
                     out[b][d][t] += 2.0 * contrib.real if is_c else contrib
                     if t == L - 1:
-                        last[b][d][n] = h
+                        # returned last state = kernel state times a constant B
+                        # (selective_scan.py:87-92); for rglru B is not in h
+                        last[b][d][n] = h * B[d][n] if (method == "rglru" and not varB) else h
             for t in range(L):
                 if D is not None:
                     out[b][d][t] += D[d] * u[b][d][t]

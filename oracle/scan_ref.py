@@ -159,6 +159,11 @@ def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
         zz = z if compute_dtype is None else z.to(rdt)
         out = out * F.silu(zz)
     out = out.to(dtype_in)
+    if return_last_state and discretization == "rglru" and not varB:
+        # The CUDA wrapper returns x's state times a constant B for every method
+        # (selective_scan.py:87-92).  For rglru that state never contained B
+        # (selective_scan.cuh:296-302), so the returned last state is h * B.
+        h = h * B.to(wdt)[None]
     return (out, h) if return_last_state else out
 
 

@@ -55,11 +55,12 @@ def test_selective_ref_vs_bruteforce(method, cplx, varB, varC):
                                   None, True, method)
     assert torch.allclose(out, torch.tensor(ob, dtype=D64), rtol=1e-12, atol=1e-12)
     assert torch.allclose(last, torch.tensor(lb, dtype=last.dtype), rtol=1e-12, atol=1e-12)
-    # kernel-boundary form: x carries hold h (without a constant B) and prod A_bar
+    # kernel-boundary form: x carries hold h (without a constant B) and prod A_bar;
+    # the wrapper multiplies a constant B back for every method (selective_scan.py:87-92)
     o2, x, oz = R.selective_scan_fwd_ref(u, delta, A, B, C, Dv, z, bias, None, True, method, compute_dtype=D64)
     assert torch.allclose(oz, out, rtol=1e-12, atol=1e-12)
     hl = x[:, :, -1, 1::2]
-    if not varB and method != "rglru":
+    if not varB:
         hl = hl * B
     assert torch.allclose(hl, last, rtol=1e-12, atol=1e-12)
 

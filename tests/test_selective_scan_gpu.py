@@ -30,8 +30,11 @@ def _run(dev, B, D, L, N, itype=torch.float32, method="mamba", varB=True, varC=T
     if A_override is not None:
         inp["A"] = A_override
     if not softplus:
-        # without softplus the time step must already be positive (as the callers guarantee)
+        # without softplus the time step delta + delta_bias must already be positive
+        # (as the callers guarantee)
         inp["delta"] = (inp["delta"].float().abs() * 0.2 + 1e-3).to(itype)
+        if inp.get("delta_bias") is not None:
+            inp["delta_bias"] = inp["delta_bias"].abs() * 0.01
     g = torch.Generator().manual_seed(seed + 100)
     dout = torch.randn(B, D, L, generator=g).to(itype)
     deltaA = (0.5 * torch.rand(B, D, L, generator=g)).to(itype) if with_deltaA else None
