@@ -1,0 +1,738 @@
+// Selective scan with complex weights (A, and constant B/C, complex64;
+// variable B/C real (.., 2L) interleaved), fp32 input.  Forward and backward.
+//
+// Semantics: reference kernels csrc/selective_scan/selective_scan.cuh:229-286
+// and selective_scan_backward.cuh:86-845 instantiated with complex weight_t
+// (methods zoh, bilinear, dirac, mamba; selective_scan_cpu.cpp:299-305):
+//   h_t = A_bar_t h_{t-1} + beta_t u_t B_t        (complex state per (b, d, n))
+//   y_t = 2 Re(sum_n C_t h_t) + D u_t,  out_z = y silu(z)
+// With a constant B the kernel keeps B out of the state and folds it into the
+// output weight (the stored state excludes B, as the reference's `x`).
+// Gradients of complex parameters follow PyTorch's convention
+// (dL/dRe + i dL/dIm); for a real delta, du, ... the real part of the
+// conjugated chain product.
+//
+// Decomposition (as the real-weight kernels): one workgroup = one batch row
+// and CB <= 64 channels of one B/C group, lane = channel, wave w = kS states
+// with their complex h in VGPRs, L walked in tiles of kTc steps staged
+// through LDS.  The forward writes complex state checkpoints every kCk
+// steps; the backward recomputes A_bar and h for one checkpoint interval in
+// VGPRs and walks it backwards.  dB/dC values of an interval (kS * kCk
+// complex values per quantity, 64 reals for B and C together) are
+// reduce-scattered over the wave's 64 channels and written as one fp32
+// partial per (channel block, b, n, t, re/im); a second kernel sums the
+// partials over channel blocks in a fixed order.
+#pragma once
+#include <type_traits>
+
+#include "ss_common.h"
+
+namespace lrnnx {
+namespace ssc {
+
+struct cf {
+  float r, i;
+};
+__device__ __forceinline__ cf cmk(float r, float i) { return cf{r, i}; }
+__device__ __forceinline__ cf cadd(cf a, cf b) { return cf{a.r + b.r, a.i + b.i}; }
+__device__ __forceinline__ cf csub(cf a, cf b) { return cf{a.r - b.r, a.i - b.i}; }
+__device__ __forceinline__ cf cmul(cf a, cf b) { return cf{a.r * b.r - a.i * b.i, a.r * b.i + a.i * b.r}; }
+__device__ __forceinline__ cf cconj(cf a) { return cf{a.r, -a.i}; }
+__device__ __forceinline__ cf cscale(cf a, float s) { return cf{a.r * s, a.i * s}; }
+// a * b + c
+__device__ __forceinline__ cf cfma(cf a, cf b, cf c) {
+  return cf{fmaf(a.r, b.r, fmaf(-a.i, b.i, c.r)), fmaf(a.r, b.i, fmaf(a.i, b.r, c.i))};
+}
+__device__ __forceinline__ cf cdiv(cf a, cf b) {
+  const float den = b.r * b.r + b.i * b.i;
+  return cf{(a.r * b.r + a.i * b.i) / den, (a.i * b.r - a.r * b.i) / den};
+}
+__device__ __forceinline__ cf cexp_(cf z) {
+  float s, c;
+  sincosf(z.i, &s, &c);
+  const float e = expf(z.r);
+  return cf{e * c, e * s};
+}
+// exp(z) - 1 without cancellation: expm1(x) cos y - 2 sin^2(y/2) + i e^x sin y
+__device__ __forceinline__ cf cexpm1_(cf z) {
+  float s, c;
+  sincosf(z.i, &s, &c);
+  const float sh = sinf(0.5f * z.i);
+  return cf{fmaf(expm1f(z.r), c, -2.f * sh * sh), expf(z.r) * s};
+}
+// Re(conj(a) * b)
+__device__ __forceinline__ float cdotr(cf a, cf b) { return fmaf(a.r, b.r, a.i * b.i); }
+
+// tile length along L (8 for 16 states per wave, so that the backward's LDS fits 160 KB)
+__host__ __device__ constexpr int tile_c(int kS) { return kS >= 16 ? 8 : 16; }
+constexpr int kPad = kWave + 1; // LDS row pitch of [kTc][64] tiles (conflict-free both ways)
+
+__host__ __device__ constexpr int ck_c(int kS) { return 16 / kS; }  // kS * kCk = 16 complex values
+
+inline int pick_kS_c(int64_t N) { return N <= 4 ? 1 : (N <= 16 ? 4 : (N <= 64 ? 8 : 16)); }
+
+struct SSCGeom {
+  int CB, n_cb, kS, nW, ck;
+  int64_t n_ck;
+};
+
+inline SSCGeom ssc_geom(const lrnnx_selective_scan_args& a) {
+  SSCGeom g;
+  const int64_t ratio = a.var_B || a.var_C ? a.dim / a.n_groups : a.dim;
+  if (a.n_groups <= 1 || !(a.var_B || a.var_C)) {
+    g.CB = 64;
+  } else {
+    int cb = 64;
+    while (cb > 1 && ratio % cb != 0) --cb;
+    g.CB = cb;
+  }
+  g.n_cb = (int)((a.dim + g.CB - 1) / g.CB);
+  g.kS = pick_kS_c(a.dstate);
+  g.nW = (int)((a.dstate + g.kS - 1) / g.kS);
+  g.ck = ck_c(g.kS);
+  g.n_ck = (a.seqlen + g.ck - 1) / g.ck;
+  return g;
+}
+
+// A_bar and beta of one (t, n) for a complex A (selective_scan.cuh:229-286).
+template <int kMethod>
+__device__ __forceinline__ void cdisc(float dtA, float dl, cf A, cf& Ab, cf& beta) {
+  if constexpr (kMethod == LRNNX_BILINEAR) {
+    const cf one = cmk(1.f, 0.f);
+    const cf v = cscale(A, 0.5f * dtA);
+    Ab = cdiv(cadd(one, v), csub(one, v));
+    beta = cdiv(cmk(dl, 0.f), csub(one, cscale(A, 0.5f * dl)));
+  } else {
+    Ab = cexp_(cscale(A, dtA));
+    if constexpr (kMethod == LRNNX_MAMBA) beta = cmk(dl, 0.f);
+    else if constexpr (kMethod == LRNNX_DIRAC) beta = cmk(1.f, 0.f);
+    else beta = cdiv(cexpm1_(cscale(A, dl)), A);  // ZOH
+  }
+}
+
+__device__ __forceinline__ float softplus_ref(float x) { return x <= 20.f ? log1pf(expf(x)) : x; }
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
+struct SSCPtrs {
+  int64_t b, d0;
+  int rows, NP;
+};
+
+// Stage one tile of (b, d0 .. d0 + 63, t0 .. t0 + kTc) sequence values in LDS
+// ([kTc][kPad], zero outside the valid rows / steps).
+template <int kTc, typename F>
+__device__ __forceinline__ void load_tile(const float* __restrict__ base, int64_t row_stride, int rows, int nt,
+                                          float* dst, int tid, int nth, F&& f) {
+  for (int j = tid; j < kWave * kTc; j += nth) {
+    const int r = j / kTc, t = j % kTc;
+    float v = 0.f;
+    if (r < rows && t < nt) v = f(base[r * row_stride + t], r);
+    dst[t * kPad + r] = v;
+  }
+}
+
+// Variable complex B or C rows of the group: s[t][n] (re, im), zero for padded states.
+template <int kTc>
+__device__ __forceinline__ void load_bc(const float* __restrict__ base, int64_t s_n, int N, int NP, int nt,
+                                        float* dst, int tid, int nth) {
+  for (int j = tid; j < NP * kTc * 2; j += nth) {
+    const int n = j / (kTc * 2), e = j % (kTc * 2);
+    const int t = e / 2;
+    float v = 0.f;
+    if (n < N && t < nt) v = base[n * s_n + e];
+    dst[(t * NP + n) * 2 + (e & 1)] = v;
+  }
+}
+
+// at most 4 / 8 / 16 waves for kS <= 4 / 8 / 16 (N <= 16 / 64 / 256)
+__host__ __device__ constexpr int ssc_max_threads(int kS) { return kS <= 4 ? 256 : kS * kWave; }
+
+template <int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
+__global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_fwd_kernel(const lrnnx_selective_scan_args a, const int CB,
+                                                       const int64_t n_ck) {
+  constexpr int kCk = ck_c(kS);
+  constexpr int kTc = tile_c(kS);
+  extern __shared__ float smem[];
+  const int nW = blockDim.x / kWave;
+  const int NP = nW * kS;
+  float* s_dl = smem;
+  float* s_u = s_dl + kTc * kPad;
+  float* s_dt = s_u + kTc * kPad;
+  float* s_z = s_dt + kTc * kPad;
+  float* s_B = s_z + kTc * kPad;
+  float* s_C = s_B + kTc * NP * 2;
+  float* s_Y = s_C + kTc * NP * 2;  // [nW][kTc][kPad]
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int64_t b = blockIdx.y, D = a.dim, L = a.seqlen;
+  const int N = (int)a.dstate;
+  const int64_t d0 = (int64_t)blockIdx.x * CB;
+  const int rows = (int)((D - d0) < CB ? (D - d0) : CB);
+  const int64_t d = d0 + lane;
+  const bool lane_ok = lane < rows;
+  const int64_t grp = (a.var_B || a.var_C) ? d0 / (D / a.n_groups) : 0;
+  const int n0 = w * kS;
+  const bool has_z = a.z.ptr != nullptr;
+  const float* gu = static_cast<const float*>(a.u.ptr) + b * a.u.s0 + d0 * a.u.s1;
+  const float* gd = static_cast<const float*>(a.delta.ptr) + b * a.delta.s0 + d0 * a.delta.s1;
+  const float* gdA = kDA ? static_cast<const float*>(a.deltaA.ptr) + b * a.deltaA.s0 + d0 * a.deltaA.s1 : nullptr;
+  const float* gz = has_z ? static_cast<const float*>(a.z.ptr) + b * a.z.s0 + d0 * a.z.s1 : nullptr;
+  const float* gB = kVarB ? static_cast<const float*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1 : nullptr;
+  const float* gC = kVarC ? static_cast<const float*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1 : nullptr;
+  float* go = a.out.ptr ? static_cast<float*>(a.out.ptr) + b * a.out.s0 + d0 * a.out.s1 : nullptr;
+  float* goz = a.out_z.ptr ? static_cast<float*>(a.out_z.ptr) + b * a.out_z.s0 + d0 * a.out_z.s1 : nullptr;
+  const float* bias = static_cast<const float*>(a.delta_bias.ptr);
+  const float* Dp = static_cast<const float*>(a.D.ptr);
+
+  cf Av[kS], cout_c[kS], h[kS], pa[kS];
+  {
+    const float* Ap = static_cast<const float*>(a.A.ptr);
+    const float* Bp = static_cast<const float*>(a.B.ptr);
+    const float* Cp = static_cast<const float*>(a.C.ptr);
+#pragma unroll
+    for (int k = 0; k < kS; ++k) {
+      const int n = n0 + k;
+      const bool ok = lane_ok && n < N;
+      Av[k] = ok ? cmk(Ap[2 * (d * a.A.s0 + n * a.A.s1)], Ap[2 * (d * a.A.s0 + n * a.A.s1) + 1]) : cmk(-1.f, 0.f);
+      const cf bc = (!kVarB && ok) ? cmk(Bp[2 * (d * a.B.s0 + n * a.B.s1)], Bp[2 * (d * a.B.s0 + n * a.B.s1) + 1])
+                                   : cmk(1.f, 0.f);
+      const cf cc = (!kVarC && ok) ? cmk(Cp[2 * (d * a.C.s0 + n * a.C.s1)], Cp[2 * (d * a.C.s0 + n * a.C.s1) + 1])
+                                   : cmk(1.f, 0.f);
+      cout_c[k] = ok ? cmul(kVarB ? cmk(1.f, 0.f) : bc, kVarC ? cmk(1.f, 0.f) : cc) : cmk(0.f, 0.f);
+      h[k] = cmk(0.f, 0.f);
+      pa[k] = cmk(1.f, 0.f);
+    }
+  }
+  float sumdt = 0.f;
+  float* ckp = static_cast<float*>(a.ckpt);
+  float* xp = static_cast<float*>(a.x);
+  const int64_t n_xc = (L + kXChunk - 1) / kXChunk;
+
+  for (int64_t t0 = 0; t0 < L; t0 += kTc) {
+    const int nt = (int)((L - t0) < kTc ? (L - t0) : kTc);
+    __syncthreads();
+    load_tile<kTc>(gd + t0, a.delta.s1, rows, nt, s_dl, tid, blockDim.x, [&](float x, int r) {
+      x += bias ? bias[(d0 + r) * a.delta_bias.s0] : 0.f;
+      return a.delta_softplus ? softplus_ref(x) : x;
+    });
+    load_tile<kTc>(gu + t0, a.u.s1, rows, nt, s_u, tid, blockDim.x, [](float x, int) { return x; });
+    if constexpr (kDA) load_tile<kTc>(gdA + t0, a.deltaA.s1, rows, nt, s_dt, tid, blockDim.x, [](float x, int) { return x; });
+    if (has_z) load_tile<kTc>(gz + t0, a.z.s1, rows, nt, s_z, tid, blockDim.x, [](float x, int) { return x; });
+    if constexpr (kVarB) load_bc<kTc>(gB + 2 * t0, a.B.s2, N, NP, nt, s_B, tid, blockDim.x);
+    if constexpr (kVarC) load_bc<kTc>(gC + 2 * t0, a.C.s2, N, NP, nt, s_C, tid, blockDim.x);
+    __syncthreads();
+
+    for (int s = 0; s < nt; ++s) {
+      const float dl = s_dl[s * kPad + lane], uu = s_u[s * kPad + lane];
+      const float dt = kDA ? s_dt[s * kPad + lane] : dl;
+      float y = 0.f;
+#pragma unroll
+      for (int k = 0; k < kS; ++k) {
+        cf Ab, beta;
+        cdisc<kMethod>(dt, dl, Av[k], Ab, beta);
+        cf bin = cmk(uu, 0.f);
+        if constexpr (kVarB) bin = cscale(cmk(s_B[(s * NP + n0 + k) * 2], s_B[(s * NP + n0 + k) * 2 + 1]), uu);
+        h[k] = cfma(Ab, h[k], cmul(beta, bin));
+        if constexpr (kMethod == LRNNX_BILINEAR) pa[k] = cmul(pa[k], Ab);
+        cf cc = cout_c[k];
+        if constexpr (kVarC) cc = cmul(cmk(s_C[(s * NP + n0 + k) * 2], s_C[(s * NP + n0 + k) * 2 + 1]), cc);
+        y += cc.r * h[k].r - cc.i * h[k].i;
+      }
+      if constexpr (kMethod != LRNNX_BILINEAR) sumdt += dt;
+      s_Y[(w * kTc + s) * kPad + lane] = 2.f * y;
+      const int64_t tg = t0 + s;
+      if (ckp != nullptr && ((tg + 1) % kCk) == 0) {
+        const int64_t kk = tg / kCk;
+#pragma unroll
+        for (int k = 0; k < kS; ++k)
+          if (lane_ok && n0 + k < N) {
+            float* p = ckp + (((b * n_ck + kk) * N + n0 + k) * D + d) * 2;
+            p[0] = h[k].r;
+            p[1] = h[k].i;
+          }
+      }
+      if (xp != nullptr && (((tg + 1) % kXChunk) == 0 || tg == L - 1)) {
+        const int64_t c = tg / kXChunk;
+#pragma unroll
+        for (int k = 0; k < kS; ++k)
+          if (lane_ok && n0 + k < N) {
+            cf ac = pa[k];
+            if constexpr (kMethod != LRNNX_BILINEAR) ac = cexp_(cscale(Av[k], sumdt));
+            float* xr = xp + (((b * D + d) * n_xc + c) * 2 * N) * 2;
+            xr[4 * (n0 + k)] = ac.r;
+            xr[4 * (n0 + k) + 1] = ac.i;
+            xr[4 * (n0 + k) + 2] = h[k].r;
+            xr[4 * (n0 + k) + 3] = h[k].i;
+          }
+      }
+    }
+    __syncthreads();
+    for (int j = tid; j < kWave * kTc; j += blockDim.x) {
+      const int r = j / kTc, t = j % kTc;
+      if (r >= rows || t >= nt) continue;
+      float y = 0.f;
+      for (int ww = 0; ww < nW; ++ww) y += s_Y[(ww * kTc + t) * kPad + r];
+      if (Dp) y = fmaf(Dp[(d0 + r) * a.D.s0], s_u[t * kPad + r], y);
+      if (go) go[r * a.out.s1 + t0 + t] = y;
+      if (has_z && goz) {
+        const float zz = s_z[t * kPad + r];
+        goz[r * a.out_z.s1 + t0 + t] = y * zz * sigmoidf_(zz);
+      }
+    }
+  }
+}
+
+struct SSCBwdWs {  // fp32 workspace sections (float offsets)
+  int64_t dBv, dCv, dA, dBc, dCc, dD, dbias, ckpt, total;
+};
+
+inline int64_t al64(int64_t x) { return (x + 63) / 64 * 64; }
+
+inline SSCBwdWs ssc_bwd_ws(const lrnnx_selective_scan_args& a, const SSCGeom& g, bool need_ckpt) {
+  SSCBwdWs w;
+  int64_t o = 0;
+  const int64_t B = a.batch, D = a.dim, N = a.dstate, L = a.seqlen;
+  w.dBv = o; if (a.var_B) o += al64((int64_t)g.n_cb * B * N * 2 * L);
+  w.dCv = o; if (a.var_C) o += al64((int64_t)g.n_cb * B * N * 2 * L);
+  w.dA = o; o += al64(B * D * N * 2);
+  w.dBc = o; if (!a.var_B) o += al64(B * D * N * 2);
+  w.dCc = o; if (!a.var_C) o += al64(B * D * N * 2);
+  w.dD = o; o += al64(B * D);
+  w.dbias = o; o += al64(B * D);
+  w.ckpt = o; if (need_ckpt) o += al64(B * g.n_ck * N * D * 2);
+  w.total = o;
+  return w;
+}
+
+template <int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
+__global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnnx_selective_scan_args a, const int CB,
+                                                       const int64_t n_ck, float* __restrict__ ws, const SSCBwdWs wo,
+                                                       const float* __restrict__ ckp) {
+  constexpr int kCk = ck_c(kS);
+  constexpr int kTc = tile_c(kS);
+  constexpr bool kP3 = kMethod == LRNNX_ZOH || kMethod == LRNNX_BILINEAR;
+  extern __shared__ float smem[];
+  const int nW = blockDim.x / kWave;
+  const int NP = nW * kS;
+  float* s_dl = smem;
+  float* s_u = s_dl + kTc * kPad;
+  float* s_dt = s_u + kTc * kPad;
+  float* s_dy = s_dt + kTc * kPad;
+  float* s_B = s_dy + kTc * kPad;
+  float* s_C = s_B + kTc * NP * 2;
+  float* s_P1 = s_C + kTc * NP * 2;  // [nW][kTc][kPad]
+  float* s_P2 = s_P1 + nW * kTc * kPad;
+  float* s_P3 = s_P2 + nW * kTc * kPad;
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int64_t b = blockIdx.y, D = a.dim, L = a.seqlen;
+  const int N = (int)a.dstate;
+  const int64_t cb = blockIdx.x;
+  const int64_t d0 = cb * CB;
+  const int rows = (int)((D - d0) < CB ? (D - d0) : CB);
+  const int64_t d = d0 + lane;
+  const bool lane_ok = lane < rows;
+  const int64_t grp = (a.var_B || a.var_C) ? d0 / (D / a.n_groups) : 0;
+  const int n0 = w * kS;
+  const bool has_z = a.z.ptr != nullptr;
+  const bool has_dA_in = a.deltaA.ptr != nullptr;
+  const float* gu = static_cast<const float*>(a.u.ptr) + b * a.u.s0 + d0 * a.u.s1;
+  const float* gd = static_cast<const float*>(a.delta.ptr) + b * a.delta.s0 + d0 * a.delta.s1;
+  const float* gdA = kDA ? static_cast<const float*>(a.deltaA.ptr) + b * a.deltaA.s0 + d0 * a.deltaA.s1 : nullptr;
+  const float* gz = has_z ? static_cast<const float*>(a.z.ptr) + b * a.z.s0 + d0 * a.z.s1 : nullptr;
+  const float* gos = has_z ? static_cast<const float*>(a.out_saved.ptr) + b * a.out_saved.s0 + d0 * a.out_saved.s1
+                           : nullptr;
+  const float* gdo = static_cast<const float*>(a.dout.ptr) + b * a.dout.s0 + d0 * a.dout.s1;
+  const float* gB = kVarB ? static_cast<const float*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1 : nullptr;
+  const float* gC = kVarC ? static_cast<const float*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1 : nullptr;
+  float* gdu = static_cast<float*>(a.du.ptr) + b * a.du.s0 + d0 * a.du.s1;
+  float* gddl = static_cast<float*>(a.ddelta.ptr) + b * a.ddelta.s0 + d0 * a.ddelta.s1;
+  float* gddA = has_dA_in ? static_cast<float*>(a.ddeltaA.ptr) + b * a.ddeltaA.s0 + d0 * a.ddeltaA.s1 : nullptr;
+  float* gdz = has_z ? static_cast<float*>(a.dz.ptr) + b * a.dz.s0 + d0 * a.dz.s1 : nullptr;
+  const float* bias = static_cast<const float*>(a.delta_bias.ptr);
+  const float* Dp = static_cast<const float*>(a.D.ptr);
+
+  cf Av[kS], bcst[kS], ccst[kS], cout_c[kS], gn[kS], dA_acc[kS], dBc_acc[kS], dCc_acc[kS];
+  {
+    const float* Ap = static_cast<const float*>(a.A.ptr);
+    const float* Bp = static_cast<const float*>(a.B.ptr);
+    const float* Cp = static_cast<const float*>(a.C.ptr);
+#pragma unroll
+    for (int k = 0; k < kS; ++k) {
+      const int n = n0 + k;
+      const bool ok = lane_ok && n < N;
+      Av[k] = ok ? cmk(Ap[2 * (d * a.A.s0 + n * a.A.s1)], Ap[2 * (d * a.A.s0 + n * a.A.s1) + 1]) : cmk(-1.f, 0.f);
+      bcst[k] = (!kVarB && ok) ? cmk(Bp[2 * (d * a.B.s0 + n * a.B.s1)], Bp[2 * (d * a.B.s0 + n * a.B.s1) + 1])
+                               : cmk(1.f, 0.f);
+      ccst[k] = (!kVarC && ok) ? cmk(Cp[2 * (d * a.C.s0 + n * a.C.s1)], Cp[2 * (d * a.C.s0 + n * a.C.s1) + 1])
+                               : cmk(1.f, 0.f);
+      cout_c[k] = ok ? cmul(kVarB ? cmk(1.f, 0.f) : bcst[k], kVarC ? cmk(1.f, 0.f) : ccst[k]) : cmk(0.f, 0.f);
+      gn[k] = dA_acc[k] = dBc_acc[k] = dCc_acc[k] = cmk(0.f, 0.f);
+    }
+  }
+  float dD_acc = 0.f, dbias_acc = 0.f;
+
+  const int64_t n_tiles = (L + kTc - 1) / kTc;
+  for (int64_t tile = n_tiles - 1; tile >= 0; --tile) {
+    const int64_t t0 = tile * kTc;
+    const int nt = (int)((L - t0) < kTc ? (L - t0) : kTc);
+    __syncthreads();
+    load_tile<kTc>(gd + t0, a.delta.s1, rows, nt, s_dl, tid, blockDim.x, [&](float x, int r) {
+      x += bias ? bias[(d0 + r) * a.delta_bias.s0] : 0.f;
+      return a.delta_softplus ? softplus_ref(x) : x;
+    });
+    load_tile<kTc>(gu + t0, a.u.s1, rows, nt, s_u, tid, blockDim.x, [](float x, int) { return x; });
+    if constexpr (kDA) load_tile<kTc>(gdA + t0, a.deltaA.s1, rows, nt, s_dt, tid, blockDim.x, [](float x, int) { return x; });
+    // dy = dout * silu(z); dz = dout * out * sigma(z) (1 + z (1 - sigma(z))) (selective_scan_backward.cuh:218-219)
+    for (int j = tid; j < kWave * kTc; j += blockDim.x) {
+      const int r = j / kTc, t = j % kTc;
+      float dy = 0.f;
+      if (r < rows && t < nt) {
+        dy = gdo[r * a.dout.s1 + t0 + t];
+        if (has_z) {
+          const float zz = gz[r * a.z.s1 + t0 + t];
+          const float sg = sigmoidf_(zz);
+          gdz[r * a.dz.s1 + t0 + t] = dy * gos[r * a.out_saved.s1 + t0 + t] * sg * (1.f + zz * (1.f - sg));
+          dy *= zz * sg;
+        }
+      }
+      s_dy[t * kPad + r] = dy;
+    }
+    if constexpr (kVarB) load_bc<kTc>(gB + 2 * t0, a.B.s2, N, NP, nt, s_B, tid, blockDim.x);
+    if constexpr (kVarC) load_bc<kTc>(gC + 2 * t0, a.C.s2, N, NP, nt, s_C, tid, blockDim.x);
+    __syncthreads();
+
+    for (int s = (nt + kCk - 1) / kCk - 1; s >= 0; --s) {
+      const int ts = s * kCk;
+      const int Ls = (nt - ts) < kCk ? (nt - ts) : kCk;
+      const int64_t kk = (t0 + ts) / kCk;
+      cf h0[kS];
+#pragma unroll
+      for (int k = 0; k < kS; ++k) {
+        h0[k] = cmk(0.f, 0.f);
+        if (kk > 0 && lane_ok && n0 + k < N) {
+          const float* p = ckp + (((b * n_ck + kk - 1) * N + n0 + k) * D + d) * 2;
+          h0[k] = cmk(p[0], p[1]);
+        }
+      }
+      cf Ab[kCk][kS], H[kCk][kS];
+      {
+        cf hc[kS];
+#pragma unroll
+        for (int k = 0; k < kS; ++k) hc[k] = h0[k];
+#pragma unroll
+        for (int j = 0; j < kCk; ++j) {
+          if (j < Ls) {
+            const int t = ts + j;
+            const float dl = s_dl[t * kPad + lane], uu = s_u[t * kPad + lane];
+            const float dt = kDA ? s_dt[t * kPad + lane] : dl;
+#pragma unroll
+            for (int k = 0; k < kS; ++k) {
+              cf ab, beta;
+              cdisc<kMethod>(dt, dl, Av[k], ab, beta);
+              cf bin = cmk(uu, 0.f);
+              if constexpr (kVarB) bin = cscale(cmk(s_B[(t * NP + n0 + k) * 2], s_B[(t * NP + n0 + k) * 2 + 1]), uu);
+              hc[k] = cfma(ab, hc[k], cmul(beta, bin));
+              Ab[j][k] = ab;
+              H[j][k] = hc[k];
+            }
+          }
+        }
+      }
+      float v[64];  // dB (0..31) and dC (32..63) of this interval: index (k * kCk + j) * 2 + re/im
+#pragma unroll
+      for (int i = 0; i < 64; ++i) v[i] = 0.f;
+#pragma unroll
+      for (int j = kCk - 1; j >= 0; --j) {
+        if (j < Ls) {
+          const int t = ts + j;
+          const float dl = s_dl[t * kPad + lane], uu = s_u[t * kPad + lane];
+          const float dt = kDA ? s_dt[t * kPad + lane] : dl;
+          const float dy = s_dy[t * kPad + lane];
+          float p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+          for (int k = 0; k < kS; ++k) {
+            cf cvar = cmk(1.f, 0.f), cc = cout_c[k], bvar = cmk(1.f, 0.f);
+            if constexpr (kVarC) {
+              cvar = cmk(s_C[(t * NP + n0 + k) * 2], s_C[(t * NP + n0 + k) * 2 + 1]);
+              cc = cmul(cvar, cout_c[k]);
+            }
+            if constexpr (kVarB) bvar = cmk(s_B[(t * NP + n0 + k) * 2], s_B[(t * NP + n0 + k) * 2 + 1]);
+            // dh_t = conj(A_bar_{t+1}) dh_{t+1} + 2 dy conj(C_eff)
+            const cf dh = cadd(gn[k], cscale(cconj(cc), 2.f * dy));
+            const cf ab = Ab[j][k];
+            const cf hp = j > 0 ? H[j - 1][k] : h0[k];
+            const cf hcur = H[j][k];
+            gn[k] = cmul(cconj(ab), dh);
+            // through A_bar
+            if constexpr (kMethod == LRNNX_BILINEAR) {
+              const cf one = cmk(1.f, 0.f);
+              const cf omv = csub(one, cscale(Av[k], 0.5f * dt));
+              const cf inv2 = cdiv(one, cmul(omv, omv));              // dA_bar/dv / 2 = 1/(1-v)^2
+              const cf g = cmul(cconj(hp), dh);                       // dL/dA_bar (conj. Wirtinger)
+              dA_acc[k] = cadd(dA_acc[k], cmul(cconj(cscale(inv2, dt)), g));
+              p2 += cdotr(g, cmul(Av[k], inv2));
+            } else {
+              const cf abhp = cmul(ab, hp);
+              dA_acc[k] = cadd(dA_acc[k], cscale(cmul(cconj(abhp), dh), dt));
+              p2 += cdotr(dh, cmul(Av[k], abhp));
+            }
+            // through the input term beta u B_in
+            if constexpr (kMethod == LRNNX_MAMBA || kMethod == LRNNX_DIRAC) {
+              p1 += cdotr(dh, bvar);  // mamba: du = delta' p1, ddelta' += u p1; dirac: du = p1
+              const cf gB = cscale(dh, kMethod == LRNNX_MAMBA ? dl * uu : uu);
+              v[(k * kCk + j) * 2] = gB.r;
+              v[(k * kCk + j) * 2 + 1] = gB.i;
+            } else if constexpr (kMethod == LRNNX_ZOH) {
+              const cf e1 = cexp_(cscale(Av[k], dl));
+              const cf beta = cdiv(cexpm1_(cscale(Av[k], dl)), Av[k]);
+              const cf bu = cscale(bvar, uu);
+              p1 += cdotr(dh, cmul(beta, bvar));
+              p3 += cdotr(dh, cmul(e1, bu));
+              const cf dbeta_dA = cdiv(csub(cscale(e1, dl), beta), Av[k]);
+              dA_acc[k] = cadd(dA_acc[k], cmul(cconj(cmul(dbeta_dA, bu)), dh));
+              const cf gB = cmul(cconj(cscale(beta, uu)), dh);
+              v[(k * kCk + j) * 2] = gB.r;
+              v[(k * kCk + j) * 2 + 1] = gB.i;
+            } else {  // BILINEAR input side
+              const cf one = cmk(1.f, 0.f);
+              const cf omw = csub(one, cscale(Av[k], 0.5f * dl));
+              const cf inv = cdiv(one, omw);
+              const cf beta = cscale(inv, dl);
+              const cf inv2 = cmul(inv, inv);
+              const cf bu = cscale(bvar, uu);
+              p1 += cdotr(dh, cmul(beta, bvar));
+              p3 += cdotr(dh, cmul(inv2, bu));
+              dA_acc[k] = cadd(dA_acc[k], cmul(cconj(cmul(cscale(inv2, 0.5f * dl * dl), bu)), dh));
+              const cf gB = cmul(cconj(cscale(beta, uu)), dh);
+              v[(k * kCk + j) * 2] = gB.r;
+              v[(k * kCk + j) * 2 + 1] = gB.i;
+            }
+            // output side y = 2 Re(C_eff h): dL/dC_eff = 2 dy conj(h)
+            const cf gCe = cscale(cconj(hcur), 2.f * dy);
+            if constexpr (kVarC) {
+              const cf gC = kVarB ? gCe : cmul(cconj(bcst[k]), gCe);
+              v[32 + (k * kCk + j) * 2] = gC.r;
+              v[32 + (k * kCk + j) * 2 + 1] = gC.i;
+            } else {
+              dCc_acc[k] = cadd(dCc_acc[k], kVarB ? gCe : cmul(cconj(bcst[k]), gCe));
+            }
+            if constexpr (!kVarB) dBc_acc[k] = cadd(dBc_acc[k], cmul(cconj(kVarC ? cvar : ccst[k]), gCe));
+          }
+          s_P1[(w * kTc + t) * kPad + lane] = p1;
+          s_P2[(w * kTc + t) * kPad + lane] = p2;
+          if constexpr (kP3) s_P3[(w * kTc + t) * kPad + lane] = p3;
+        }
+      }
+      if constexpr (kVarB || kVarC) {
+        // lanes past the last channel hold zero operands, so their values are zero
+        const float r = reduce_scatter64(v, lane);
+        const int q = lane >> 5, e = lane & 31;
+        const int kq = (e >> 1) / kCk, jq = (e >> 1) % kCk, c = e & 1;
+        const bool wr = n0 + kq < N && jq < Ls && (q == 0 ? kVarB : kVarC);
+        if (wr) {
+          const int64_t off = ((cb * a.batch + b) * N + n0 + kq) * (2 * L) + 2 * (t0 + ts + jq) + c;
+          ws[(q == 0 ? wo.dBv : wo.dCv) + off] = r;
+        }
+      }
+    }
+    __syncthreads();
+    // epilogue: du, ddelta, ddeltaA; dD / ddelta_bias terms
+    for (int j = tid; j < kWave * kTc; j += blockDim.x) {
+      const int r = j / kTc, t = j % kTc;
+      if (r >= rows || t >= nt) continue;
+      float P1 = 0.f, P2 = 0.f, P3 = 0.f;
+      for (int ww = 0; ww < nW; ++ww) {
+        P1 += s_P1[(ww * kTc + t) * kPad + r];
+        P2 += s_P2[(ww * kTc + t) * kPad + r];
+        if constexpr (kP3) P3 += s_P3[(ww * kTc + t) * kPad + r];
+      }
+      const float dl = s_dl[t * kPad + r], uu = s_u[t * kPad + r], dy = s_dy[t * kPad + r];
+      const float Dv = Dp ? Dp[(d0 + r) * a.D.s0] : 0.f;
+      float du, ddl;
+      if constexpr (kMethod == LRNNX_MAMBA) {
+        du = fmaf(dl, P1, Dv * dy);
+        ddl = uu * P1;
+      } else {
+        du = fmaf(Dv, dy, P1);
+        ddl = P3;
+      }
+      float dda = 0.f;
+      if constexpr (kDA) dda = P2;
+      else ddl += P2;
+      if (a.delta_softplus) {
+        float x = s_dl[t * kPad + r];  // softplus'(x) = sigmoid(x) = 1 - exp(-softplus(x))
+        ddl *= -expm1f(-x);
+      }
+      gdu[r * a.du.s1 + t0 + t] = du;
+      gddl[r * a.ddelta.s1 + t0 + t] = ddl;
+      if (has_dA_in) gddA[r * a.ddeltaA.s1 + t0 + t] = dda;
+      s_P1[t * kPad + r] = dy * uu;  // wave-0 slots: per-element dD / ddelta_bias terms
+      s_P2[t * kPad + r] = ddl;
+    }
+    __syncthreads();
+    if (w == 0 && lane_ok) {
+      for (int t = 0; t < nt; ++t) {
+        dD_acc += s_P1[t * kPad + lane];
+        dbias_acc += s_P2[t * kPad + lane];
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kS; ++k) {
+    if (lane_ok && n0 + k < N) {
+      const int64_t o = ((b * D + d) * N + n0 + k) * 2;
+      ws[wo.dA + o] = dA_acc[k].r;
+      ws[wo.dA + o + 1] = dA_acc[k].i;
+      if constexpr (!kVarB) { ws[wo.dBc + o] = dBc_acc[k].r; ws[wo.dBc + o + 1] = dBc_acc[k].i; }
+      if constexpr (!kVarC) { ws[wo.dCc + o] = dCc_acc[k].r; ws[wo.dCc + o + 1] = dCc_acc[k].i; }
+    }
+  }
+  if (w == 0 && lane_ok) {
+    ws[wo.dD + b * D + d] = dD_acc;
+    ws[wo.dbias + b * D + d] = dbias_acc;
+  }
+}
+
+// sum over channel blocks of the dB / dC partials (.., 2L) real; written with the caller's strides
+template <int kUnused = 0>
+__global__ void __launch_bounds__(256)
+ssc_reduce_bc_kernel(const float* __restrict__ part, lrnnx_view out, int64_t B, int64_t G, int64_t N, int64_t L2,
+                     int64_t ncpg) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = blockIdx.y;
+  if (t >= L2) return;
+  const int64_t n = row % N, g = (row / N) % G, b = row / (N * G);
+  float acc = 0.f;
+  for (int64_t j = 0; j < ncpg; ++j) acc += part[(((g * ncpg + j) * B + b) * N + n) * L2 + t];
+  static_cast<float*>(out.ptr)[b * out.s0 + g * out.s1 + n * out.s2 + t] = acc;
+}
+
+// out[d, n] (complex, strides in complex elements) = sum_b part[b, d, n]
+template <int kUnused = 0>
+__global__ void __launch_bounds__(256)
+ssc_reduce_batch_c_kernel(const float* __restrict__ part, lrnnx_view out, int64_t B, int64_t D, int64_t N) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= D * N) return;
+  float re = 0.f, im = 0.f;
+  for (int64_t b = 0; b < B; ++b) {
+    re += part[(b * D * N + i) * 2];
+    im += part[(b * D * N + i) * 2 + 1];
+  }
+  const int64_t d = i / N, n = i % N;
+  float* o = static_cast<float*>(out.ptr) + 2 * (d * out.s0 + n * out.s1);
+  o[0] = re;
+  o[1] = im;
+}
+
+template <int kUnused = 0>
+__global__ void __launch_bounds__(256)
+ssc_reduce_batch_r_kernel(const float* __restrict__ part, lrnnx_view out, int64_t B, int64_t D) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= D) return;
+  float acc = 0.f;
+  for (int64_t b = 0; b < B; ++b) acc += part[b * D + i];
+  static_cast<float*>(out.ptr)[i * out.s0] = acc;
+}
+
+inline size_t ssc_fwd_smem(int nW, int kS) {
+  const int NP = nW * kS, kTc = tile_c(kS);
+  return sizeof(float) * ((size_t)4 * kTc * kPad + (size_t)2 * kTc * NP * 2 + (size_t)nW * kTc * kPad);
+}
+inline size_t ssc_bwd_smem(int nW, int kS) {
+  const int NP = nW * kS, kTc = tile_c(kS);
+  return sizeof(float) * ((size_t)4 * kTc * kPad + (size_t)2 * kTc * NP * 2 + (size_t)3 * nW * kTc * kPad);
+}
+
+template <int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
+hipError_t ssc_fwd_t(const lrnnx_selective_scan_args& a, const SSCGeom& g, hipStream_t st) {
+  const size_t sm = ssc_fwd_smem(g.nW, kS);
+  if (sm > kMaxLds) return hipErrorInvalidConfiguration;
+  auto fn = ssc_fwd_kernel<kS, kMethod, kVarB, kVarC, kDA>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)sm);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(fn, dim3(g.n_cb, (unsigned)a.batch), dim3(g.nW * kWave), sm, st, a, g.CB, g.n_ck);
+  return hipGetLastError();
+}
+
+template <int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
+hipError_t ssc_bwd_t(const lrnnx_selective_scan_args& a, const SSCGeom& g, float* ws, const SSCBwdWs& wo,
+                     const float* ckp, hipStream_t st) {
+  const size_t sm = ssc_bwd_smem(g.nW, kS);
+  if (sm > kMaxLds) return hipErrorInvalidConfiguration;
+  auto fn = ssc_bwd_kernel<kS, kMethod, kVarB, kVarC, kDA>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)sm);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(fn, dim3(g.n_cb, (unsigned)a.batch), dim3(g.nW * kWave), sm, st, a, g.CB, g.n_ck, ws, wo, ckp);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t B = a.batch, D = a.dim, N = a.dstate, L = a.seqlen, G = a.n_groups;
+  if constexpr (kVarB || kVarC) {
+    const int64_t ncpg = g.n_cb / G;
+    dim3 rg((unsigned)((2 * L + 255) / 256), (unsigned)(B * G * N));
+    if constexpr (kVarB)
+      hipLaunchKernelGGL(ssc_reduce_bc_kernel<0>, rg, dim3(256), 0, st, ws + wo.dBv, a.dB, B, G, N, 2 * L, ncpg);
+    if constexpr (kVarC)
+      hipLaunchKernelGGL(ssc_reduce_bc_kernel<0>, rg, dim3(256), 0, st, ws + wo.dCv, a.dC, B, G, N, 2 * L, ncpg);
+  }
+  const unsigned gdn = (unsigned)((D * N + 255) / 256), gd = (unsigned)((D + 255) / 256);
+  hipLaunchKernelGGL(ssc_reduce_batch_c_kernel<0>, dim3(gdn), dim3(256), 0, st, ws + wo.dA, a.dA, B, D, N);
+  if constexpr (!kVarB)
+    hipLaunchKernelGGL(ssc_reduce_batch_c_kernel<0>, dim3(gdn), dim3(256), 0, st, ws + wo.dBc, a.dB, B, D, N);
+  if constexpr (!kVarC)
+    hipLaunchKernelGGL(ssc_reduce_batch_c_kernel<0>, dim3(gdn), dim3(256), 0, st, ws + wo.dCc, a.dC, B, D, N);
+  if (a.dD.ptr) hipLaunchKernelGGL(ssc_reduce_batch_r_kernel<0>, dim3(gd), dim3(256), 0, st, ws + wo.dD, a.dD, B, D);
+  if (a.ddelta_bias.ptr)
+    hipLaunchKernelGGL(ssc_reduce_batch_r_kernel<0>, dim3(gd), dim3(256), 0, st, ws + wo.dbias, a.ddelta_bias, B, D);
+  return hipGetLastError();
+}
+
+// dispatch on (method, var B/C, deltaA) for one kS
+template <int kS, bool kBwd>
+hipError_t ssc_dispatch_m(const lrnnx_selective_scan_args& a, const SSCGeom& g, float* ws, const SSCBwdWs* wo,
+                          const float* ckp, hipStream_t st) {
+  auto go = [&](auto m, auto vb, auto vc, auto da) -> hipError_t {
+    constexpr int M = decltype(m)::value;
+    constexpr bool VB = decltype(vb)::value, VC = decltype(vc)::value, DA = decltype(da)::value;
+    if constexpr (kBwd) return ssc_bwd_t<kS, M, VB, VC, DA>(a, g, ws, *wo, ckp, st);
+    else return ssc_fwd_t<kS, M, VB, VC, DA>(a, g, st);
+  };
+  auto with_bc = [&](auto m, auto da) -> hipError_t {
+    using T = std::true_type;
+    using F = std::false_type;
+    if (a.var_B && a.var_C) return go(m, T{}, T{}, da);
+    if (a.var_B) return go(m, T{}, F{}, da);
+    if (a.var_C) return go(m, F{}, T{}, da);
+    return go(m, F{}, F{}, da);
+  };
+  auto with_da = [&](auto m) -> hipError_t {
+    if (a.deltaA.ptr) return with_bc(m, std::true_type{});
+    return with_bc(m, std::false_type{});
+  };
+  switch (a.method) {
+    case LRNNX_ZOH: return with_da(std::integral_constant<int, LRNNX_ZOH>{});
+    case LRNNX_BILINEAR: return with_da(std::integral_constant<int, LRNNX_BILINEAR>{});
+    case LRNNX_DIRAC: return with_da(std::integral_constant<int, LRNNX_DIRAC>{});
+    case LRNNX_MAMBA: return with_da(std::integral_constant<int, LRNNX_MAMBA>{});
+  }
+  return hipErrorInvalidValue;
+}
+
+template <bool kBwd>
+hipError_t ssc_dispatch(const lrnnx_selective_scan_args& a, const SSCGeom& g, float* ws, const SSCBwdWs* wo,
+                        const float* ckp, hipStream_t st) {
+  switch (g.kS) {
+    case 1: return ssc_dispatch_m<1, kBwd>(a, g, ws, wo, ckp, st);
+    case 4: return ssc_dispatch_m<4, kBwd>(a, g, ws, wo, ckp, st);
+    case 8: return ssc_dispatch_m<8, kBwd>(a, g, ws, wo, ckp, st);
+    case 16: return ssc_dispatch_m<16, kBwd>(a, g, ws, wo, ckp, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ssc
+}  // namespace lrnnx

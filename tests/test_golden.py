@@ -75,8 +75,6 @@ def test_kernel_matches_selective_fixture(dev, path):
     from lrnnx_amd import selective_scan_fn
 
     rec = _load(path)
-    if rec["inputs"]["A"].is_complex():
-        pytest.skip("complex-weight selective scan: checked in test_selective_complex_gpu.py")
     i = {k: _f32(v, dev).requires_grad_(True) for k, v in rec["inputs"].items()}
     out, last = selective_scan_fn(i["u"], i["delta"], i["A"], i["B"], i["C"], i["D"], i["z"], i["delta_bias"],
                                   i.get("deltaA"), True, True, rec["meta"]["method"])
