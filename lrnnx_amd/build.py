@@ -45,13 +45,26 @@ def _sources():
     return sorted(CSRC.glob("*.hip"))
 
 
-def _headers():
-    return sorted(CSRC.glob("*.h")) + sorted((ROOT / "include").glob("*.h"))
+def _deps(src: Path) -> set[Path]:
+    """Files `src` includes with #include "...", followed recursively."""
+    seen: set[Path] = set()
+    todo = [src]
+    while todo:
+        f = todo.pop()
+        for line in f.read_text().splitlines():
+            line = line.strip()
+            if not line.startswith("#include") or '"' not in line:
+                continue
+            dep = (f.parent / line.split('"')[1]).resolve()
+            if dep.exists() and dep not in seen:
+                seen.add(dep)
+                todo.append(dep)
+    return seen
 
 
 def _compile(src: Path, force: bool) -> tuple[Path, float, str]:
     obj = BUILD / (src.stem + ".o")
-    newest_dep = max([src.stat().st_mtime] + [h.stat().st_mtime for h in _headers()])
+    newest_dep = max([src.stat().st_mtime] + [h.stat().st_mtime for h in _deps(src)])
     if not force and obj.exists() and obj.stat().st_mtime >= newest_dep:
         return obj, 0.0, ""
     t = time.time()

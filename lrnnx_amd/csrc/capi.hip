@@ -7,6 +7,7 @@
 // returns 1 and leaves the message in lrnnx_last_error().
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "ss_common.h"
@@ -15,6 +16,9 @@ namespace lrnnx {
 hipError_t ss_fwd_mamba_f32(const lrnnx_selective_scan_args&, hipStream_t);
 hipError_t ss_fwd_mamba_bf16(const lrnnx_selective_scan_args&, hipStream_t);
 hipError_t ss_fwd_mamba_f16(const lrnnx_selective_scan_args&, hipStream_t);
+bool ssf_fwd_f32(const lrnnx_selective_scan_args&, hipStream_t, hipError_t*);
+bool ssf_fwd_bf16(const lrnnx_selective_scan_args&, hipStream_t, hipError_t*);
+bool ssf_fwd_f16(const lrnnx_selective_scan_args&, hipStream_t, hipError_t*);
 hipError_t ss_fwd_other_f32(const lrnnx_selective_scan_args&, hipStream_t);
 hipError_t ss_bwd_mamba_f32(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
 hipError_t ss_bwd_mamba_bf16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
@@ -65,6 +69,30 @@ const char* method_name(int m) {
     case LRNNX_RGLRU: return "rglru";
   }
   return "?";
+}
+
+// LRNNX_SCAN_GENERIC=1 in the environment routes every call to the generic
+// kernels (for A/B timing and cross-checks of the fast paths).
+bool fast_paths_enabled() {
+  const char* v = getenv("LRNNX_SCAN_GENERIC");
+  return !(v && v[0] && v[0] != '0');
+}
+
+// Forward of the "mamba" method: fast path when it covers the call, else the
+// generic kernel.
+hipError_t fwd_mamba(const lrnnx_selective_scan_args& a, hipStream_t st) {
+  hipError_t e = hipSuccess;
+  if (fast_paths_enabled()) {
+    const bool done = a.itype == LRNNX_F32    ? ssf_fwd_f32(a, st, &e)
+                      : a.itype == LRNNX_BF16 ? ssf_fwd_bf16(a, st, &e)
+                                              : ssf_fwd_f16(a, st, &e);
+    if (done) return e;
+  }
+  switch (a.itype) {
+    case LRNNX_F32: return ss_fwd_mamba_f32(a, st);
+    case LRNNX_BF16: return ss_fwd_mamba_bf16(a, st);
+    default: return ss_fwd_mamba_f16(a, st);
+  }
 }
 
 int check_ss(const lrnnx_selective_scan_args* a, bool bwd) {
@@ -128,11 +156,7 @@ int lrnnx_selective_scan_fwd(const lrnnx_selective_scan_args* a, void* stream) {
   if (a->wtype == LRNNX_C64) return from_hip(ssc_fwd_launch(*a, st), "selective_scan_fwd (complex)");
   hipError_t e;
   if (a->method == LRNNX_MAMBA) {
-    switch (a->itype) {
-      case LRNNX_F32: e = ss_fwd_mamba_f32(*a, st); break;
-      case LRNNX_BF16: e = ss_fwd_mamba_bf16(*a, st); break;
-      default: e = ss_fwd_mamba_f16(*a, st); break;
-    }
+    e = fwd_mamba(*a, st);
   } else {
     e = ss_fwd_other_f32(*a, st);
   }
@@ -158,10 +182,7 @@ int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args* a, void* stream) {
     f.z.ptr = nullptr;
     f.x = nullptr;
     f.ckpt = reinterpret_cast<char*>(a->workspace) + ss_bwd_ckpt_offset_bytes(*a);
-    hipError_t e = a->method == LRNNX_MAMBA
-                       ? (a->itype == LRNNX_F32 ? ss_fwd_mamba_f32(f, st)
-                          : a->itype == LRNNX_BF16 ? ss_fwd_mamba_bf16(f, st) : ss_fwd_mamba_f16(f, st))
-                       : ss_fwd_other_f32(f, st);
+    hipError_t e = a->method == LRNNX_MAMBA ? fwd_mamba(f, st) : ss_fwd_other_f32(f, st);
     if (from_hip(e, "selective_scan_bwd (checkpoint rebuild)")) return 1;
     ckp = static_cast<const float*>(f.ckpt);
   }

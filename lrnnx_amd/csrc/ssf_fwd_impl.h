@@ -1,0 +1,314 @@
+// Selective scan forward, fast path of the headline case (gfx950).
+//
+// Covers: method "mamba", variable B and C of any group count, no deltaA,
+// 8 < d_state <= 16, real fp32 A, f32 / bf16 / f16 I/O, d_model a multiple
+// of 64 per group, L a multiple of the tile length, 16-byte aligned rows
+// (ssf_fwd_eligible).  Everything else runs the generic kernel of
+// ss_fwd_impl.h.  Semantics are those of the reference kernel
+// csrc/selective_scan/selective_scan.cuh:73-382 (delta' = softplus(delta +
+// bias) with threshold 20, h_t = exp(delta' A) h_{t-1} + delta' B_t u_t,
+// y = sum_n C_t h_t + D u, out_z = y silu(z), chunk carries every 2048 steps).
+//
+// Decomposition: one workgroup = one batch row and 64 channels; 4 waves, wave
+// w owns states 4w..4w+3 of every channel (lane = channel) with their fp32 h
+// in VGPRs.  L is walked in tiles of kT steps (64 bytes of every input row).
+// Per tile k:
+//   compute(k)  issue the LDS-DMA fetch of raw tile k+1 (u, delta, z, B, C),
+//               then run the kT steps of the recurrence for the wave's states
+//               and write the wave's partial y (sum over its states of C h).
+//   finish(k)   wait + barrier; epilogue of tile k: y = partials of the 4
+//               waves + D u (a fifth partial written by the conversion),
+//               out / out_z as 16-byte stores; conversion of raw tile k+1 into
+//               the fp32 operands delta', delta' u, D u and B, C rows.
+// The per-element work of both phases is done by a fixed thread -> (channel,
+// 16-byte block) map, so a thread rewrites its own D u slot right after the
+// epilogue has read it.  The chunk carries x need the sum of delta' over a
+// 2048-step chunk; each thread accumulates the sum of its own block across
+// the tiles of a chunk and the four block sums of a channel are added when
+// the chunk ends.
+#pragma once
+#include <type_traits>
+
+#include "ss_common.h"
+#include "tile_io.h"
+
+namespace lrnnx {
+
+namespace ssf {
+
+constexpr int kNW = 4;             // waves per workgroup
+constexpr int kS = 4;              // states per wave
+constexpr int kNT = kNW * kWave;   // threads per workgroup
+constexpr int kCk = 16;            // checkpoint interval (same layout as ss_fwd_kernel with kS = 4)
+
+template <typename IT>
+__host__ __device__ constexpr int tile_steps() { return (int)(64 / sizeof(IT)); }  // 64-byte rows
+
+// softplus with the reference's threshold 20; log1p by a 4-term series below 1/32
+__device__ __forceinline__ float softplus20_fast(float x) {
+  const float e = __builtin_amdgcn_exp2f(x * kLog2e);
+  const float small = e * fmaf(e, fmaf(e, fmaf(e, -0.25f, 0.33333334f), -0.5f), 1.f);
+  const float big = __builtin_amdgcn_logf(1.f + e) * kLn2;
+  const float r = e < 0.03125f ? small : big;
+  return x > 20.f ? x : r;
+}
+
+__device__ __forceinline__ float sigmoidf_fast(float z) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-z * kLog2e));
+}
+
+}  // namespace ssf
+
+template <typename IT, bool kSP, bool kZ>
+__global__ void __launch_bounds__(ssf::kNT)
+ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
+  using namespace ssf;
+  constexpr int kT = tile_steps<IT>();   // steps per tile
+  constexpr int kE = 16 / sizeof(IT);    // elements per 16-byte block
+  constexpr int kQ = kT / kE;            // blocks per row (= 4)
+  constexpr int kG = kT / 4;             // groups of 4 steps
+  static_assert(kQ * kWave == kNT, "one 16-byte block per thread and tile");
+  static_assert(kCk % kT == 0 || kT % kCk == 0, "checkpoint interval vs tile");
+  constexpr int kRaw = kWave * kT * (int)sizeof(IT);   // [64][kT] raw tile, bytes
+  constexpr int kRawS = 16 * kT * (int)sizeof(IT);     // [16][kT] raw B or C tile
+
+  __shared__ __attribute__((aligned(16))) char s_raw_u[kRaw];
+  __shared__ __attribute__((aligned(16))) char s_raw_d[kRaw];
+  __shared__ __attribute__((aligned(16))) char s_raw_z[kZ ? 2 * kRaw : 16];
+  __shared__ __attribute__((aligned(16))) char s_raw_b[kRawS];
+  __shared__ __attribute__((aligned(16))) char s_raw_c[kRawS];
+  __shared__ __attribute__((aligned(16))) float s_dl[kG * kWave * 4];       // [g][lane][4] delta'
+  __shared__ __attribute__((aligned(16))) float s_x[kG * kWave * 4];        // [g][lane][4] delta' u
+  __shared__ __attribute__((aligned(16))) float s_B[16 * kT];               // [n][t]
+  __shared__ __attribute__((aligned(16))) float s_C[16 * kT];
+  __shared__ __attribute__((aligned(16))) float s_Y[(kNW + 1) * kG * kWave * 4];  // [w][g][lane][4]; w = 4: D u
+  __shared__ __attribute__((aligned(16))) float s_dsum[kNT];                // [lane][q] chunk sums of delta'
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t b = blockIdx.y;
+  const int64_t D = a.dim, L = a.seqlen;
+  const int N = (int)a.dstate;
+  const int64_t d0 = (int64_t)blockIdx.x * kWave;
+  const int64_t grp = d0 / (D / a.n_groups);
+  const int n0 = w * kS;
+
+  // thread -> (row r, block q) of the per-element phases
+  const int er = tid / kQ, eq = tid % kQ;
+
+  const IT* gu = static_cast<const IT*>(a.u.ptr) + b * a.u.s0 + d0 * a.u.s1;
+  const IT* gd = static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d0 * a.delta.s1;
+  const IT* gz = kZ ? static_cast<const IT*>(a.z.ptr) + b * a.z.s0 + d0 * a.z.s1 : nullptr;
+  const IT* gB = static_cast<const IT*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1;
+  const IT* gC = static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1;
+  IT* go = a.out.ptr ? static_cast<IT*>(a.out.ptr) + b * a.out.s0 + (d0 + er) * a.out.s1 + eq * kE : nullptr;
+  IT* goz = kZ ? static_cast<IT*>(a.out_z.ptr) + b * a.out_z.s0 + (d0 + er) * a.out_z.s1 + eq * kE : nullptr;
+  const uint32_t su = (uint32_t)a.u.s1, sd = (uint32_t)a.delta.s1, sz = (uint32_t)a.z.s1;
+  const uint32_t sBn = (uint32_t)a.B.s2, sCn = (uint32_t)a.C.s2;
+  float* ckp = static_cast<float*>(a.ckpt);
+  float* xp = static_cast<float*>(a.x);
+
+  // per-lane constants of the recurrence (channel d0 + lane, states n0..n0+3)
+  float a2[kS], h[kS];
+#pragma unroll
+  for (int k = 0; k < kS; ++k) {
+    const int n = n0 + k;
+    const float Av = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + lane) * a.A.s0 + n * a.A.s1] : -1.f;
+    a2[k] = Av * kLog2e;
+    h[k] = 0.f;
+  }
+  // per-thread constants of the per-element phases (channel d0 + er)
+  const float e_bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[(d0 + er) * a.delta_bias.s0] : 0.f;
+  const float e_D = a.D.ptr ? static_cast<const float*>(a.D.ptr)[(d0 + er) * a.D.s0] : 0.f;
+  float e_dsum = 0.f;  // sum of this thread's delta' over the current 2048-step chunk
+
+  const int64_t n_tiles = L / kT;
+  const int64_t n_xc = (L + kXChunk - 1) / kXChunk;
+
+  auto fetch = [&](int64_t tile) __attribute__((always_inline)) {
+    const int64_t t0 = tile * kT;
+    tile_fetch_async<IT, kQ>(gu + t0, su, kWave, s_raw_u, w, kNW, lane);
+    tile_fetch_async<IT, kQ>(gd + t0, sd, kWave, s_raw_d, w, kNW, lane);
+    if constexpr (kZ) tile_fetch_async<IT, kQ>(gz + t0, sz, kWave, s_raw_z + (tile & 1) * kRaw, w, kNW, lane);
+    // B on wave 0, C on wave 1 (N * kQ <= 64 blocks each: one instruction)
+    if (w == 0) tile_fetch_async<IT, kQ>(gB + t0, sBn, N, s_raw_b, 0, 1, lane);
+    if (w == 1) tile_fetch_async<IT, kQ>(gC + t0, sCn, N, s_raw_c, 0, 1, lane);
+  };
+
+  // raw tile -> fp32 operands; thread tid owns row er, steps eq*kE .. +kE
+  auto convert = [&]() __attribute__((always_inline)) {
+    float vu[kE], vd[kE];
+    raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_u + 16 * tid), vu);
+    raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_d + 16 * tid), vd);
+    float dsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < kE; ++i) {
+      const float x = vd[i] + e_bias;
+      const float dl = kSP ? softplus20_fast(x) : x;
+      dsum += dl;
+      vd[i] = dl;
+    }
+    e_dsum += dsum;
+#pragma unroll
+    for (int i = 0; i < kE; i += 4) {
+      const int o = (((eq * kE + i) >> 2) * kWave + er) * 4;
+      *reinterpret_cast<float4*>(s_dl + o) = make_float4(vd[i], vd[i + 1], vd[i + 2], vd[i + 3]);
+      *reinterpret_cast<float4*>(s_x + o) =
+          make_float4(vd[i] * vu[i], vd[i + 1] * vu[i + 1], vd[i + 2] * vu[i + 2], vd[i + 3] * vu[i + 3]);
+      *reinterpret_cast<float4*>(s_Y + kNW * kG * kWave * 4 + o) =
+          make_float4(e_D * vu[i], e_D * vu[i + 1], e_D * vu[i + 2], e_D * vu[i + 3]);
+    }
+    // B / C rows: threads [0, 64) convert B, [64, 128) C; rows >= N are zero
+    if (tid < 2 * 16 * kQ) {
+      const bool isC = tid >= 16 * kQ;
+      const int j = isC ? tid - 16 * kQ : tid;
+      const int n = j / kQ;
+      float v[kE];
+      raw_to_f32<IT>(*reinterpret_cast<const uint4*>((isC ? s_raw_c : s_raw_b) + 16 * j), v);
+      float* dst = (isC ? s_C : s_B) + j * kE;
+#pragma unroll
+      for (int i = 0; i < kE; i += 4)
+        *reinterpret_cast<float4*>(dst + i) = n < N ? make_float4(v[i], v[i + 1], v[i + 2], v[i + 3])
+                                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+
+  auto epilogue = [&](int64_t tile) __attribute__((always_inline)) {
+    float y[kE];
+#pragma unroll
+    for (int i = 0; i < kE; i += 4) {
+      const int o = (((eq * kE + i) >> 2) * kWave + er) * 4;
+      float4 acc = *reinterpret_cast<const float4*>(s_Y + kNW * kG * kWave * 4 + o);
+#pragma unroll
+      for (int ww = 0; ww < kNW; ++ww) {
+        const float4 p = *reinterpret_cast<const float4*>(s_Y + ww * kG * kWave * 4 + o);
+        acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
+      }
+      y[i] = acc.x; y[i + 1] = acc.y; y[i + 2] = acc.z; y[i + 3] = acc.w;
+    }
+    const int64_t t0 = tile * kT;
+    if (go) *reinterpret_cast<uint4*>(go + t0) = f32_to_raw<IT>(y);
+    if constexpr (kZ) {
+      float vz[kE];
+      raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_z + (tile & 1) * kRaw + 16 * tid), vz);
+#pragma unroll
+      for (int i = 0; i < kE; ++i) y[i] *= vz[i] * sigmoidf_fast(vz[i]);
+      *reinterpret_cast<uint4*>(goz + t0) = f32_to_raw<IT>(y);
+    }
+  };
+
+  // chunk carry after the last step of `tile`: (exp(A sum delta'), h) per state
+  auto store_x = [&](int64_t tile) __attribute__((always_inline)) {
+    const float4 s4 = *reinterpret_cast<const float4*>(s_dsum + lane * 4);
+    const float S = (s4.x + s4.y) + (s4.z + s4.w);
+    const int64_t c = (tile * kT) / kXChunk;
+    float* xr = xp + ((b * D + d0 + lane) * n_xc + c) * 2 * N;
+#pragma unroll
+    for (int k = 0; k < kS; ++k) {
+      if (n0 + k < N) {
+        xr[2 * (n0 + k)] = __builtin_amdgcn_exp2f(a2[k] * S);
+        xr[2 * (n0 + k) + 1] = h[k];
+      }
+    }
+  };
+  auto chunk_end = [&](int64_t tile) __attribute__((always_inline)) {
+    return ((tile + 1) * kT) % kXChunk == 0 || tile + 1 == n_tiles;
+  };
+
+  // ---- prologue: tile 0
+  fetch(0);
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  __syncthreads();
+  convert();
+  __syncthreads();
+
+  float* sYw = s_Y + w * kG * kWave * 4;
+  for (int64_t tile = 0; tile < n_tiles; ++tile) {
+    if (tile + 1 < n_tiles) fetch(tile + 1);
+    if (tile > 0 && xp && chunk_end(tile - 1)) store_x(tile - 1);
+
+    // ---- compute(tile)
+    const int64_t t0 = tile * kT;
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      const float4 dl4 = *reinterpret_cast<const float4*>(s_dl + (g * kWave + lane) * 4);
+      const float4 x4 = *reinterpret_cast<const float4*>(s_x + (g * kWave + lane) * 4);
+      float4 b4[kS], c4[kS];
+#pragma unroll
+      for (int k = 0; k < kS; ++k) {
+        b4[k] = *reinterpret_cast<const float4*>(s_B + (n0 + k) * kT + 4 * g);
+        c4[k] = *reinterpret_cast<const float4*>(s_C + (n0 + k) * kT + 4 * g);
+      }
+      const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+      const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+      float y[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < kS; ++k) {
+          const float ab = __builtin_amdgcn_exp2f(dlv[i] * a2[k]);
+          h[k] = fmaf(ab, h[k], xv[i] * (&b4[k].x)[i]);
+          acc = fmaf((&c4[k].x)[i], h[k], acc);
+        }
+        y[i] = acc;
+      }
+      *reinterpret_cast<float4*>(sYw + (g * kWave + lane) * 4) = make_float4(y[0], y[1], y[2], y[3]);
+      if (ckp != nullptr && ((4 * g + 4) % kCk) == 0) {
+        const int64_t kk = (t0 + 4 * g + 4) / kCk - 1;
+        float* cp = ckp + ((b * n_ck + kk) * N + n0) * D + d0 + lane;
+#pragma unroll
+        for (int k = 0; k < kS; ++k)
+          if (n0 + k < N) cp[(int64_t)k * D] = h[k];
+      }
+    }
+
+    // ---- finish(tile)
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    epilogue(tile);
+    if (chunk_end(tile)) {
+      s_dsum[tid] = e_dsum;
+      e_dsum = 0.f;
+    }
+    if (tile + 1 < n_tiles) convert();
+    __syncthreads();
+  }
+  if (xp) store_x(n_tiles - 1);
+}
+
+// Whether the fast path covers this call (see the header comment).
+template <typename IT>
+inline bool ssf_fwd_eligible(const lrnnx_selective_scan_args& a) {
+  constexpr int kT = ssf::tile_steps<IT>();
+  if (a.method != LRNNX_MAMBA || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C || a.deltaA.ptr) return false;
+  if (a.dstate <= 8 || a.dstate > 16 || a.seqlen % kT != 0 || a.seqlen <= 0) return false;
+  if (a.n_groups <= 0 || a.dim % a.n_groups != 0 || (a.dim / a.n_groups) % kWave != 0) return false;
+  if ((a.z.ptr != nullptr) != (a.out_z.ptr != nullptr)) return false;
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  auto rows_ok = [&](const lrnnx_view& v, bool four_d) {
+    if (v.ptr == nullptr) return true;
+    const int64_t s = sizeof(IT);
+    return al(v.ptr) && (v.s0 * s) % 16 == 0 && (v.s1 * s) % 16 == 0 && (!four_d || (v.s2 * s) % 16 == 0);
+  };
+  return rows_ok(a.u, false) && rows_ok(a.delta, false) && rows_ok(a.z, false) && rows_ok(a.B, true) &&
+         rows_ok(a.C, true) && rows_ok(a.out, false) && rows_ok(a.out_z, false);
+}
+
+template <typename IT>
+inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_ck, hipStream_t st) {
+  dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch);
+  dim3 block(ssf::kNT);
+  const bool z = a.z.ptr != nullptr;
+  if (a.delta_softplus) {
+    if (z) hipLaunchKernelGGL((ssf_fwd_kernel<IT, true, true>), grid, block, 0, st, a, n_ck);
+    else hipLaunchKernelGGL((ssf_fwd_kernel<IT, true, false>), grid, block, 0, st, a, n_ck);
+  } else {
+    if (z) hipLaunchKernelGGL((ssf_fwd_kernel<IT, false, true>), grid, block, 0, st, a, n_ck);
+    else hipLaunchKernelGGL((ssf_fwd_kernel<IT, false, false>), grid, block, 0, st, a, n_ck);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace lrnnx

@@ -123,3 +123,39 @@ def test_mamba_bf16_cfg2_slice(dev):
 def test_mamba_fp32_long_chunks(dev):
     # crosses the 2048-step chunk of the reference x carries
     _run(dev, 1, 64, 4100, 16, seed=5)
+
+
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+def test_mamba_fast_path_long_chunks(dev, itype):
+    # L a multiple of the fast path's tile: the fast kernels run, and the
+    # 2048-step chunk carries (last_state) cross two chunk ends
+    _run(dev, 1, 64, 4160, 16, itype=itype, seed=6)
+
+
+@pytest.mark.parametrize("N", [12, 16])
+def test_mamba_fast_path_dstate(dev, N):
+    _run(dev, 2, 64, 96, N, itype=torch.bfloat16, seed=7)
+
+
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+def test_fast_path_matches_generic(dev, itype, monkeypatch):
+    """The fast kernels and the generic kernels (LRNNX_SCAN_GENERIC=1) agree on
+    the same inputs (both fp32 state; only the order of the final sums differs)."""
+    inp = R.make_selective_inputs(2, 128, 512, 16, seed=8, itype=itype, groups=2)
+    g = torch.Generator().manual_seed(9)
+    dout = torch.randn(2, 128, 512, generator=g).to(itype).to(dev)
+    d = to_dev(inp, dev)
+    res = []
+    for generic in ("0", "1"):
+        monkeypatch.setenv("LRNNX_SCAN_GENERIC", generic)
+        leaves = {k: d[k].clone().requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D", "z",
+                                                                 "delta_bias")}
+        out, last = selective_scan_fn(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"],
+                                      leaves["D"], leaves["z"], leaves["delta_bias"], None, True, True, "mamba")
+        out.backward(dout)
+        torch.cuda.synchronize()
+        res.append([out.detach().float(), last.detach()] + [leaves[k].grad.float() for k in leaves])
+    names = ["out", "last_state"] + ["d" + k for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")]
+    rt = 1e-5 if itype == torch.float32 else 1e-2
+    for n, a, b in zip(names, res[0], res[1]):
+        close(n, a, b.cpu().double(), rt, rt)
