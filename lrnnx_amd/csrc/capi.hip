@@ -19,6 +19,9 @@ hipError_t ss_fwd_mamba_f16(const lrnnx_selective_scan_args&, hipStream_t);
 bool ssf_fwd_f32(const lrnnx_selective_scan_args&, hipStream_t, hipError_t*);
 bool ssf_fwd_bf16(const lrnnx_selective_scan_args&, hipStream_t, hipError_t*);
 bool ssf_fwd_f16(const lrnnx_selective_scan_args&, hipStream_t, hipError_t*);
+bool ssf_bwd_f32(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t, hipError_t*);
+bool ssf_bwd_bf16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t, hipError_t*);
+bool ssf_bwd_f16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t, hipError_t*);
 hipError_t ss_fwd_other_f32(const lrnnx_selective_scan_args&, hipStream_t);
 hipError_t ss_bwd_mamba_f32(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
 hipError_t ss_bwd_mamba_bf16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
@@ -92,6 +95,23 @@ hipError_t fwd_mamba(const lrnnx_selective_scan_args& a, hipStream_t st) {
     case LRNNX_F32: return ss_fwd_mamba_f32(a, st);
     case LRNNX_BF16: return ss_fwd_mamba_bf16(a, st);
     default: return ss_fwd_mamba_f16(a, st);
+  }
+}
+
+// Backward of the "mamba" method: fast path when it covers the call, else the
+// generic kernel.
+hipError_t bwd_mamba(const lrnnx_selective_scan_args& a, float* ws, const float* ckp, hipStream_t st) {
+  hipError_t e = hipSuccess;
+  if (fast_paths_enabled()) {
+    const bool done = a.itype == LRNNX_F32    ? ssf_bwd_f32(a, ws, ckp, st, &e)
+                      : a.itype == LRNNX_BF16 ? ssf_bwd_bf16(a, ws, ckp, st, &e)
+                                              : ssf_bwd_f16(a, ws, ckp, st, &e);
+    if (done) return e;
+  }
+  switch (a.itype) {
+    case LRNNX_F32: return ss_bwd_mamba_f32(a, ws, ckp, st);
+    case LRNNX_BF16: return ss_bwd_mamba_bf16(a, ws, ckp, st);
+    default: return ss_bwd_mamba_f16(a, ws, ckp, st);
   }
 }
 
@@ -188,11 +208,7 @@ int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args* a, void* stream) {
   }
   hipError_t e;
   if (a->method == LRNNX_MAMBA) {
-    switch (a->itype) {
-      case LRNNX_F32: e = ss_bwd_mamba_f32(*a, ws, ckp, st); break;
-      case LRNNX_BF16: e = ss_bwd_mamba_bf16(*a, ws, ckp, st); break;
-      default: e = ss_bwd_mamba_f16(*a, ws, ckp, st); break;
-    }
+    e = bwd_mamba(*a, ws, ckp, st);
   } else {
     e = ss_bwd_other_f32(*a, ws, ckp, st);
   }

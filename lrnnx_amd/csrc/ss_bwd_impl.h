@@ -737,6 +737,10 @@ ss_reduce_batch_kernel(const float* __restrict__ part, lrnnx_view out, int64_t B
   static_cast<OT*>(out.ptr)[d * out.s0 + n * out.s1] = acc;
 }
 
+template <typename IT, bool kVarB, bool kVarC>
+static hipError_t ss_bwd_reductions(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws,
+                                    const SSBwdWs& wo, hipStream_t st);
+
 template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
 static hipError_t launch_bwd_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                                const float* ckp, hipStream_t st) {
@@ -763,6 +767,14 @@ static hipError_t launch_bwd_t(const lrnnx_selective_scan_args& a, const SSGeom&
                      wo, ckp, flags);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  return ss_bwd_reductions<IT, kVarB, kVarC>(a, g, ws, wo, st);
+}
+
+// Second-stage reductions of the backward: dB / dC partials over channel
+// blocks (variable B / C), dA, constant dB / dC, dD, ddelta_bias over the batch.
+template <typename IT, bool kVarB, bool kVarC>
+static hipError_t ss_bwd_reductions(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws,
+                                    const SSBwdWs& wo, hipStream_t st) {
   const int64_t B = a.batch, D = a.dim, N = a.dstate, L = a.seqlen, G = a.n_groups;
   if constexpr (kVarB || kVarC) {
     const int64_t ncpg = g.n_cb / G;

@@ -1,0 +1,11 @@
+// Selective scan backward fast path (ssf_bwd_impl.h), f32 I/O (instantiation unit).
+#include "ssf_bwd_impl.h"
+namespace lrnnx {
+// Launches the fast path (kernel + reductions) when it covers the call;
+// returns false otherwise.
+bool ssf_bwd_f32(const lrnnx_selective_scan_args& a, float* ws, const float* ckp, hipStream_t st, hipError_t* err) {
+  if (!ssf_bwd_eligible<float>(a)) return false;
+  *err = ssf_bwd_launch<float>(a, ws, ckp, st);
+  return true;
+}
+}  // namespace lrnnx

@@ -1,0 +1,397 @@
+// Selective scan backward, fast path of the headline case (gfx950).
+//
+// Same coverage as the fast forward (ssf_fwd_eligible): method "mamba",
+// variable B and C, no deltaA, 8 < d_state <= 16, f32 / bf16 / f16 I/O, 64
+// channels per group block, L a multiple of 16, 16-byte aligned rows.
+// Gradients of the reference kernel
+// csrc/selective_scan/selective_scan_backward.cuh:86-845 for this method:
+//   dh_t  = A_bar_{t+1} dh_{t+1} + C_t dy_t      (dy = dout silu(z))
+//   du    = delta' sum_n dh B + D dy
+//   ddelta' = u sum_n dh B + sum_n A A_bar h_{t-1} dh, times sigmoid(delta + bias)
+//   dA    = sum_t delta' A_bar h_{t-1} dh,  dB_t = sum_d dh delta' u,
+//   dC_t  = sum_d dy h_t,  dD = sum dy u,  ddelta_bias = sum ddelta,
+//   dz    = dout out sigma(z) (1 + z (1 - sigma(z)))      (:218-219)
+//
+// Decomposition as in the forward (ssf_fwd_impl.h): one workgroup = one batch
+// row and 64 channels, wave w owns states 4w..4w+3, lane = channel.  The
+// sequence is walked from the end in tiles of 16 steps = one checkpoint
+// interval of the forward (fp32 states every 16 steps, layout (B, n_ck, N, D)).
+// Per tile k:
+//   compute(k)  issue the LDS-DMA fetch of raw tile k-1 (u, delta, dout, z,
+//               out, B, C) and of the checkpoint row that starts tile k-1;
+//               recompute A_bar and h over the 16 steps of tile k from its
+//               checkpoint into VGPRs; walk the steps backwards accumulating
+//               dA (per lane), the per-step sums over the wave's states of
+//               dh B and A A_bar h_{t-1} dh (to LDS, summed over waves in the
+//               epilogue) and the dB / dC values, reduce-scattered over the
+//               64 channels of the wave (one fp32 partial per channel block,
+//               summed over blocks in a fixed order by ss_reduce_bc_kernel).
+//   finish(k)   wait + barrier; epilogue of tile k (du, ddelta; the dD and
+//               ddelta_bias terms stay in per-thread registers) and
+//               conversion of raw tile k-1 (delta' = softplus(delta + bias),
+//               u, dy = dout silu(z) to fp32, dz written here, B / C rows).
+// The fp32 operands are double buffered: the epilogue of tile k and the
+// conversion of tile k-1 share the finish phase.
+#pragma once
+#include <type_traits>
+
+#include "ss_bwd_impl.h"
+#include "ssf_fwd_impl.h"
+
+namespace lrnnx {
+
+namespace ssf {
+// 1 - exp(-d) for d = softplus(x) >= 0, i.e. sigmoid(x); 4-term series below
+// 1/32 so that small d keeps its relative precision
+__device__ __forceinline__ float sigmoid_from_softplus(float d) {
+  const float small = d * fmaf(d, fmaf(d, fmaf(d, -0.041666668f, 0.16666667f), -0.5f), 1.f);
+  const float big = 1.f - __builtin_amdgcn_exp2f(-d * kLog2e);
+  return d < 0.03125f ? small : big;
+}
+}  // namespace ssf
+
+template <typename IT, bool kSP, bool kZ>
+__global__ void __launch_bounds__(ssf::kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __restrict__ ws, const SSBwdWs wo,
+               const float* __restrict__ ckp) {
+  using namespace ssf;
+  constexpr int kT = 16;                  // steps per tile = checkpoint interval
+  static_assert(kT == kCk, "one checkpoint interval per tile");
+  constexpr int kG = kT / 4;              // groups of 4 steps
+  constexpr int kRow = kT * (int)sizeof(IT);   // bytes of one raw row of a tile
+  constexpr int kQ = kRow / 16;           // 16-byte blocks per raw row
+  constexpr int kRaw = kWave * kRow;      // [64][kT] raw tile
+  constexpr int kRawS = 16 * kRow;        // [16][kT] raw B or C tile
+  constexpr int kOp = kG * kWave * 4;     // floats of one [g][64][4] operand tile
+
+  __shared__ __attribute__((aligned(16))) char s_raw_u[kRaw];
+  __shared__ __attribute__((aligned(16))) char s_raw_d[kRaw];
+  __shared__ __attribute__((aligned(16))) char s_raw_do[kRaw];
+  __shared__ __attribute__((aligned(16))) char s_raw_z[kZ ? kRaw : 16];
+  __shared__ __attribute__((aligned(16))) char s_raw_o[kZ ? kRaw : 16];
+  __shared__ __attribute__((aligned(16))) char s_raw_b[kRawS];
+  __shared__ __attribute__((aligned(16))) char s_raw_c[kRawS];
+  __shared__ __attribute__((aligned(16))) float s_ck[2][16 * kWave];   // [buf][n][lane] h at the tile start
+  __shared__ __attribute__((aligned(16))) float s_dl[2][kOp];          // [buf][g][lane][4] delta'
+  __shared__ __attribute__((aligned(16))) float s_u[2][kOp];           // u
+  __shared__ __attribute__((aligned(16))) float s_dy[2][kOp];          // dout silu(z)
+  __shared__ __attribute__((aligned(16))) float s_B[kT * 16];          // [t][n]
+  __shared__ __attribute__((aligned(16))) float s_C[kT * 16];
+  __shared__ __attribute__((aligned(16))) float s_P1[kNW * kOp];       // [w][g][lane][4] sum_k dh B
+  __shared__ __attribute__((aligned(16))) float s_P2[kNW * kOp];       // sum_k A log2(e) A_bar h_{t-1} dh
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t b = blockIdx.y;
+  const int64_t D = a.dim, L = a.seqlen;
+  const int N = (int)a.dstate;
+  const int64_t cb = blockIdx.x;
+  const int64_t d0 = cb * kWave;
+  const int64_t grp = d0 / (D / a.n_groups);
+  const int n0 = w * kS;
+  // thread -> (row er, 4-step group eq) of the per-element phases
+  const int er = tid >> 2, eq = tid & 3;
+  constexpr int kEb = 4 * (int)sizeof(IT);  // bytes of a thread's 4 raw elements
+
+  const IT* gu = static_cast<const IT*>(a.u.ptr) + b * a.u.s0 + d0 * a.u.s1;
+  const IT* gd = static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d0 * a.delta.s1;
+  const IT* gdo = static_cast<const IT*>(a.dout.ptr) + b * a.dout.s0 + d0 * a.dout.s1;
+  const IT* gz = kZ ? static_cast<const IT*>(a.z.ptr) + b * a.z.s0 + d0 * a.z.s1 : nullptr;
+  const IT* gos = kZ ? static_cast<const IT*>(a.out_saved.ptr) + b * a.out_saved.s0 + d0 * a.out_saved.s1 : nullptr;
+  const IT* gB = static_cast<const IT*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1;
+  const IT* gC = static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1;
+  IT* gdu = static_cast<IT*>(a.du.ptr) + b * a.du.s0 + (d0 + er) * a.du.s1 + 4 * eq;
+  IT* gddl = static_cast<IT*>(a.ddelta.ptr) + b * a.ddelta.s0 + (d0 + er) * a.ddelta.s1 + 4 * eq;
+  IT* gdz = kZ ? static_cast<IT*>(a.dz.ptr) + b * a.dz.s0 + (d0 + er) * a.dz.s1 + 4 * eq : nullptr;
+  const uint32_t su = (uint32_t)a.u.s1, sd = (uint32_t)a.delta.s1, sdo = (uint32_t)a.dout.s1;
+  const uint32_t sz = (uint32_t)a.z.s1, sos = (uint32_t)a.out_saved.s1;
+  const uint32_t sBn = (uint32_t)a.B.s2, sCn = (uint32_t)a.C.s2;
+  const float* gck = ckp + b * n_ck * N * D + d0;   // checkpoint kk, state n: gck[(kk * N + n) * D + lane]
+  float* wsB = ws + wo.dBv + ((cb * a.batch + b) * N + n0 + (lane >> 4)) * L + (lane & 15);
+  float* wsC = ws + wo.dCv + ((cb * a.batch + b) * N + n0 + (lane >> 4)) * L + (lane & 15);
+  const bool wr_bc = n0 + (lane >> 4) < N;
+
+  float a2[kS], gn[kS], dA_acc[kS];
+#pragma unroll
+  for (int k = 0; k < kS; ++k) {
+    const int n = n0 + k;
+    const float A_ = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + lane) * a.A.s0 + n * a.A.s1] : -1.f;
+    a2[k] = A_ * kLog2e;
+    gn[k] = 0.f;
+    dA_acc[k] = 0.f;
+  }
+  const float e_bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[(d0 + er) * a.delta_bias.s0] : 0.f;
+  const float e_D = a.D.ptr ? static_cast<const float*>(a.D.ptr)[(d0 + er) * a.D.s0] : 0.f;
+  float e_dD = 0.f, e_dbias = 0.f;  // this thread's share of dD and ddelta_bias (channel d0 + er)
+
+  const int64_t n_tiles = L / kT;
+
+  auto fetch = [&](int64_t tile) __attribute__((always_inline)) {
+    const int64_t t0 = tile * kT;
+    tile_fetch_async<IT, kQ>(gu + t0, su, kWave, s_raw_u, w, kNW, lane);
+    tile_fetch_async<IT, kQ>(gd + t0, sd, kWave, s_raw_d, w, kNW, lane);
+    tile_fetch_async<IT, kQ>(gdo + t0, sdo, kWave, s_raw_do, w, kNW, lane);
+    if constexpr (kZ) {
+      tile_fetch_async<IT, kQ>(gz + t0, sz, kWave, s_raw_z, w, kNW, lane);
+      tile_fetch_async<IT, kQ>(gos + t0, sos, kWave, s_raw_o, w, kNW, lane);
+    }
+    if (w == 2) tile_fetch_async<IT, kQ>(gB + t0, sBn, N, s_raw_b, 0, 1, lane);
+    if (w == 3) tile_fetch_async<IT, kQ>(gC + t0, sCn, N, s_raw_c, 0, 1, lane);
+    // h at the start of `tile` = checkpoint tile - 1 (none for tile 0)
+    if (tile > 0)
+      tile_fetch_async<float, kWave * 4 / 16>(gck + (tile - 1) * N * D, (uint32_t)D, N,
+                                               reinterpret_cast<char*>(s_ck[tile & 1]), w, kNW, lane);
+  };
+
+  // raw tile -> fp32 operands of buffer p; dz is written here
+  auto convert = [&](int64_t tile, int p) __attribute__((always_inline)) {
+    float vu[4], vd[4], vdo[4];
+    const int ro = er * kRow + eq * kEb;   // byte offset of this thread's 4 raw elements
+    raw4_to_f32<IT>(s_raw_u + ro, vu);
+    raw4_to_f32<IT>(s_raw_d + ro, vd);
+    raw4_to_f32<IT>(s_raw_do + ro, vdo);
+    float dy[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = vd[i] + e_bias;
+      vd[i] = kSP ? softplus20_fast(x) : x;
+      dy[i] = vdo[i];
+    }
+    if constexpr (kZ) {
+      float vz[4], vo[4], dz[4];
+      raw4_to_f32<IT>(s_raw_z + ro, vz);
+      raw4_to_f32<IT>(s_raw_o + ro, vo);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float sg = sigmoidf_fast(vz[i]);
+        const float zs = vz[i] * sg;
+        dz[i] = vdo[i] * vo[i] * fmaf(zs, 1.f - sg, sg);   // sg (1 + z (1 - sg))
+        dy[i] = vdo[i] * zs;
+      }
+      store4<IT>(gdz + tile * kT, dz);
+    }
+    const int o = (eq * kWave + er) * 4;
+    *reinterpret_cast<float4*>(&s_dl[p][o]) = make_float4(vd[0], vd[1], vd[2], vd[3]);
+    *reinterpret_cast<float4*>(&s_u[p][o]) = make_float4(vu[0], vu[1], vu[2], vu[3]);
+    *reinterpret_cast<float4*>(&s_dy[p][o]) = make_float4(dy[0], dy[1], dy[2], dy[3]);
+    // B / C rows, transposed to step-major: threads [0, 64) B, [64, 128) C,
+    // 4 steps of one state each; states >= N are zero
+    if (tid < 2 * 16 * 4) {
+      const bool isC = tid >= 64;
+      const int j = tid & 63;
+      const int n = j >> 2, s4 = (j & 3) * 4;
+      float v[4];
+      raw4_to_f32<IT>((isC ? s_raw_c : s_raw_b) + n * kRow + s4 * (int)sizeof(IT), v);
+      float* dst = (isC ? s_C : s_B) + s4 * 16 + n;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[i * 16] = n < N ? v[i] : 0.f;
+    }
+  };
+
+  // epilogue of tile (fp32 buffer p): du, ddelta; dD / ddelta_bias terms
+  auto epilogue = [&](int64_t tile, int p) __attribute__((always_inline)) {
+    const int o = (eq * kWave + er) * 4;
+    float4 P1 = *reinterpret_cast<const float4*>(&s_P1[o]);
+    float4 P2 = *reinterpret_cast<const float4*>(&s_P2[o]);
+#pragma unroll
+    for (int ww = 1; ww < kNW; ++ww) {
+      const float4 q1 = *reinterpret_cast<const float4*>(&s_P1[ww * kOp + o]);
+      const float4 q2 = *reinterpret_cast<const float4*>(&s_P2[ww * kOp + o]);
+      P1.x += q1.x; P1.y += q1.y; P1.z += q1.z; P1.w += q1.w;
+      P2.x += q2.x; P2.y += q2.y; P2.z += q2.z; P2.w += q2.w;
+    }
+    const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[p][o]);
+    const float4 u4 = *reinterpret_cast<const float4*>(&s_u[p][o]);
+    const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[p][o]);
+    const float p1[4] = {P1.x, P1.y, P1.z, P1.w}, p2[4] = {P2.x, P2.y, P2.z, P2.w};
+    const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, uu[4] = {u4.x, u4.y, u4.z, u4.w};
+    const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+    float du[4], dd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      du[i] = fmaf(dl[i], p1[i], e_D * dy[i]);
+      const float ddl = fmaf(uu[i], p1[i], kLn2 * p2[i]);
+      dd[i] = kSP ? ddl * sigmoid_from_softplus(dl[i]) : ddl;
+      e_dD = fmaf(dy[i], uu[i], e_dD);
+      e_dbias += dd[i];
+    }
+    store4<IT>(gdu + tile * kT, du);
+    store4<IT>(gddl + tile * kT, dd);
+  };
+
+  // ---- prologue: last tile
+  fetch(n_tiles - 1);
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  __syncthreads();
+  convert(n_tiles - 1, (int)((n_tiles - 1) & 1));
+  __syncthreads();
+
+  for (int64_t tile = n_tiles - 1; tile >= 0; --tile) {
+    const int p = (int)(tile & 1);
+    if (tile > 0) fetch(tile - 1);
+
+    // ---- compute(tile)
+    float h0[kS];
+#pragma unroll
+    for (int k = 0; k < kS; ++k) h0[k] = (tile > 0 && n0 + k < N) ? s_ck[p][(n0 + k) * kWave + lane] : 0.f;
+    // recompute A_bar and h over the tile; dC_t = sum_d dy_t h_t is complete
+    // here, so its reduce-scatter runs before the reverse walk
+    float AB[kT][kS], H[kT][kS], accC[kT];
+    {
+      float hc[kS];
+#pragma unroll
+      for (int k = 0; k < kS; ++k) hc[k] = h0[k];
+#pragma unroll
+      for (int g = 0; g < kG; ++g) {
+        // scheduling fence: the LDS operand loads of later groups are not
+        // hoisted above this group's arithmetic (that would exceed 256 VGPRs)
+        __builtin_amdgcn_sched_barrier(0);
+        const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[p][(g * kWave + lane) * 4]);
+        const float4 u4 = *reinterpret_cast<const float4*>(&s_u[p][(g * kWave + lane) * 4]);
+        const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[p][(g * kWave + lane) * 4]);
+        const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, uu[4] = {u4.x, u4.y, u4.z, u4.w};
+        const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 4 * g + i;
+          const float4 b4 = *reinterpret_cast<const float4*>(s_B + t * 16 + n0);
+          const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+          const float x = dl[i] * uu[i];
+          float vC[kS];
+#pragma unroll
+          for (int k = 0; k < kS; ++k) {
+            const float ab = __builtin_amdgcn_exp2f(dl[i] * a2[k]);
+            hc[k] = fmaf(ab, hc[k], x * bv[k]);
+            AB[t][k] = ab;
+            H[t][k] = hc[k];
+            vC[k] = dy[i] * hc[k];
+          }
+          // index bits 5, 4 of the reduce-scatter (= the wave's state k): lanes
+          // 0-31 keep states 0-1, lanes 32-63 states 2-3, then odd rows keep k odd
+          rs_step32<2>(vC);
+          rs_step16<1>(vC);
+          accC[t] = vC[0];
+        }
+      }
+    }
+    // index bits 3..0 = step; lane l ends with state n0 + l / 16, step l % 16
+    rs_tail16(accC, lane);
+    const float dC_part = accC[0];
+
+    // reverse walk; the last four reduce-scatter stages of dB (index bits 3..0
+    // = step) run as a butterfly that consumes step t as soon as it exists:
+    // bit 3 pairs t with t + 8, bit 2 t with t + 4, bit 1 t with t + 2, bit 0
+    // 0 with 1 (rs_tail16 applied in step order), so at most 8 partials live
+    float r8[8], r4[4], r2[2], r1 = 0.f, dB_part = 0.f;
+    auto rs_pair = [&](float lo, float hi, bool bit, auto ctrl) __attribute__((always_inline)) {
+      const float keep = bit ? hi : lo;
+      const float send = bit ? lo : hi;
+      return keep + dpp_mov<decltype(ctrl)::value>(send);
+    };
+    auto stream_dB = [&](int t, float v) __attribute__((always_inline)) {
+      if (t >= 8) { r8[t - 8] = v; return; }
+      const float x3 = rs_pair(v, r8[t], lane & 8, std::integral_constant<int, kDppRowMirror>{});
+      if (t >= 4) { r4[t - 4] = x3; return; }
+      const float x2 = rs_pair(x3, r4[t], lane & 4, std::integral_constant<int, kDppRowHalfMirror>{});
+      if (t >= 2) { r2[t - 2] = x2; return; }
+      const float x1 = rs_pair(x2, r2[t], lane & 2, std::integral_constant<int, kDppQuadXor2>{});
+      if (t == 1) { r1 = x1; return; }
+      dB_part = rs_pair(x1, r1, lane & 1, std::integral_constant<int, kDppQuadXor1>{});
+    };
+#pragma unroll
+    for (int g = kG - 1; g >= 0; --g) {
+      __builtin_amdgcn_sched_barrier(0);
+      const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[p][(g * kWave + lane) * 4]);
+      const float4 u4 = *reinterpret_cast<const float4*>(&s_u[p][(g * kWave + lane) * 4]);
+      const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[p][(g * kWave + lane) * 4]);
+      const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+      const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
+      float p1v[4], p2v[4];
+#pragma unroll
+      for (int i = 3; i >= 0; --i) {
+        const int t = 4 * g + i;
+        const float4 b4 = *reinterpret_cast<const float4*>(s_B + t * 16 + n0);
+        const float4 c4 = *reinterpret_cast<const float4*>(s_C + t * 16 + n0);
+        const float bv[4] = {b4.x, b4.y, b4.z, b4.w}, cv[4] = {c4.x, c4.y, c4.z, c4.w};
+        const float x = dl[i] * uu[i];
+        float p1 = 0.f, p2 = 0.f, vB[kS];
+#pragma unroll
+        for (int k = 0; k < kS; ++k) {
+          const float dh = fmaf(dy[i], cv[k], gn[k]);
+          const float gk = AB[t][k] * dh;
+          gn[k] = gk;
+          const float wv = gk * (t > 0 ? H[t - 1][k] : h0[k]);
+          p2 = fmaf(wv, a2[k], p2);   // A log2(e) units; the epilogue multiplies by ln 2
+          dA_acc[k] = fmaf(wv, dl[i], dA_acc[k]);
+          p1 = fmaf(dh, bv[k], p1);
+          vB[k] = dh * x;
+        }
+        p1v[i] = p1;
+        p2v[i] = p2;
+        rs_step32<2>(vB);
+        rs_step16<1>(vB);
+        stream_dB(t, vB[0]);
+      }
+      *reinterpret_cast<float4*>(&s_P1[(w * kG + g) * kWave * 4 + lane * 4]) = make_float4(p1v[0], p1v[1], p1v[2], p1v[3]);
+      *reinterpret_cast<float4*>(&s_P2[(w * kG + g) * kWave * 4 + lane * 4]) = make_float4(p2v[0], p2v[1], p2v[2], p2v[3]);
+    }
+
+    // ---- finish(tile).  The wait covers the fetch of tile - 1 and the stores
+    // of the previous finish phase; this tile's partials are stored after it.
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (wr_bc) {
+      wsB[tile * kT] = dB_part;
+      wsC[tile * kT] = dC_part;
+    }
+    epilogue(tile, p);
+    if (tile > 0) convert(tile - 1, p ^ 1);
+    __syncthreads();
+  }
+
+  // per-(b, d, n) and per-(b, d) partials, summed over b by ss_reduce_batch_kernel
+#pragma unroll
+  for (int k = 0; k < kS; ++k)
+    if (n0 + k < N) ws[wo.dA + (b * D + d0 + lane) * N + n0 + k] = dA_acc[k];
+  // dD / ddelta_bias: the 4 threads of a channel are consecutive lanes
+  e_dD += dpp_mov<kDppQuadXor1>(e_dD);
+  e_dD += dpp_mov<kDppQuadXor2>(e_dD);
+  e_dbias += dpp_mov<kDppQuadXor1>(e_dbias);
+  e_dbias += dpp_mov<kDppQuadXor2>(e_dbias);
+  if (eq == 0) {
+    ws[wo.dD + b * D + d0 + er] = e_dD;
+    ws[wo.dbias + b * D + d0 + er] = e_dbias;
+  }
+}
+
+// Whether the fast backward covers this call.
+template <typename IT>
+inline bool ssf_bwd_eligible(const lrnnx_selective_scan_args& a) {
+  using ssf::rows_aligned;
+  if (!ssf::shape_ok<IT>(a, ssf::kCk)) return false;
+  if (a.z.ptr && (!a.out_saved.ptr || !a.dz.ptr)) return false;
+  return rows_aligned<IT>(a.dout, false) && rows_aligned<IT>(a.out_saved, false) && rows_aligned<IT>(a.du, false) &&
+         rows_aligned<IT>(a.ddelta, false) && rows_aligned<IT>(a.dz, false);
+}
+
+template <typename IT>
+inline hipError_t ssf_bwd_launch(const lrnnx_selective_scan_args& a, float* ws, const float* ckp, hipStream_t st) {
+  const SSGeom g = ss_geom(a);
+  const SSBwdWs wo = ss_bwd_ws(a, g, a.ckpt == nullptr);
+  dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch);
+  dim3 block(ssf::kNT);
+  const bool z = a.z.ptr != nullptr;
+  if (a.delta_softplus) {
+    if (z) hipLaunchKernelGGL((ssf_bwd_kernel<IT, true, true>), grid, block, 0, st, a, g.n_ck, ws, wo, ckp);
+    else hipLaunchKernelGGL((ssf_bwd_kernel<IT, true, false>), grid, block, 0, st, a, g.n_ck, ws, wo, ckp);
+  } else {
+    if (z) hipLaunchKernelGGL((ssf_bwd_kernel<IT, false, true>), grid, block, 0, st, a, g.n_ck, ws, wo, ckp);
+    else hipLaunchKernelGGL((ssf_bwd_kernel<IT, false, false>), grid, block, 0, st, a, g.n_ck, ws, wo, ckp);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return ss_bwd_reductions<IT, true, true>(a, g, ws, wo, st);
+}
+
+}  // namespace lrnnx

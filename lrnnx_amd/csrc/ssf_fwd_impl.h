@@ -212,6 +212,13 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
       }
     }
   };
+  // fp32 state after step t_end - 1 (t_end a multiple of kCk): checkpoint t_end / kCk - 1
+  auto store_ckpt = [&](int64_t t_end) __attribute__((always_inline)) {
+    float* cp = ckp + ((b * n_ck + t_end / kCk - 1) * N + n0) * D + d0 + lane;
+#pragma unroll
+    for (int k = 0; k < kS; ++k)
+      if (n0 + k < N) cp[(int64_t)k * D] = h[k];
+  };
   auto chunk_end = [&](int64_t tile) __attribute__((always_inline)) {
     return ((tile + 1) * kT) % kXChunk == 0 || tile + 1 == n_tiles;
   };
@@ -255,18 +262,16 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
         y[i] = acc;
       }
       *reinterpret_cast<float4*>(sYw + (g * kWave + lane) * 4) = make_float4(y[0], y[1], y[2], y[3]);
-      if (ckp != nullptr && ((4 * g + 4) % kCk) == 0) {
-        const int64_t kk = (t0 + 4 * g + 4) / kCk - 1;
-        float* cp = ckp + ((b * n_ck + kk) * N + n0) * D + d0 + lane;
-#pragma unroll
-        for (int k = 0; k < kS; ++k)
-          if (n0 + k < N) cp[(int64_t)k * D] = h[k];
-      }
+      // checkpoints inside the tile; the one at the tile end is stored after
+      // the barrier below, so that the wait before it does not wait for it
+      if (ckp != nullptr && ((4 * g + 4) % kCk) == 0 && 4 * g + 4 < kT) store_ckpt(t0 + 4 * g + 4);
     }
 
-    // ---- finish(tile)
+    // ---- finish(tile).  The wait covers the fetch of tile + 1 and the stores
+    // of the previous finish phase.
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
+    if (ckp != nullptr) store_ckpt(t0 + kT);
     epilogue(tile);
     if (chunk_end(tile)) {
       s_dsum[tid] = e_dsum;
@@ -278,22 +283,34 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
   if (xp) store_x(n_tiles - 1);
 }
 
-// Whether the fast path covers this call (see the header comment).
+namespace ssf {
+// A sequence view whose rows (and, for 4-D B / C, state rows) all start on
+// 16-byte boundaries, as the LDS-DMA tile fetch and the vector stores need.
+template <typename IT>
+inline bool rows_aligned(const lrnnx_view& v, bool four_d) {
+  if (v.ptr == nullptr) return true;
+  const int64_t s = sizeof(IT);
+  return (reinterpret_cast<uintptr_t>(v.ptr) & 15u) == 0 && (v.s0 * s) % 16 == 0 && (v.s1 * s) % 16 == 0 &&
+         (!four_d || (v.s2 * s) % 16 == 0);
+}
+
+// Shape / option part of the fast-path coverage (both directions).
+template <typename IT>
+inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile) {
+  if (a.method != LRNNX_MAMBA || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C || a.deltaA.ptr) return false;
+  if (a.dstate <= 8 || a.dstate > 16 || a.seqlen <= 0 || a.seqlen % tile != 0) return false;
+  if (a.n_groups <= 0 || a.dim % a.n_groups != 0 || (a.dim / a.n_groups) % kWave != 0) return false;
+  return rows_aligned<IT>(a.u, false) && rows_aligned<IT>(a.delta, false) && rows_aligned<IT>(a.z, false) &&
+         rows_aligned<IT>(a.B, true) && rows_aligned<IT>(a.C, true);
+}
+}  // namespace ssf
+
+// Whether the fast forward covers this call (see the header comment).
 template <typename IT>
 inline bool ssf_fwd_eligible(const lrnnx_selective_scan_args& a) {
-  constexpr int kT = ssf::tile_steps<IT>();
-  if (a.method != LRNNX_MAMBA || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C || a.deltaA.ptr) return false;
-  if (a.dstate <= 8 || a.dstate > 16 || a.seqlen % kT != 0 || a.seqlen <= 0) return false;
-  if (a.n_groups <= 0 || a.dim % a.n_groups != 0 || (a.dim / a.n_groups) % kWave != 0) return false;
+  if (!ssf::shape_ok<IT>(a, ssf::tile_steps<IT>())) return false;
   if ((a.z.ptr != nullptr) != (a.out_z.ptr != nullptr)) return false;
-  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  auto rows_ok = [&](const lrnnx_view& v, bool four_d) {
-    if (v.ptr == nullptr) return true;
-    const int64_t s = sizeof(IT);
-    return al(v.ptr) && (v.s0 * s) % 16 == 0 && (v.s1 * s) % 16 == 0 && (!four_d || (v.s2 * s) % 16 == 0);
-  };
-  return rows_ok(a.u, false) && rows_ok(a.delta, false) && rows_ok(a.z, false) && rows_ok(a.B, true) &&
-         rows_ok(a.C, true) && rows_ok(a.out, false) && rows_ok(a.out_z, false);
+  return ssf::rows_aligned<IT>(a.out, false) && ssf::rows_aligned<IT>(a.out_z, false);
 }
 
 template <typename IT>

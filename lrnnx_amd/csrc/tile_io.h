@@ -148,6 +148,33 @@ __device__ __forceinline__ uint4 f32_to_raw(const float* v) {
   return raw;
 }
 
+// 4 consecutive elements at LDS byte address p (8-byte aligned for 16-bit
+// types, 16-byte for f32) -> floats
+template <typename IT>
+__device__ __forceinline__ void raw4_to_f32(const char* p, float* out) {
+  if constexpr (sizeof(IT) == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  } else {
+    const uint2 raw = *reinterpret_cast<const uint2*>(p);
+    const IT* e = reinterpret_cast<const IT*>(&raw);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = to_f32(e[i]);
+  }
+}
+
+// 4 floats -> 4 consecutive elements at global address p (one 8- or 16-byte store)
+template <typename IT>
+__device__ __forceinline__ void store4(IT* p, const float* v) {
+  if constexpr (sizeof(IT) == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    float w8[8] = {v[0], v[1], v[2], v[3], 0.f, 0.f, 0.f, 0.f};
+    const uint4 raw = f32_to_raw<IT>(w8);
+    *reinterpret_cast<uint2*>(p) = make_uint2(raw.x, raw.y);
+  }
+}
+
 // fast transcendental helpers (v_exp_f32 / v_log_f32 / v_rcp_f32)
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 __device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
