@@ -13,6 +13,13 @@
 #include "ss_common.h"
 
 namespace lrnnx {
+// LRNNX_SCAN_GENERIC=1 in the environment routes every call to the generic
+// kernels (for A/B timing and cross-checks of the fast paths).
+bool fast_paths_enabled() {
+  const char* v = getenv("LRNNX_SCAN_GENERIC");
+  return !(v && v[0] && v[0] != '0');
+}
+
 hipError_t ss_fwd_mamba_f32(const lrnnx_selective_scan_args&, hipStream_t);
 hipError_t ss_fwd_mamba_bf16(const lrnnx_selective_scan_args&, hipStream_t);
 hipError_t ss_fwd_mamba_f16(const lrnnx_selective_scan_args&, hipStream_t);
@@ -74,12 +81,6 @@ const char* method_name(int m) {
   return "?";
 }
 
-// LRNNX_SCAN_GENERIC=1 in the environment routes every call to the generic
-// kernels (for A/B timing and cross-checks of the fast paths).
-bool fast_paths_enabled() {
-  const char* v = getenv("LRNNX_SCAN_GENERIC");
-  return !(v && v[0] && v[0] != '0');
-}
 
 // Forward of the "mamba" method: fast path when it covers the call, else the
 // generic kernel.

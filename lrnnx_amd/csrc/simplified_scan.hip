@@ -19,55 +19,11 @@
 // per-thread partials of dA, dB, dC that a last kernel sums in a fixed order.
 // When delta (and deltaA) has zero stride along L, A_bar and beta are
 // computed once per (b, p, s) instead of per element.
-#include "common.h"
+#include "simp_common.h"
 
 namespace lrnnx {
 
 constexpr int kSC = 32;  // chunk length along L
-
-struct cf {
-  float r, i;
-};
-__device__ __forceinline__ cf cmake(float r, float i) { return cf{r, i}; }
-__device__ __forceinline__ cf cadd(cf a, cf b) { return cf{a.r + b.r, a.i + b.i}; }
-__device__ __forceinline__ cf csub(cf a, cf b) { return cf{a.r - b.r, a.i - b.i}; }
-__device__ __forceinline__ cf cmul(cf a, cf b) { return cf{a.r * b.r - a.i * b.i, a.r * b.i + a.i * b.r}; }
-__device__ __forceinline__ cf cconj(cf a) { return cf{a.r, -a.i}; }
-__device__ __forceinline__ cf cscale(cf a, float s) { return cf{a.r * s, a.i * s}; }
-// a * b + c
-__device__ __forceinline__ cf cfma(cf a, cf b, cf c) {
-  return cf{fmaf(a.r, b.r, fmaf(-a.i, b.i, c.r)), fmaf(a.r, b.i, fmaf(a.i, b.r, c.i))};
-}
-__device__ __forceinline__ cf cdiv(cf a, cf b) {
-  const float den = b.r * b.r + b.i * b.i;
-  return cf{(a.r * b.r + a.i * b.i) / den, (a.i * b.r - a.r * b.i) / den};
-}
-__device__ __forceinline__ cf cexp_(cf z) {
-  float s, c;
-  sincosf(z.i, &s, &c);
-  const float e = expf(z.r);
-  return cf{e * c, e * s};
-}
-__device__ __forceinline__ cf ld(const float* p) {
-  const float2 v = *reinterpret_cast<const float2*>(p);
-  return cf{v.x, v.y};
-}
-__device__ __forceinline__ void st(float* p, cf v) { *reinterpret_cast<float2*>(p) = make_float2(v.r, v.i); }
-
-// A_bar and beta for one element (simplified_scan.cuh:198-224)
-template <int kMethod>
-__device__ __forceinline__ void sdisc(float dtA, float dl, cf A, cf& Ab, cf& beta) {
-  const cf one = cmake(1.f, 0.f);
-  if constexpr (kMethod == LRNNX_BILINEAR) {
-    const cf vA = cscale(A, 0.5f * dtA);
-    Ab = cdiv(cadd(one, vA), csub(one, vA));
-    beta = cdiv(cmake(dl, 0.f), csub(one, cscale(A, 0.5f * dl)));
-  } else {
-    Ab = cexp_(cscale(A, dtA));
-    if constexpr (kMethod == LRNNX_ZOH) beta = cdiv(csub(cexp_(cscale(A, dl)), one), A);
-    else beta = one;
-  }
-}
 
 struct SView {  // (b, p, l) real or complex sequence view
   const float* p;
@@ -414,7 +370,13 @@ static SimpParams simp_params(const lrnnx_simplified_scan_args& a) {
   return P;
 }
 
+bool simpf_fwd(const lrnnx_simplified_scan_args& a, hipStream_t st, hipError_t* err);
+bool simpf_bwd(const lrnnx_simplified_scan_args& a, float* part, hipStream_t st, hipError_t* err);
+bool fast_paths_enabled();
+
 hipError_t simp_fwd_launch(const lrnnx_simplified_scan_args& a, hipStream_t st) {
+  hipError_t e = hipSuccess;
+  if (fast_paths_enabled() && simpf_fwd(a, st, &e)) return e;
   SimpParams P = simp_params(a);
   int64_t agg, carry, ck, part, total;
   simp_ws(a, false, false, agg, carry, ck, part, total);
@@ -456,6 +418,8 @@ hipError_t simp_bwd_launch(const lrnnx_simplified_scan_args& a, hipStream_t st) 
   int64_t agg, carry, ck, part, total;
   simp_ws(a, true, a.ckpt == nullptr, agg, carry, ck, part, total);
   float* ws = static_cast<float*>(a.workspace);
+  hipError_t e = hipSuccess;
+  if (fast_paths_enabled() && simpf_bwd(a, ws + part, st, &e)) return e;
   P.agg = ws + agg;
   P.carry = ws + carry;
   P.ckpt = a.ckpt ? static_cast<float*>(a.ckpt) : ws + ck;

@@ -725,6 +725,33 @@ ss_reduce_bc_kernel(const float* __restrict__ part, lrnnx_view out, int64_t B, i
   static_cast<OT*>(out.ptr)[b * out.s0 + g * out.s1 + n * out.s2 + t] = from_f32<OT>(acc);
 }
 
+// Vector form of ss_reduce_bc_kernel for dB and dC in one launch (blockIdx.z
+// selects the quantity): each thread sums 4 consecutive steps with 16-byte
+// loads, the channel blocks in the same fixed order.  Needs L % 4 == 0 and
+// output rows aligned to 4 elements (checked by the caller).
+template <typename OT>
+__global__ void __launch_bounds__(256)
+ss_reduce_bc4_kernel(const float* __restrict__ part_b, const float* __restrict__ part_c, lrnnx_view out_b,
+                     lrnnx_view out_c, int64_t B, int64_t G, int64_t N, int64_t L, int64_t ncpg) {
+  const int64_t t = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+  const int64_t row = blockIdx.y;  // (b, g, n)
+  if (t >= L) return;
+  const bool isC = blockIdx.z != 0;
+  const float* part = isC ? part_c : part_b;
+  const lrnnx_view out = isC ? out_c : out_b;
+  const int64_t n = row % N, g = (row / N) % G, b = row / (N * G);
+  const int64_t step = B * N * L;  // between consecutive channel blocks
+  const float* p = part + ((g * ncpg * B + b) * N + n) * L + t;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+  for (int64_t j = 0; j < ncpg; ++j) {
+    const float4 v = *reinterpret_cast<const float4*>(p + j * step);
+    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+  }
+  const float r[4] = {acc.x, acc.y, acc.z, acc.w};
+  store4<OT>(static_cast<OT*>(out.ptr) + b * out.s0 + g * out.s1 + n * out.s2 + t, r);
+}
+
 // out[d, n] = sum_b part[b, d, n]  (fp32; n == 1 for per-channel vectors)
 template <typename OT>
 __global__ void __launch_bounds__(256)
@@ -739,7 +766,7 @@ ss_reduce_batch_kernel(const float* __restrict__ part, lrnnx_view out, int64_t B
 
 template <typename IT, bool kVarB, bool kVarC>
 static hipError_t ss_bwd_reductions(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws,
-                                    const SSBwdWs& wo, hipStream_t st);
+                                    const SSBwdWs& wo, hipStream_t st, bool batch_only = false);
 
 template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
 static hipError_t launch_bwd_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
@@ -774,8 +801,21 @@ static hipError_t launch_bwd_t(const lrnnx_selective_scan_args& a, const SSGeom&
 // blocks (variable B / C), dA, constant dB / dC, dD, ddelta_bias over the batch.
 template <typename IT, bool kVarB, bool kVarC>
 static hipError_t ss_bwd_reductions(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws,
-                                    const SSBwdWs& wo, hipStream_t st) {
+                                    const SSBwdWs& wo, hipStream_t st, bool batch_only) {
   const int64_t B = a.batch, D = a.dim, N = a.dstate, L = a.seqlen, G = a.n_groups;
+  if constexpr (kVarB && kVarC) {
+    auto al4 = [](const lrnnx_view& v) {
+      const int64_t s = sizeof(IT);
+      return (reinterpret_cast<uintptr_t>(v.ptr) % (4 * s)) == 0 && v.s0 % 4 == 0 && v.s1 % 4 == 0 && v.s2 % 4 == 0;
+    };
+    if (L % 4 == 0 && al4(a.dB) && al4(a.dC)) {
+      const int64_t ncpg = g.n_cb / G;
+      dim3 rg((unsigned)((L / 4 + 255) / 256), (unsigned)(B * G * N), 2);
+      hipLaunchKernelGGL(ss_reduce_bc4_kernel<IT>, rg, dim3(256), 0, st, ws + wo.dBv, ws + wo.dCv, a.dB, a.dC, B, G,
+                         N, L, ncpg);
+      return ss_bwd_reductions<IT, false, false>(a, g, ws, wo, st, /*batch_only=*/true);
+    }
+  }
   if constexpr (kVarB || kVarC) {
     const int64_t ncpg = g.n_cb / G;
     dim3 rg((unsigned)((L + 255) / 256), (unsigned)(B * G * N));
@@ -786,9 +826,9 @@ static hipError_t ss_bwd_reductions(const lrnnx_selective_scan_args& a, const SS
   }
   const unsigned gdn = (unsigned)((D * N + 255) / 256), gd = (unsigned)((D + 255) / 256);
   hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dA, a.dA, B, D, N);
-  if constexpr (!kVarB)
+  if (!kVarB && !batch_only)
     hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dBc, a.dB, B, D, N);
-  if constexpr (!kVarC)
+  if (!kVarC && !batch_only)
     hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dCc, a.dC, B, D, N);
   if (a.dD.ptr) {
     lrnnx_view v = a.dD;

@@ -171,7 +171,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       }
       store4<IT>(gdz + tile * kT, dz);
     }
-    const int o = (eq * kWave + er) * 4;
+    const int o = op_off<0>(eq, er);
     *reinterpret_cast<float4*>(&s_dl[p][o]) = make_float4(vd[0], vd[1], vd[2], vd[3]);
     *reinterpret_cast<float4*>(&s_u[p][o]) = make_float4(vu[0], vu[1], vu[2], vu[3]);
     *reinterpret_cast<float4*>(&s_dy[p][o]) = make_float4(dy[0], dy[1], dy[2], dy[3]);
@@ -191,7 +191,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
 
   // epilogue of tile (fp32 buffer p): du, ddelta; dD / ddelta_bias terms
   auto epilogue = [&](int64_t tile, int p) __attribute__((always_inline)) {
-    const int o = (eq * kWave + er) * 4;
+    const int o = op_off<0>(eq, er);
     float4 P1 = *reinterpret_cast<const float4*>(&s_P1[o]);
     float4 P2 = *reinterpret_cast<const float4*>(&s_P2[o]);
 #pragma unroll
@@ -247,9 +247,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
         // scheduling fence: the LDS operand loads of later groups are not
         // hoisted above this group's arithmetic (that would exceed 256 VGPRs)
         __builtin_amdgcn_sched_barrier(0);
-        const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[p][(g * kWave + lane) * 4]);
-        const float4 u4 = *reinterpret_cast<const float4*>(&s_u[p][(g * kWave + lane) * 4]);
-        const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[p][(g * kWave + lane) * 4]);
+        const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[p][op_off<0>(g, lane)]);
+        const float4 u4 = *reinterpret_cast<const float4*>(&s_u[p][op_off<0>(g, lane)]);
+        const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[p][op_off<0>(g, lane)]);
         const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, uu[4] = {u4.x, u4.y, u4.z, u4.w};
         const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
 #pragma unroll
@@ -302,9 +302,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
 #pragma unroll
     for (int g = kG - 1; g >= 0; --g) {
       __builtin_amdgcn_sched_barrier(0);
-      const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[p][(g * kWave + lane) * 4]);
-      const float4 u4 = *reinterpret_cast<const float4*>(&s_u[p][(g * kWave + lane) * 4]);
-      const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[p][(g * kWave + lane) * 4]);
+      const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[p][op_off<0>(g, lane)]);
+      const float4 u4 = *reinterpret_cast<const float4*>(&s_u[p][op_off<0>(g, lane)]);
+      const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[p][op_off<0>(g, lane)]);
       const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
       const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
       float p1v[4], p2v[4];
@@ -333,8 +333,8 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
         rs_step16<1>(vB);
         stream_dB(t, vB[0]);
       }
-      *reinterpret_cast<float4*>(&s_P1[(w * kG + g) * kWave * 4 + lane * 4]) = make_float4(p1v[0], p1v[1], p1v[2], p1v[3]);
-      *reinterpret_cast<float4*>(&s_P2[(w * kG + g) * kWave * 4 + lane * 4]) = make_float4(p2v[0], p2v[1], p2v[2], p2v[3]);
+      *reinterpret_cast<float4*>(&s_P1[w * kOp + op_off<0>(g, lane)]) = make_float4(p1v[0], p1v[1], p1v[2], p1v[3]);
+      *reinterpret_cast<float4*>(&s_P2[w * kOp + op_off<0>(g, lane)]) = make_float4(p2v[0], p2v[1], p2v[2], p2v[3]);
     }
 
     // ---- finish(tile).  The wait covers the fetch of tile - 1 and the stores

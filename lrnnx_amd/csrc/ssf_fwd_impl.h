@@ -53,6 +53,17 @@ __device__ __forceinline__ float softplus20_fast(float x) {
   return x > 20.f ? x : r;
 }
 
+// Float offset of (4-step group g, channel row r) in a [g][64][4] fp32 operand
+// tile.  Rows are XOR-swizzled by 2 * (g >> kSh) so that both access patterns
+// are free of LDS bank conflicts: a wave reading one group for its 64 lanes
+// (a permutation of 64 consecutive 16-byte slots), and the per-element phases,
+// where lane 4 r + q handles groups of one row r (consecutive lanes then hit
+// different 16-byte bank groups).  kSh = log2(4-step groups per thread).
+template <int kSh>
+__device__ __forceinline__ int op_off(int g, int r) {
+  return (g * kWave + (r ^ ((g >> kSh) << 1))) * 4;
+}
+
 __device__ __forceinline__ float sigmoidf_fast(float z) {
   return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-z * kLog2e));
 }
@@ -71,6 +82,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
   static_assert(kCk % kT == 0 || kT % kCk == 0, "checkpoint interval vs tile");
   constexpr int kRaw = kWave * kT * (int)sizeof(IT);   // [64][kT] raw tile, bytes
   constexpr int kRawS = 16 * kT * (int)sizeof(IT);     // [16][kT] raw B or C tile
+  constexpr int kSh = kE == 8 ? 1 : 0;                 // log2(4-step groups per thread)
 
   __shared__ __attribute__((aligned(16))) char s_raw_u[kRaw];
   __shared__ __attribute__((aligned(16))) char s_raw_d[kRaw];
@@ -152,7 +164,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
     e_dsum += dsum;
 #pragma unroll
     for (int i = 0; i < kE; i += 4) {
-      const int o = (((eq * kE + i) >> 2) * kWave + er) * 4;
+      const int o = op_off<kSh>((eq * kE + i) >> 2, er);
       *reinterpret_cast<float4*>(s_dl + o) = make_float4(vd[i], vd[i + 1], vd[i + 2], vd[i + 3]);
       *reinterpret_cast<float4*>(s_x + o) =
           make_float4(vd[i] * vu[i], vd[i + 1] * vu[i + 1], vd[i + 2] * vu[i + 2], vd[i + 3] * vu[i + 3]);
@@ -178,7 +190,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
     float y[kE];
 #pragma unroll
     for (int i = 0; i < kE; i += 4) {
-      const int o = (((eq * kE + i) >> 2) * kWave + er) * 4;
+      const int o = op_off<kSh>((eq * kE + i) >> 2, er);
       float4 acc = *reinterpret_cast<const float4*>(s_Y + kNW * kG * kWave * 4 + o);
 #pragma unroll
       for (int ww = 0; ww < kNW; ++ww) {
@@ -239,8 +251,9 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
     const int64_t t0 = tile * kT;
 #pragma unroll
     for (int g = 0; g < kG; ++g) {
-      const float4 dl4 = *reinterpret_cast<const float4*>(s_dl + (g * kWave + lane) * 4);
-      const float4 x4 = *reinterpret_cast<const float4*>(s_x + (g * kWave + lane) * 4);
+      const int og = op_off<kSh>(g, lane);
+      const float4 dl4 = *reinterpret_cast<const float4*>(s_dl + og);
+      const float4 x4 = *reinterpret_cast<const float4*>(s_x + og);
       float4 b4[kS], c4[kS];
 #pragma unroll
       for (int k = 0; k < kS; ++k) {
@@ -261,7 +274,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
         }
         y[i] = acc;
       }
-      *reinterpret_cast<float4*>(sYw + (g * kWave + lane) * 4) = make_float4(y[0], y[1], y[2], y[3]);
+      *reinterpret_cast<float4*>(sYw + og) = make_float4(y[0], y[1], y[2], y[3]);
       // checkpoints inside the tile; the one at the tile end is stored after
       // the barrier below, so that the wait before it does not wait for it
       if (ckp != nullptr && ((4 * g + 4) % kCk) == 0 && 4 * g + 4 < kT) store_ckpt(t0 + 4 * g + 4);
