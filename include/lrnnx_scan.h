@@ -4,9 +4,10 @@
  * The library (lrnnx_amd/liblrnnx_scan.so) replaces the two pybind11 torch
  * extensions of the reference, `selective_scan_cuda` and
  * `simplified_scan_cuda` (reference csrc/selective_scan/bindings.cpp:5-8,
- * csrc/simplified_scan/bindings.cpp:5-8), and the Triton decode kernel
- * `_selective_scan_update_kernel`
- * (lrnnx/ops/triton/selective_state_update.py:17-297).
+ * csrc/simplified_scan/bindings.cpp:5-8), and the Triton decode kernels
+ * `_selective_scan_update_kernel` and `_simplified_state_update_kernel`
+ * (lrnnx/ops/triton/selective_state_update.py:17-297,
+ * lrnnx/ops/triton/simplified_state_update.py:13-251).
  *
  * Conventions
  *  - Plain pointers and sizes only.  Every buffer (inputs, outputs and the
@@ -165,13 +166,42 @@ typedef struct lrnnx_state_update_args {
 
 int lrnnx_selective_state_update(const lrnnx_state_update_args *a, void *stream);
 
+/*
+ * One-token S5 decode update, in place on the complex state.
+ * state (b, P) complex64; x (b, H) f32; dt, deltaA (b, P) f32 (s0 = 0 for a
+ * (P,) vector shared by the batch); A (P) complex64; B (P, H) and C (H, P)
+ * complex64; D (H, H) f32 or NULL; out (b, H) f32.
+ *   A_bar = bilinear | exp(dtA A),  gamma = dt / (1 - dt A / 2) | (exp(dt A) - 1) / A | 1,
+ *   state = A_bar state + gamma (B @ x),
+ *   out   = (conj_sym ? 2 : 1) Re(C @ state) + x @ D^T.
+ * Strides in elements (complex elements for complex tensors).
+ * Replaces simplified_state_update
+ *   (reference lrnnx/ops/triton/simplified_state_update.py:254-401).
+ */
+typedef struct lrnnx_simplified_state_update_args {
+  int64_t batch, H, P;
+  int32_t method;          /* LRNNX_ZOH, LRNNX_BILINEAR or LRNNX_DIRAC */
+  int32_t conj_sym;
+  void *state; int64_t state_s0, state_s1;
+  const void *x; int64_t x_s0, x_s1;
+  const void *dt; int64_t dt_s0, dt_s1;
+  const void *A; int64_t A_s0;
+  const void *B; int64_t B_s0, B_s1;
+  const void *C; int64_t C_s0, C_s1;
+  const void *D; int64_t D_s0, D_s1;
+  const void *deltaA; int64_t dA_s0, dA_s1;
+  void *out; int64_t out_s0, out_s1;
+} lrnnx_simplified_state_update_args;
+
+int lrnnx_simplified_state_update(const lrnnx_simplified_state_update_args *a, void *stream);
+
 /* Last error message of this thread ("" if none). */
 const char *lrnnx_last_error(void);
 
 /* ABI version of this header (bumped on any struct change). */
 int lrnnx_abi_version(void);
 
-#define LRNNX_ABI_VERSION 1
+#define LRNNX_ABI_VERSION 2
 
 #ifdef __cplusplus
 }

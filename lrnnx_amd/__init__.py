@@ -7,6 +7,7 @@ Public API (same names, arguments and return conventions as the reference's
 * ``simplified_scan_fn`` / ``SimplifiedScanFn``, ``s5_inner_fn`` / ``S5InnerFn``
   (lrnnx/ops/simplified_scan.py)
 * ``selective_state_update``  (lrnnx/ops/triton/selective_state_update.py)
+* ``simplified_state_update``  (lrnnx/ops/triton/simplified_state_update.py)
 * ``selective_scan_cuda``, ``simplified_scan_cuda``: drop-in replacements of
   the reference's pybind11 extension modules (``fwd`` / ``bwd``).
 
@@ -17,4 +18,5 @@ include/lrnnx_scan.h).  There is no CPU fallback.
 from . import selective_scan_cuda, simplified_scan_cuda  # noqa: F401
 from .selective_scan import SelectiveScanFn, selective_scan_fn  # noqa: F401
 from .selective_state_update import selective_state_update  # noqa: F401
+from .simplified_state_update import simplified_state_update  # noqa: F401
 from .simplified_scan import S5InnerFn, SimplifiedScanFn, s5_inner_fn, simplified_scan_fn  # noqa: F401

@@ -70,6 +70,17 @@ class StateUpdateArgs(ctypes.Structure):
     )
 
 
+class SimplifiedStateUpdateArgs(ctypes.Structure):
+    _fields_ = (
+        [(n, c_i64) for n in ("batch", "H", "P")]
+        + [(n, c_i32) for n in ("method", "conj_sym")]
+        + _ptr_fields("state", 2) + _ptr_fields("x", 2) + _ptr_fields("dt", 2) + _ptr_fields("A", 1)
+        + _ptr_fields("B", 2) + _ptr_fields("C", 2) + _ptr_fields("D", 2)
+        + [("deltaA", c_vp), ("dA_s0", c_i64), ("dA_s1", c_i64)]
+        + _ptr_fields("out", 2)
+    )
+
+
 EXPORTS = (
     "lrnnx_selective_scan_ckpt_size",
     "lrnnx_selective_scan_workspace_size",
@@ -80,11 +91,12 @@ EXPORTS = (
     "lrnnx_simplified_scan_fwd",
     "lrnnx_simplified_scan_bwd",
     "lrnnx_selective_state_update",
+    "lrnnx_simplified_state_update",
     "lrnnx_last_error",
     "lrnnx_abi_version",
 )
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def lib():
@@ -114,9 +126,11 @@ def lib():
         L.lrnnx_simplified_scan_fwd.argtypes = [P(SimplifiedScanArgs), c_vp]
         L.lrnnx_simplified_scan_bwd.argtypes = [P(SimplifiedScanArgs), c_vp]
         L.lrnnx_selective_state_update.argtypes = [P(StateUpdateArgs), c_vp]
+        L.lrnnx_simplified_state_update.argtypes = [P(SimplifiedStateUpdateArgs), c_vp]
         L.lrnnx_last_error.restype = ctypes.c_char_p
         for fn in ("lrnnx_selective_scan_fwd", "lrnnx_selective_scan_bwd", "lrnnx_simplified_scan_fwd",
-                   "lrnnx_simplified_scan_bwd", "lrnnx_selective_state_update", "lrnnx_abi_version"):
+                   "lrnnx_simplified_scan_bwd", "lrnnx_selective_state_update",
+                   "lrnnx_simplified_state_update", "lrnnx_abi_version"):
             getattr(L, fn).restype = ctypes.c_int
         if L.lrnnx_abi_version() != ABI_VERSION:
             raise RuntimeError(f"lrnnx_amd: ABI version mismatch ({L.lrnnx_abi_version()} != {ABI_VERSION})")

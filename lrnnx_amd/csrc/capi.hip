@@ -43,6 +43,7 @@ hipError_t simp_bwd_launch(const lrnnx_simplified_scan_args&, hipStream_t);
 int64_t simp_ckpt_bytes(const lrnnx_simplified_scan_args&);
 int64_t simp_ws_bytes(const lrnnx_simplified_scan_args&, int);
 hipError_t state_update_launch(const lrnnx_state_update_args&, hipStream_t);
+hipError_t simp_state_update_launch(const lrnnx_simplified_state_update_args&, hipStream_t);
 
 // defined in ss_bwd_layout.hip (shares ss_bwd_ws with the backward units)
 int64_t ss_bwd_ws_bytes(const lrnnx_selective_scan_args&);
@@ -262,6 +263,19 @@ int lrnnx_selective_state_update(const lrnnx_state_update_args* a, void* stream)
   for (int t : {a->state_type, a->x_type, a->bc_type})
     if (t != LRNNX_F32 && t != LRNNX_F16 && t != LRNNX_BF16) return fail("unsupported dtype code %d", t);
   return from_hip(state_update_launch(*a, static_cast<hipStream_t>(stream)), "selective_state_update");
+}
+
+int lrnnx_simplified_state_update(const lrnnx_simplified_state_update_args* a, void* stream) {
+  if (!a) return fail("null argument struct");
+  if (a->method != LRNNX_ZOH && a->method != LRNNX_BILINEAR && a->method != LRNNX_DIRAC)
+    return fail("discretization must be one of ['bilinear', 'zoh', 'dirac']");
+  if (a->batch <= 0 || a->H <= 0 || a->P <= 0) return fail("empty or negative shape");
+  if (!a->state || !a->x || !a->dt || !a->A || !a->B || !a->C || !a->out)
+    return fail("state, x, dt, A, B, C, out are required");
+  // x staged in LDS together with the updated state
+  if ((a->H + 2 * a->P) * 4 > 64 * 1024) return fail("H + 2 P must fit 64 KiB of LDS (H=%lld, P=%lld)",
+                                                     (long long)a->H, (long long)a->P);
+  return from_hip(simp_state_update_launch(*a, static_cast<hipStream_t>(stream)), "simplified_state_update");
 }
 
 }  // extern "C"

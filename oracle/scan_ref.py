@@ -15,6 +15,7 @@ Reference anchors (paths relative to the reference checkout):
   simplified kernel (B*C out) csrc/simplified_scan/simplified_scan.cuh:172-246
   s5_inner_ref .............. lrnnx/ops/simplified_scan.py:586-640
   selective_state_update_ref  lrnnx/ops/triton/selective_state_update.py:479-599
+  simplified_state_update_ref lrnnx/ops/triton/simplified_state_update.py:404-469
   s7_scan_ref ............... lrnnx/ops/s7_scan.py:179-233
   rglru_scan_ref ............ lrnnx/ops/rglru_scan.py:148-203
 """
@@ -379,6 +380,52 @@ def selective_state_update_ref(state, x, dt, A, B, C, D=None, z=None, dt_bias=No
         out = out * F.silu(z_.to(rdt))
     out = out.to(x.dtype) if compute_dtype is None else out
     return out if has_heads else out.squeeze(1)
+
+
+def simplified_state_update_ref(state, x, dt, A, B, C, D=None, deltaA=None, discretization="bilinear",
+                                conj_sym=True, compute_dtype=None):
+    """Restatement of ``simplified_state_update_ref``
+    (simplified_state_update.py:404-469): one S5 decode step.
+
+    state (b, P) complex, updated in place (stored in its dtype); x (b, H)
+    real; dt, deltaA (b, P) or (P,) real (deltaA, if given, replaces dt in
+    A_bar only); A (P,) complex; B (P, H), C (H, P) complex; D (H, H) real.
+      A_bar = (1 + dtA A / 2) / (1 - dtA A / 2)  (bilinear) | exp(dtA A)
+      gamma = dt / (1 - dt A / 2) | (exp(dt A) - 1) / A (zoh) | 1 (dirac)
+      state = A_bar state + gamma (B @ x)
+      y = (2 if conj_sym else 1) Re(C @ state) + x @ D^T
+    """
+    rdt = _real(compute_dtype)
+    cdt = _cplx(compute_dtype)
+    batch, P = state.shape
+    dt_ = dt if dt.dim() == 2 else dt.unsqueeze(0).expand(batch, -1)
+    dtA = deltaA if deltaA is not None else dt
+    dtA = dtA if dtA.dim() == 2 else dtA.unsqueeze(0).expand(batch, -1)
+    dt_, dtA = dt_.to(rdt), dtA.to(rdt)
+    Ac = A.to(cdt)
+    disc = discretization.lower()
+    if disc == "bilinear":
+        hA = 0.5 * dtA * Ac
+        A_bar = (1.0 + hA) / (1.0 - hA)
+        gamma = dt_ / (1.0 - 0.5 * dt_ * Ac)
+    elif disc == "zoh":
+        A_bar = torch.exp(dtA * Ac)
+        gamma = (torch.exp(dt_ * Ac) - 1.0) / Ac
+    elif disc == "dirac":
+        A_bar = torch.exp(dtA * Ac)
+        gamma = torch.ones_like(dt_, dtype=cdt)
+    else:
+        raise ValueError(f"Unknown discretization: {discretization}")
+    Bu = torch.einsum("ph,bh->bp", B.to(cdt), x.to(cdt))
+    new = A_bar * state.to(cdt) + gamma * Bu
+    state.copy_(new.to(state.dtype))
+    stv = state.to(cdt) if compute_dtype is None else new
+    y = torch.einsum("hp,bp->bh", C.to(cdt), stv).real
+    if conj_sym:
+        y = 2.0 * y
+    if D is not None:
+        y = y + x.to(rdt) @ D.to(rdt).T
+    return y
 
 
 # ----------------------------------------------------------------------------

@@ -90,6 +90,29 @@ def state_update_case(name, method, seed=2):
     torch.save(rec, os.path.join(HERE, name + ".pt"))
 
 
+def simplified_state_update_case(name, method, seed, deltaA=False, D=True, dt_per_state=False):
+    g = torch.Generator().manual_seed(seed)
+    b, H, P = 3, 20, 12
+    cplx = lambda *shape: torch.complex(torch.randn(*shape, generator=g, dtype=D64),
+                                        torch.randn(*shape, generator=g, dtype=D64))
+    state = cplx(b, P)
+    x = torch.randn(b, H, generator=g, dtype=D64)
+    dt = 0.05 + 0.2 * torch.rand(*((P,) if dt_per_state else (b, P)), generator=g, dtype=D64)
+    A = torch.complex(-0.2 - torch.rand(P, generator=g, dtype=D64), torch.randn(P, generator=g, dtype=D64))
+    Bm, Cm = cplx(P, H) / H ** 0.5, cplx(H, P) / P ** 0.5
+    Dm = torch.randn(H, H, generator=g, dtype=D64) / H ** 0.5 if D else None
+    dA = 0.05 + 0.2 * torch.rand(b, P, generator=g, dtype=D64) if deltaA else None
+    st = state.clone()
+    out = R.simplified_state_update_ref(st, x, dt, A, Bm, Cm, Dm, dA, method, True, compute_dtype=D64)
+    inputs = dict(state=state, x=x, dt=dt, A=A, B=Bm, C=Cm)
+    if Dm is not None:
+        inputs["D"] = Dm
+    if dA is not None:
+        inputs["deltaA"] = dA
+    rec = {"inputs": inputs, "out": out, "state_after": st, "meta": {"method": method, "conj_sym": True}}
+    torch.save(rec, os.path.join(HERE, name + ".pt"))
+
+
 def main():
     selective_case("selective_mamba_var", "mamba")
     selective_case("selective_mamba_const_deltaA", "mamba", varB=False, varC=False, deltaA=True, seed=3)
@@ -105,6 +128,9 @@ def main():
     simplified_case("simplified_zoh_deltaA", "zoh", seed=12, deltaA=True)
     for m in ("mamba", "zoh", "bilinear", "dirac", "s7", "rglru"):
         state_update_case(f"state_update_{m}", m)
+    simplified_state_update_case("s5_state_update_bilinear", "bilinear", seed=15)
+    simplified_state_update_case("s5_state_update_zoh_deltaA", "zoh", seed=16, deltaA=True, dt_per_state=True)
+    simplified_state_update_case("s5_state_update_dirac_noD", "dirac", seed=17, D=False)
     print("golden fixtures written to", HERE)
 
 

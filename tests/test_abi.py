@@ -50,6 +50,9 @@ int main(void) {
          offsetof(lrnnx_simplified_scan_args, workspace_bytes));
   printf("%zu %zu %zu\n", offsetof(lrnnx_state_update_args, state), offsetof(lrnnx_state_update_args, deltaA),
          offsetof(lrnnx_state_update_args, out_s2));
+  printf("%zu %zu %zu %zu %zu\n", sizeof(lrnnx_simplified_state_update_args),
+         offsetof(lrnnx_simplified_state_update_args, state), offsetof(lrnnx_simplified_state_update_args, A_s0),
+         offsetof(lrnnx_simplified_state_update_args, deltaA), offsetof(lrnnx_simplified_state_update_args, out_s1));
   return 0;
 }
 '''
@@ -64,6 +67,9 @@ int main(void) {
     assert got[1].split() == [str(getattr(S, f).offset) for f in ("u", "x", "dout", "workspace", "dz")]
     assert got[2].split() == [str(getattr(M, f).offset) for f in ("x", "dout", "workspace_bytes")]
     assert got[3].split() == [str(getattr(U, f).offset) for f in ("state", "deltaA", "out_s2")]
+    Z = _lib.SimplifiedStateUpdateArgs
+    assert got[4].split() == [str(ctypes.sizeof(Z))] + [str(getattr(Z, f).offset)
+                                                        for f in ("state", "A_s0", "deltaA", "out_s1")]
 
 
 def _err():
@@ -100,6 +106,13 @@ def test_argument_checks_mirror_reference_messages():
     u.batch, u.nheads, u.dim, u.dstate, u.ngroups, u.method = 1, 3, 4, 4, 2, 3
     assert L.lrnnx_selective_state_update(u, None) != 0
     assert "divisible" in _err()
+    z = _lib.SimplifiedStateUpdateArgs()
+    z.batch, z.H, z.P, z.method = 1, 4, 4, _lib.METHODS["mamba"]
+    assert L.lrnnx_simplified_state_update(z, None) != 0
+    assert "discretization must be one of" in _err()
+    z.method = _lib.METHODS["zoh"]
+    assert L.lrnnx_simplified_state_update(z, None) != 0   # null tensors
+    assert "required" in _err()
 
 
 def test_python_api_refuses_cpu_tensors():
@@ -113,6 +126,18 @@ def test_python_api_refuses_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU only"):
         selective_scan_cuda.fwd(u, u.clone(), A, B[:, None], B[:, None].clone(), None, None, None, None, False,
                                 "mamba")
+
+
+def test_simplified_state_update_refuses_cpu_tensors():
+    from lrnnx_amd import simplified_state_update
+
+    st = torch.zeros(2, 3, dtype=torch.complex64)
+    A = torch.zeros(3, dtype=torch.complex64)
+    B = torch.zeros(3, 4, dtype=torch.complex64)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        simplified_state_update(st, torch.zeros(2, 4), torch.ones(3), A, B, B.T.contiguous())
+    with pytest.raises(AssertionError):   # the reference's shape assertions
+        simplified_state_update(st, torch.zeros(2, 5), torch.ones(3), A, B, B.T.contiguous())
 
 
 def test_workspace_queries_are_host_only():

@@ -17,6 +17,7 @@ HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 SEL = sorted(glob.glob(os.path.join(HERE, "selective_*.pt")))
 SIMP = sorted(glob.glob(os.path.join(HERE, "simplified_*.pt")))
 SU = sorted(glob.glob(os.path.join(HERE, "state_update_*.pt")))
+S5U = sorted(glob.glob(os.path.join(HERE, "s5_state_update_*.pt")))
 
 
 def _load(p):
@@ -60,6 +61,16 @@ def test_oracle_reproduces_state_update_fixture(path):
     st = i["state"].clone()
     out = R.selective_state_update_ref(st, i["x"], i["dt"], i["A"], i["B"], i["C"], i["D"], i["z"], i["dt_bias"],
                                        True, None, rec["meta"]["method"], compute_dtype=torch.float64)
+    assert torch.equal(out, rec["out"]) and torch.equal(st, rec["state_after"])
+
+
+@pytest.mark.parametrize("path", S5U, ids=[os.path.basename(p) for p in S5U])
+def test_oracle_reproduces_s5_state_update_fixture(path):
+    rec = _load(path)
+    i = rec["inputs"]
+    st = i["state"].clone()
+    out = R.simplified_state_update_ref(st, i["x"], i["dt"], i["A"], i["B"], i["C"], i.get("D"), i.get("deltaA"),
+                                        rec["meta"]["method"], rec["meta"]["conj_sym"], compute_dtype=torch.float64)
     assert torch.equal(out, rec["out"]) and torch.equal(st, rec["state_after"])
 
 
@@ -113,6 +124,21 @@ def test_kernel_matches_state_update_fixture(dev, path):
     st = i["state"].clone()
     out = selective_state_update(st, i["x"], i["dt"], i["A"], i["B"], i["C"], i["D"], i["z"], i["dt_bias"], True,
                                  None, None, rec["meta"]["method"])
+    torch.cuda.synchronize()
+    close("out", out, rec["out"], 1e-4, 1e-5)
+    close("state", st, rec["state_after"], 1e-4, 1e-5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", S5U, ids=[os.path.basename(p) for p in S5U])
+def test_kernel_matches_s5_state_update_fixture(dev, path):
+    from lrnnx_amd import simplified_state_update
+
+    rec = _load(path)
+    i = {k: _f32(v, dev) for k, v in rec["inputs"].items()}
+    st = i["state"].clone()
+    out = simplified_state_update(st, i["x"], i["dt"], i["A"], i["B"], i["C"], i.get("D"), i.get("deltaA"),
+                                  rec["meta"]["method"], rec["meta"]["conj_sym"])
     torch.cuda.synchronize()
     close("out", out, rec["out"], 1e-4, 1e-5)
     close("state", st, rec["state_after"], 1e-4, 1e-5)

@@ -260,3 +260,63 @@ def test_s7_and_rglru_wrapper_refs_match_kernel_semantics():
     onesH = torch.ones(H, n, dtype=D64)
     y2k = R.selective_scan_ref(u2, dl, Ar, onesH, onesH, discretization="rglru", compute_dtype=D64)
     assert torch.allclose(y2, y2k, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("method", ["bilinear", "zoh", "dirac"])
+@pytest.mark.parametrize("use_deltaA", [False, True])
+@pytest.mark.parametrize("conj_sym", [True, False])
+def test_simplified_state_update_loop_equals_s5_scan(method, use_deltaA, conj_sym):
+    # L decode steps from the zero state == s5_inner_ref over the sequence
+    # (the decode's dense D (H, H) taken diagonal, as s5_inner's D (H,))
+    g = torch.Generator().manual_seed(13)
+    b, H, P, L = 2, 5, 3, 9
+    A = torch.complex(-0.5 - torch.rand(P, generator=g, dtype=D64), torch.randn(P, generator=g, dtype=D64))
+    Bm = torch.complex(torch.randn(P, H, generator=g, dtype=D64), torch.randn(P, H, generator=g, dtype=D64))
+    Cm = torch.complex(torch.randn(H, P, generator=g, dtype=D64), torch.randn(H, P, generator=g, dtype=D64))
+    u = torch.randn(b, H, L, generator=g, dtype=D64)
+    delta = 0.05 + 0.2 * torch.rand(b, P, L, generator=g, dtype=D64)
+    dA = 0.05 + 0.2 * torch.rand(b, P, L, generator=g, dtype=D64) if use_deltaA else None
+    Dv = torch.randn(H, generator=g, dtype=D64)
+    uc = torch.complex(u, torch.zeros_like(u))   # the scan takes complex u; Re(u) = x
+    full = R.s5_inner_ref(uc, delta, A, Bm, Cm, Dv, deltaA=dA, discretization=method, conj_sym=conj_sym,
+                          compute_dtype=D64)
+    state = torch.zeros(b, P, dtype=torch.complex128)
+    outs = [R.simplified_state_update_ref(state, u[..., t], delta[..., t], A, Bm, Cm, torch.diag(Dv),
+                                          None if dA is None else dA[..., t], method, conj_sym, compute_dtype=D64)
+            for t in range(L)]
+    assert torch.allclose(torch.stack(outs, -1), full, rtol=1e-12, atol=1e-12)
+
+
+def test_simplified_state_update_scalar_step():
+    # one step against scalar complex arithmetic (cmath), with a dense D and
+    # dt given per state (P,) broadcast over the batch
+    import cmath
+    g = torch.Generator().manual_seed(14)
+    b, H, P = 2, 3, 2
+    A = torch.complex(-torch.rand(P, generator=g, dtype=D64), torch.randn(P, generator=g, dtype=D64))
+    Bm = torch.complex(torch.randn(P, H, generator=g, dtype=D64), torch.randn(P, H, generator=g, dtype=D64))
+    Cm = torch.complex(torch.randn(H, P, generator=g, dtype=D64), torch.randn(H, P, generator=g, dtype=D64))
+    st0 = torch.complex(torch.randn(b, P, generator=g, dtype=D64), torch.randn(b, P, generator=g, dtype=D64))
+    x = torch.randn(b, H, generator=g, dtype=D64)
+    dt = 0.1 + torch.rand(P, generator=g, dtype=D64)
+    Dm = torch.randn(H, H, generator=g, dtype=D64)
+    for method in ("bilinear", "zoh", "dirac"):
+        st = st0.clone()
+        y = R.simplified_state_update_ref(st, x, dt, A, Bm, Cm, Dm, None, method, True, compute_dtype=D64)
+        for bi in range(b):
+            new = []
+            for p in range(P):
+                a, d = complex(A[p]), float(dt[p])
+                if method == "bilinear":
+                    ab, gam = (1 + 0.5 * d * a) / (1 - 0.5 * d * a), d / (1 - 0.5 * d * a)
+                elif method == "zoh":
+                    ab, gam = cmath.exp(d * a), (cmath.exp(d * a) - 1) / a
+                else:
+                    ab, gam = cmath.exp(d * a), 1.0
+                bu = sum(complex(Bm[p, h]) * float(x[bi, h]) for h in range(H))
+                new.append(ab * complex(st0[bi, p]) + gam * bu)
+                assert abs(new[-1] - complex(st[bi, p])) < 1e-12
+            for h in range(H):
+                yy = 2 * sum(complex(Cm[h, p]) * new[p] for p in range(P)).real
+                yy += sum(float(Dm[h, k]) * float(x[bi, k]) for k in range(H))
+                assert abs(yy - float(y[bi, h])) < 1e-12
