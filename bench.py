@@ -114,6 +114,58 @@ class SelectiveStep:
         self.L.check(self.L.lib().lrnnx_selective_scan_bwd(self.args, self.stream.cuda_stream), "bwd")
 
 
+class LRUStep:
+    """Config 1 (LRU, complex64): simplified scan fwd + bwd at the reference
+    boundary (dirac, delta = 1 broadcast along L, A = log Lambda, identity B/C),
+    with every output and workspace preallocated (no allocation in the timed
+    loop).  Algorithmic bytes: fwd reads Bu and writes h; bwd reads dh and Bu,
+    writes dBu (8 bytes per complex element each)."""
+
+    def __init__(self, dev, torch, L_, Bt, P, L, seed=1):
+        from lrnnx_amd import simplified_scan_cuda as sc
+        self.L_ = L_
+        g = torch.Generator(device=dev).manual_seed(seed)
+        r = 0.9 + 0.099 * torch.rand(P, device=dev, generator=g)
+        th = (math.pi / 10) * torch.rand(P, device=dev, generator=g)
+        lam = torch.polar(r, th)
+        cn = lambda: torch.complex(torch.randn(Bt, P, L, device=dev, generator=g),
+                                   torch.randn(Bt, P, L, device=dev, generator=g)) / math.sqrt(2.0)
+        self.Bu, self.dh = cn(), cn()
+        A = torch.log(lam).unsqueeze(-1).to(torch.complex64)
+        ones = torch.ones(P, 1, dtype=torch.complex64, device=dev)
+        delta = torch.ones(1, 1, 1, device=dev).expand(Bt, P, L)
+        self.keep = (A, ones, delta)
+        self.fa = sc.build_args(self.Bu, delta, A, ones, ones, None, "dirac")
+        self.out = torch.empty_like(self.Bu)
+        self.x = torch.empty((Bt, P, (L + 2047) // 2048, 2), dtype=torch.complex64, device=dev)
+        self.fa.out = L_.view(self.out, 2)
+        self.fa.x = self.x.data_ptr()
+        nck = L_.lib().lrnnx_simplified_scan_ckpt_size(self.fa)
+        self.ckpt = torch.empty(max(nck, 8) // 8, dtype=torch.complex64, device=dev)
+        self.fa.ckpt = self.ckpt.data_ptr()
+        nws = max(L_.lib().lrnnx_simplified_scan_workspace_size(self.fa, 0), 256)
+        self.wsf = torch.empty(nws, dtype=torch.uint8, device=dev)
+        self.fa.workspace, self.fa.workspace_bytes = self.wsf.data_ptr(), nws
+        self.ba = sc.build_args(self.Bu, delta, A, ones, ones, None, "dirac")
+        self.du = torch.empty_like(self.Bu)
+        self.dA, self.dB, self.dC = (torch.empty_like(A) for _ in range(3))
+        self.ba.need_ddelta = 0
+        self.ba.dout = L_.view(self.dh, 2)
+        self.ba.du = L_.view(self.du, 2)
+        self.ba.dA, self.ba.dB, self.ba.dC = L_.view(self.dA, 2), L_.view(self.dB, 2), L_.view(self.dC, 2)
+        self.ba.ckpt = self.ckpt.data_ptr()
+        nwb = max(L_.lib().lrnnx_simplified_scan_workspace_size(self.ba, 1), 256)
+        self.wsb = torch.empty(nwb, dtype=torch.uint8, device=dev)
+        self.ba.workspace, self.ba.workspace_bytes = self.wsb.data_ptr(), nwb
+        self.stream = torch.cuda.current_stream(dev)
+
+    def fwd(self):
+        self.L_.check(self.L_.lib().lrnnx_simplified_scan_fwd(self.fa, self.stream.cuda_stream), "lru fwd")
+
+    def bwd(self):
+        self.L_.check(self.L_.lib().lrnnx_simplified_scan_bwd(self.ba, self.stream.cuda_stream), "lru bwd")
+
+
 def time_steps(step, torch, steps, warmup):
     for _ in range(warmup):
         step.fwd()
@@ -172,7 +224,6 @@ def cpu_baseline(torch, R, D_slice=8, Bt=8, L=4096, N=16, D_full=4096):
 def other_configs(torch, ss, L_, dev):
     """Config 2 (Mamba-130m layer, fwd+bwd) and config 1 (LRU complex scan,
     fwd+bwd) timings, reported beside the headline line."""
-    from oracle import scan_ref as R  # noqa: F401  (inputs only)
     res = {}
     inp = make_cfg3(dev, torch, None, Bt=8, D=1536, L=2048, N=16, seed=2)
     st = SelectiveStep(inp, torch, ss, L_)
@@ -183,99 +234,104 @@ def other_configs(torch, ss, L_, dev):
                                      "pct_hbm": round(100 * (fb + bb) / t / 1e9 / HBM_PEAK_GBS, 2),
                                      "elem_per_s": round(8 * 1536 * 2048 / t, 1)}
     del st, inp
-    # config 1: simplified scan, dirac, delta = 1 broadcast, identity B/C
-    from lrnnx_amd import simplified_scan_cuda as sc
+    # config 1: simplified scan, dirac, delta = 1 broadcast, identity B/C,
+    # preallocated outputs / workspace, straight through the C ABI
     Bt, P, L = 8, 256, 4096
-    g = torch.Generator(device=dev).manual_seed(1)
-    r = 0.9 + 0.099 * torch.rand(P, device=dev, generator=g)
-    th = (math.pi / 10) * torch.rand(P, device=dev, generator=g)
-    lam = torch.polar(r, th)
-    Bu = torch.complex(torch.randn(Bt, P, L, device=dev, generator=g),
-                       torch.randn(Bt, P, L, device=dev, generator=g)) / math.sqrt(2.0)
-    dh = torch.complex(torch.randn(Bt, P, L, device=dev, generator=g),
-                       torch.randn(Bt, P, L, device=dev, generator=g)) / math.sqrt(2.0)
-    A = torch.log(lam).unsqueeze(-1).to(torch.complex64)
-    ones = torch.ones(P, 1, dtype=torch.complex64, device=dev)
-    delta = torch.ones(1, 1, 1, device=dev).expand(Bt, P, L)
-    a = sc.build_args(Bu, delta, A, ones, ones, None, "dirac")
-    out, x, ck = sc.run_fwd(a, Bu, want_ckpt=True)
-
-    def step():
-        sc.run_fwd(a, Bu, want_ckpt=False)
-        sc.run_bwd(a, Bu, delta, A, ones, ones, None, dh, ck, need_ddelta=False)
-
-    for _ in range(3):
-        step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    n = 10
-    for _ in range(n):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) / n * 1e-3
+    st = LRUStep(dev, torch, L_, Bt, P, L)
+    tot, f, b = time_steps(st, torch, 20, 3)
     alg = Bt * P * L * 8 * 2 + Bt * P * L * 8 * 3
-    res["cfg1_lru_fwd_bwd"] = {"ms": round(t * 1e3, 4), "GB_s": round(alg / t / 1e9, 1),
+    t = (f[len(f) // 2] + b[len(b) // 2]) * 1e-3
+    res["cfg1_lru_fwd_bwd"] = {"ms": round(t * 1e3, 4), "fwd_ms": round(f[len(f) // 2], 4),
+                               "bwd_ms": round(b[len(b) // 2], 4), "GB_s": round(alg / t / 1e9, 1),
                                "pct_hbm": round(100 * alg / t / 1e9 / HBM_PEAK_GBS, 2),
                                "elem_per_s": round(Bt * P * L / t, 1),
-                               "note": "includes per-call workspace/output allocation by the torch caching allocator"}
+                               "alg_bytes": alg}
     return res
 
 
 COPY_CALIB_BYTES = 1 << 30
+TRAFFIC_TAGS = ("ssf_bwd_kernel", "ssf_fwd_kernel", "ss_reduce_bc4_kernel", "ss_reduce_batch_kernel")
 
 
-def traffic_from_counters(fetch_csv, write_csv):
-    """HBM bytes per launch of the headline kernels from rocprofv3 --pmc runs.
-
-    FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are scaled by what the same
-    counter reads for the plain copy of --copy-calib (COPY_CALIB_BYTES read and
-    written), so the result is in bytes of HBM traffic.
+def traffic_from_counters(read_csv, write_csv):
+    """HBM-side bytes per launch of the headline kernels from two rocprofv3
+    --pmc runs of ``bench.py --copy-calib``:
+      read pass : TCC_EA0_RDREQ TCC_EA0_RDREQ_32B TCC_EA0_RDREQ_64B TCC_EA0_RDREQ_128B
+      write pass: TCC_EA0_WRREQ TCC_EA0_WRREQ_64B
+    (requests from the L2 to the memory fabric, per dispatch, summed over
+    the L2 instances).  Bytes = 32 n32 + 64 n64 + 128 n128 for reads and
+    64 n64 + 32 (n - n64) for writes.  The plain 1 GiB copy of --copy-calib
+    checks the byte conversion: its read and write bytes over 1 GiB are
+    reported as the calibration factors (they come out at 1.00).
     """
     import csv
-    import re
 
-    def load(path, counter):
+    def load(path):
         per = {}
         with open(path) as fh:
             for row in csv.DictReader(fh):
-                if row.get("Counter_Name") != counter:
-                    continue
-                name = row.get("Kernel_Name", "")
-                per.setdefault(name, []).append(float(row["Counter_Value"]))
+                key = (row["Dispatch_Id"], row.get("Kernel_Name", ""))
+                per.setdefault(key, {})[row["Counter_Name"]] = float(row["Counter_Value"])
         return per
 
-    out = {}
-    for key, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
-        per = load(path, counter)
-        copy = [v for k, vs in per.items() if re.search(r"copy|elementwise", k, re.I) for v in vs]
-        if not copy:
-            raise SystemExit(f"no copy kernel in {path}")
-        scale = COPY_CALIB_BYTES / (max(copy) * 1024.0)
-        for k, vs in per.items():
-            for tag in ("ss_bwd_kernel", "ss_fwd_kernel", "ss_reduce_bc_kernel", "ss_reduce_batch_kernel"):
-                if tag in k:
-                    ent = out.setdefault(tag, {})
-                    ent.setdefault(key, []).extend(v * 1024.0 * scale for v in vs)
-        out.setdefault("calibration", {})[key] = {"copy_counter_kib": max(copy), "scale": scale}
-    summary = {"calibration": out.pop("calibration")}
-    for tag, ent in out.items():
-        f = ent.get("fetch", [])
-        w = ent.get("write", [])
-        summary[tag] = {"fetch_bytes_per_launch": sum(f) / len(f) if f else None,
-                        "write_bytes_per_launch": sum(w) / len(w) if w else None, "launches": len(f)}
-    bwd = [summary.get(t) for t in ("ss_bwd_kernel",)]
-    if bwd[0] and bwd[0]["fetch_bytes_per_launch"] is not None:
-        red = summary.get("ss_reduce_bc_kernel", {})
-        tot = bwd[0]["fetch_bytes_per_launch"] + bwd[0]["write_bytes_per_launch"]
-        if red.get("fetch_bytes_per_launch") is not None:
-            tot += 2 * (red["fetch_bytes_per_launch"] + red["write_bytes_per_launch"])  # dB and dC launches
-        summary["bwd_bytes_per_launch"] = tot
+    rd, wr = load(read_csv), load(write_csv)
+
+    def rbytes(c):
+        n32, n64, n128 = c.get("TCC_EA0_RDREQ_32B", 0.0), c.get("TCC_EA0_RDREQ_64B", 0.0), c.get("TCC_EA0_RDREQ_128B", 0.0)
+        return 32 * n32 + 64 * n64 + 128 * n128
+
+    def wbytes(c):
+        n, n64 = c.get("TCC_EA0_WRREQ", 0.0), c.get("TCC_EA0_WRREQ_64B", 0.0)
+        return 64 * n64 + 32 * (n - n64)
+
+    copy_r = max((rbytes(c) for (d, k), c in rd.items() if "MulFunctor" in k), default=None)
+    copy_w = max((wbytes(c) for (d, k), c in wr.items() if "MulFunctor" in k), default=None)
+    if copy_r is None or copy_w is None:
+        raise SystemExit("no copy-calibration kernel in the counter files (run bench.py --copy-calib)")
+    out = {"calibration": {"copy_bytes": COPY_CALIB_BYTES, "read_factor": copy_r / COPY_CALIB_BYTES,
+                           "write_factor": copy_w / COPY_CALIB_BYTES}}
+    for tag in TRAFFIC_TAGS:
+        r = [rbytes(c) for (d, k), c in rd.items() if tag in k]
+        w = [wbytes(c) for (d, k), c in wr.items() if tag in k]
+        if r and w:
+            out[tag] = {"read_bytes_per_launch": sum(r) / len(r), "write_bytes_per_launch": sum(w) / len(w),
+                        "launches": len(r)}
+    bw = out.get("ssf_bwd_kernel")
+    if bw:
+        tot = bw["read_bytes_per_launch"] + bw["write_bytes_per_launch"]
+        for t, per_step in (("ss_reduce_bc4_kernel", 1), ("ss_reduce_batch_kernel", 3)):
+            if t in out:
+                tot += per_step * (out[t]["read_bytes_per_launch"] + out[t]["write_bytes_per_launch"])
+        out["bwd_bytes_per_launch"] = tot
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_cfg3.json")
     with open(path, "w") as fh:
-        json.dump(summary, fh, indent=1)
-    print(json.dumps(summary, indent=1))
+        json.dump(out, fh, indent=1)
+    print(json.dumps(out, indent=1))
+
+
+def summarize_trace(trace_csv):
+    """Markdown table of a rocprofv3 --kernel-trace CSV of this bench: the
+    library's kernels grouped by (kernel, grid), with calls, mean / median /
+    min / max duration in microseconds (torch's input-generation kernels left
+    out)."""
+    import csv
+    import re
+
+    groups = {}
+    with open(trace_csv) as fh:
+        for row in csv.DictReader(fh):
+            name = row["Kernel_Name"]
+            if "lrnnx::" not in name:
+                continue
+            short = re.sub(r"\(lrnnx_.*$|\(float const\*.*$", "", name).replace("void ", "")
+            grid = "x".join(row[f"Grid_Size_{a}"] for a in "XYZ")
+            dur = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) * 1e-3
+            groups.setdefault((short, grid), []).append(dur)
+    print("| kernel | grid (threads) | calls | mean (us) | median (us) | min (us) | max (us) |")
+    print("|---|---|---|---|---|---|---|")
+    for (k, g), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        m = sorted(v)[len(v) // 2]
+        print(f"| `{k}` | {g} | {len(v)} | {sum(v) / len(v):.1f} | {m:.1f} | {min(v):.1f} | {max(v):.1f} |")
 
 
 def main():
@@ -287,10 +343,15 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip configs 1 and 2")
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run a plain 1 GiB device copy (reference kernel for HBM byte counters)")
-    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+    ap.add_argument("--traffic-from", nargs=2, metavar=("READ_CSV", "WRITE_CSV"),
                     help="write profiles/traffic_cfg3.json from two rocprofv3 --pmc counter_collection.csv "
-                         "files (FETCH_SIZE, WRITE_SIZE) of a --copy-calib run, then exit")
+                         "files (TCC_EA0_RDREQ*, TCC_EA0_WRREQ*) of a --copy-calib run, then exit")
+    ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
+                    help="print a markdown summary of a rocprofv3 --kernel-trace CSV of this bench, then exit")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.traffic_from:
         traffic_from_counters(*args.traffic_from)
         return
@@ -363,7 +424,7 @@ def main():
         "fwd_ms_median": round(f_med, 4),
         "bwd_ms_median": round(b_med, 4),
         "alg_bytes": {"fwd": fb, "bwd": bb},
-        "roofline": {"bound": "hbm", "kernel": "lrnnx_selective_scan_bwd (ss_bwd_kernel + dB/dC/dA reductions)",
+        "roofline": {"bound": "hbm", "kernel": "lrnnx_selective_scan_bwd (ssf_bwd_kernel + dB/dC, dA/dD/ddelta_bias reductions)",
                      "achieved": round(bwd_achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(bwd_achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "fwd_achieved": round(fb / (f_avg * 1e-3) / 1e9, 2)},
