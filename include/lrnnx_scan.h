@@ -195,13 +195,48 @@ typedef struct lrnnx_simplified_state_update_args {
 
 int lrnnx_simplified_state_update(const lrnnx_simplified_state_update_args *a, void *stream);
 
+/*
+ * Depthwise causal conv1d (the short convolution of the Mamba block), the
+ * operator of the causal-conv1d package that lrnnx calls (pyproject.toml:33,
+ * optional dependency; lrnnx/models/ltv/mamba.py:274, :411 and
+ * lrnnx/ops/selective_scan.py:448, :640).  Semantics are the reference's own
+ * fallback (mamba.py:271, :398-410):
+ *   out[b,d,t] = act(bias[d] + sum_{k<W} weight[d,k] x[b,d,t-W+1+k]),  x[t<0] = 0,
+ *   act = silu if `silu` else identity.
+ * x, out, dout, dx, conv_state in `itype` (f32 / f16 / bf16); weight (dim,
+ * width), bias (dim), dweight, dbias in f32.  width 1..8.  x / out / dout / dx
+ * views: s0 batch, s1 channel, s2 step (must be 1 for fwd / bwd).
+ * Update: conv_state (batch, dim, state_len >= width - 1) holds the last
+ * state_len inputs and is shifted in place; x (batch, dim, seqlen) are the
+ * new inputs (seqlen usually 1).
+ */
+typedef struct lrnnx_causal_conv1d_args {
+  int64_t batch, dim, seqlen, width, state_len;
+  int32_t itype;
+  int32_t silu;
+  lrnnx_view x, weight, bias, out;
+  lrnnx_view dout, dx, dweight, dbias;
+  lrnnx_view conv_state;
+  void *workspace;                 /* backward: >= lrnnx_causal_conv1d_workspace_size() bytes */
+  int64_t workspace_bytes;
+} lrnnx_causal_conv1d_args;
+
+/* Replaces causal_conv1d_fwd_function (x, weight, bias, None, None, None, silu). */
+int lrnnx_causal_conv1d_fwd(const lrnnx_causal_conv1d_args *a, void *stream);
+int64_t lrnnx_causal_conv1d_workspace_size(const lrnnx_causal_conv1d_args *a);
+/* Replaces causal_conv1d_bwd_function (x, weight, bias, dout, None, None, None, dx, False, silu):
+ * writes dx, dweight, dbias (if bias given). */
+int lrnnx_causal_conv1d_bwd(const lrnnx_causal_conv1d_args *a, void *stream);
+/* Replaces causal_conv1d_update (x, conv_state, weight, bias, activation). */
+int lrnnx_causal_conv1d_update(const lrnnx_causal_conv1d_args *a, void *stream);
+
 /* Last error message of this thread ("" if none). */
 const char *lrnnx_last_error(void);
 
 /* ABI version of this header (bumped on any struct change). */
 int lrnnx_abi_version(void);
 
-#define LRNNX_ABI_VERSION 2
+#define LRNNX_ABI_VERSION 3
 
 #ifdef __cplusplus
 }

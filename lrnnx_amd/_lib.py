@@ -81,6 +81,15 @@ class SimplifiedStateUpdateArgs(ctypes.Structure):
     )
 
 
+class CausalConv1dArgs(ctypes.Structure):
+    _fields_ = (
+        [(n, c_i64) for n in ("batch", "dim", "seqlen", "width", "state_len")]
+        + [(n, c_i32) for n in ("itype", "silu")]
+        + [(n, View) for n in ("x", "weight", "bias", "out", "dout", "dx", "dweight", "dbias", "conv_state")]
+        + [("workspace", c_vp), ("workspace_bytes", c_i64)]
+    )
+
+
 EXPORTS = (
     "lrnnx_selective_scan_ckpt_size",
     "lrnnx_selective_scan_workspace_size",
@@ -92,11 +101,15 @@ EXPORTS = (
     "lrnnx_simplified_scan_bwd",
     "lrnnx_selective_state_update",
     "lrnnx_simplified_state_update",
+    "lrnnx_causal_conv1d_fwd",
+    "lrnnx_causal_conv1d_bwd",
+    "lrnnx_causal_conv1d_update",
+    "lrnnx_causal_conv1d_workspace_size",
     "lrnnx_last_error",
     "lrnnx_abi_version",
 )
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def lib():
@@ -127,6 +140,11 @@ def lib():
         L.lrnnx_simplified_scan_bwd.argtypes = [P(SimplifiedScanArgs), c_vp]
         L.lrnnx_selective_state_update.argtypes = [P(StateUpdateArgs), c_vp]
         L.lrnnx_simplified_state_update.argtypes = [P(SimplifiedStateUpdateArgs), c_vp]
+        for fn in ("lrnnx_causal_conv1d_fwd", "lrnnx_causal_conv1d_bwd", "lrnnx_causal_conv1d_update"):
+            getattr(L, fn).argtypes = [P(CausalConv1dArgs), c_vp]
+            getattr(L, fn).restype = ctypes.c_int
+        L.lrnnx_causal_conv1d_workspace_size.argtypes = [P(CausalConv1dArgs)]
+        L.lrnnx_causal_conv1d_workspace_size.restype = c_i64
         L.lrnnx_last_error.restype = ctypes.c_char_p
         for fn in ("lrnnx_selective_scan_fwd", "lrnnx_selective_scan_bwd", "lrnnx_simplified_scan_fwd",
                    "lrnnx_simplified_scan_bwd", "lrnnx_selective_state_update",

@@ -44,6 +44,7 @@ int64_t simp_ckpt_bytes(const lrnnx_simplified_scan_args&);
 int64_t simp_ws_bytes(const lrnnx_simplified_scan_args&, int);
 hipError_t state_update_launch(const lrnnx_state_update_args&, hipStream_t);
 hipError_t simp_state_update_launch(const lrnnx_simplified_state_update_args&, hipStream_t);
+hipError_t cconv_launch(const lrnnx_causal_conv1d_args&, int, float*, hipStream_t);
 
 // defined in ss_bwd_layout.hip (shares ss_bwd_ws with the backward units)
 int64_t ss_bwd_ws_bytes(const lrnnx_selective_scan_args&);
@@ -263,6 +264,49 @@ int lrnnx_selective_state_update(const lrnnx_state_update_args* a, void* stream)
   for (int t : {a->state_type, a->x_type, a->bc_type})
     if (t != LRNNX_F32 && t != LRNNX_F16 && t != LRNNX_BF16) return fail("unsupported dtype code %d", t);
   return from_hip(state_update_launch(*a, static_cast<hipStream_t>(stream)), "selective_state_update");
+}
+
+static int check_cconv(const lrnnx_causal_conv1d_args* a, int which) {
+  if (!a) return fail("null argument struct");
+  if (a->itype != LRNNX_F32 && a->itype != LRNNX_F16 && a->itype != LRNNX_BF16)
+    return fail("x must be float32, float16 or bfloat16");
+  if (a->width < 1 || a->width > 8) return fail("causal_conv1d: width must be between 1 and 8 (got %lld)",
+                                                (long long)a->width);
+  if (a->batch <= 0 || a->dim <= 0 || a->seqlen <= 0) return fail("empty or negative shape");
+  if (!a->x.ptr || !a->weight.ptr || !a->out.ptr) return fail("x, weight, out are required");
+  if (which != 2 && a->x.s2 != 1) return fail("causal_conv1d: x must have unit stride along the sequence");
+  if (which == 1) {
+    if (!a->dout.ptr || !a->dx.ptr || !a->dweight.ptr) return fail("dout, dx, dweight are required");
+    if (a->dout.s2 != 1 || a->dx.s2 != 1) return fail("causal_conv1d: dout / dx must have unit stride along the sequence");
+    if (a->bias.ptr && !a->dbias.ptr) return fail("dbias is required when bias is given");
+    if (!a->workspace || a->workspace_bytes < lrnnx_causal_conv1d_workspace_size(a))
+      return fail("workspace too small");
+  }
+  if (which == 2) {
+    if (!a->conv_state.ptr) return fail("conv_state is required");
+    if (a->state_len < a->width - 1) return fail("conv_state must hold at least width - 1 steps");
+  }
+  return 0;
+}
+
+int64_t lrnnx_causal_conv1d_workspace_size(const lrnnx_causal_conv1d_args* a) {
+  return a ? a->batch * a->dim * (a->width + 1) * (int64_t)sizeof(float) : -1;
+}
+
+int lrnnx_causal_conv1d_fwd(const lrnnx_causal_conv1d_args* a, void* stream) {
+  if (check_cconv(a, 0)) return 1;
+  return from_hip(cconv_launch(*a, 0, nullptr, static_cast<hipStream_t>(stream)), "causal_conv1d_fwd");
+}
+
+int lrnnx_causal_conv1d_bwd(const lrnnx_causal_conv1d_args* a, void* stream) {
+  if (check_cconv(a, 1)) return 1;
+  return from_hip(cconv_launch(*a, 1, static_cast<float*>(a->workspace), static_cast<hipStream_t>(stream)),
+                  "causal_conv1d_bwd");
+}
+
+int lrnnx_causal_conv1d_update(const lrnnx_causal_conv1d_args* a, void* stream) {
+  if (check_cconv(a, 2)) return 1;
+  return from_hip(cconv_launch(*a, 2, nullptr, static_cast<hipStream_t>(stream)), "causal_conv1d_update");
 }
 
 int lrnnx_simplified_state_update(const lrnnx_simplified_state_update_args* a, void* stream) {

@@ -16,6 +16,9 @@ Reference anchors (paths relative to the reference checkout):
   s5_inner_ref .............. lrnnx/ops/simplified_scan.py:586-640
   selective_state_update_ref  lrnnx/ops/triton/selective_state_update.py:479-599
   simplified_state_update_ref lrnnx/ops/triton/simplified_state_update.py:404-469
+  causal_conv1d_ref ......... lrnnx/models/ltv/mamba.py:271 (nn.Conv1d fallback of causal_conv1d_fn)
+  causal_conv1d_update_ref .. lrnnx/models/ltv/mamba.py:398-410 (roll-and-sum fallback of causal_conv1d_update)
+  mamba_inner_ref ........... lrnnx/ops/selective_scan.py:789-846
   s7_scan_ref ............... lrnnx/ops/s7_scan.py:179-233
   rglru_scan_ref ............ lrnnx/ops/rglru_scan.py:148-203
 """
@@ -426,6 +429,91 @@ def simplified_state_update_ref(state, x, dt, A, B, C, D=None, deltaA=None, disc
     if D is not None:
         y = y + x.to(rdt) @ D.to(rdt).T
     return y
+
+
+# ----------------------------------------------------------------------------
+# Causal conv1d (the causal-conv1d package, an optional dependency of the
+# reference, pyproject.toml:33, unpinned; its semantics are the reference's own
+# fallbacks in the Mamba layer)
+# ----------------------------------------------------------------------------
+
+def causal_conv1d_ref(x, weight, bias=None, activation=None, compute_dtype=None):
+    """Restatement of the Mamba layer's fallback for ``causal_conv1d_fn``
+    (mamba.py:271: ``act(conv1d(x)[..., :seqlen])`` with nn.Conv1d(groups=d,
+    padding=w-1)).  x (b, d, l); weight (d, w); bias (d,); activation None or
+    "silu" / "swish".  Returns the input dtype (compute_dtype None) or the
+    compute dtype."""
+    rdt = _real(compute_dtype)
+    d, w = weight.shape
+    L = x.shape[-1]
+    out = F.conv1d(x.to(rdt), weight.to(rdt).unsqueeze(1), None if bias is None else bias.to(rdt),
+                   padding=w - 1, groups=d)[..., :L]
+    if activation in ("silu", "swish"):
+        out = F.silu(out)
+    elif activation is not None:
+        raise NotImplementedError("activation must be None, silu or swish")
+    return out.to(x.dtype) if compute_dtype is None else out
+
+
+def causal_conv1d_update_ref(x, conv_state, weight, bias=None, activation=None, compute_dtype=None):
+    """Restatement of the Mamba layer's step fallback (mamba.py:398-410),
+    for x (b, d) or (b, d, l_new) new inputs: for each new step the state
+    (b, d, s) is shifted left by one and the input appended, and
+    out = act(sum(state[..., -w:] * weight) + bias).  Updates conv_state in
+    place (its dtype); returns out like x."""
+    rdt = _real(compute_dtype)
+    squeeze = x.dim() == 2
+    xs = x.unsqueeze(-1) if squeeze else x
+    d, w = weight.shape
+    st = conv_state.to(rdt)
+    outs = []
+    for j in range(xs.shape[-1]):
+        st = torch.roll(st, shifts=-1, dims=-1)
+        st[:, :, -1] = xs[:, :, j].to(rdt)
+        o = torch.sum(st[:, :, -w:] * weight.to(rdt), dim=-1)
+        if bias is not None:
+            o = o + bias.to(rdt)
+        if activation in ("silu", "swish"):
+            o = F.silu(o)
+        outs.append(o)
+    conv_state.copy_(st.to(conv_state.dtype))
+    out = torch.stack(outs, -1)
+    out = out.to(x.dtype) if compute_dtype is None else out
+    return out.squeeze(-1) if squeeze else out
+
+
+def mamba_inner_ref(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
+                    out_proj_bias, A, B=None, C=None, D=None, delta_bias=None, B_proj_bias=None,
+                    C_proj_bias=None, delta_softplus=True, compute_dtype=None):
+    """Restatement of ``mamba_inner_ref`` (selective_scan.py:789-846): causal
+    conv (silu) -> x_proj -> delta_proj -> selective scan (variable B / C from
+    x_proj) -> out_proj.  xz (b, 2d, l); conv1d_weight (d, 1, w)."""
+    rdt = _real(compute_dtype)
+    L = xz.shape[-1]
+    delta_rank = delta_proj_weight.shape[1]
+    d_state = A.shape[-1] * (1 if not A.is_complex() else 2)
+    x, z = xz.chunk(2, dim=1)
+    x = causal_conv1d_ref(x, conv1d_weight[:, 0, :], conv1d_bias, activation="silu", compute_dtype=compute_dtype)
+    xt = x.to(rdt).transpose(1, 2).reshape(-1, x.shape[1])                       # (b l) d
+    x_dbl = xt @ x_proj_weight.to(rdt).t()                                        # (b l) (r + 2n)
+    delta = (delta_proj_weight.to(rdt) @ x_dbl[:, :delta_rank].t())               # d (b l)
+    delta = delta.reshape(-1, xz.shape[0], L).transpose(0, 1)                     # b d l
+    if B is None:
+        B = x_dbl[:, delta_rank:delta_rank + d_state]
+        if B_proj_bias is not None:
+            B = B + B_proj_bias.to(rdt)
+        B = B.reshape(xz.shape[0], L, d_state).transpose(1, 2).contiguous()
+    if C is None:
+        C = x_dbl[:, -d_state:]
+        if C_proj_bias is not None:
+            C = C + C_proj_bias.to(rdt)
+        C = C.reshape(xz.shape[0], L, d_state).transpose(1, 2).contiguous()
+    y = selective_scan_ref(x.to(rdt), delta, A, B, C, D, z=z.to(rdt), delta_bias=delta_bias,
+                           delta_softplus=delta_softplus, compute_dtype=compute_dtype)
+    out = y.to(rdt).transpose(1, 2) @ out_proj_weight.to(rdt).t()
+    if out_proj_bias is not None:
+        out = out + out_proj_bias.to(rdt)
+    return out
 
 
 # ----------------------------------------------------------------------------

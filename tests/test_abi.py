@@ -50,6 +50,8 @@ int main(void) {
          offsetof(lrnnx_simplified_scan_args, workspace_bytes));
   printf("%zu %zu %zu\n", offsetof(lrnnx_state_update_args, state), offsetof(lrnnx_state_update_args, deltaA),
          offsetof(lrnnx_state_update_args, out_s2));
+  printf("%zu %zu %zu %zu\n", sizeof(lrnnx_causal_conv1d_args), offsetof(lrnnx_causal_conv1d_args, x),
+         offsetof(lrnnx_causal_conv1d_args, conv_state), offsetof(lrnnx_causal_conv1d_args, workspace_bytes));
   printf("%zu %zu %zu %zu %zu\n", sizeof(lrnnx_simplified_state_update_args),
          offsetof(lrnnx_simplified_state_update_args, state), offsetof(lrnnx_simplified_state_update_args, A_s0),
          offsetof(lrnnx_simplified_state_update_args, deltaA), offsetof(lrnnx_simplified_state_update_args, out_s1));
@@ -67,8 +69,11 @@ int main(void) {
     assert got[1].split() == [str(getattr(S, f).offset) for f in ("u", "x", "dout", "workspace", "dz")]
     assert got[2].split() == [str(getattr(M, f).offset) for f in ("x", "dout", "workspace_bytes")]
     assert got[3].split() == [str(getattr(U, f).offset) for f in ("state", "deltaA", "out_s2")]
+    K = _lib.CausalConv1dArgs
+    assert got[4].split() == [str(ctypes.sizeof(K))] + [str(getattr(K, f).offset)
+                                                        for f in ("x", "conv_state", "workspace_bytes")]
     Z = _lib.SimplifiedStateUpdateArgs
-    assert got[4].split() == [str(ctypes.sizeof(Z))] + [str(getattr(Z, f).offset)
+    assert got[5].split() == [str(ctypes.sizeof(Z))] + [str(getattr(Z, f).offset)
                                                         for f in ("state", "A_s0", "deltaA", "out_s1")]
 
 
@@ -113,6 +118,14 @@ def test_argument_checks_mirror_reference_messages():
     z.method = _lib.METHODS["zoh"]
     assert L.lrnnx_simplified_state_update(z, None) != 0   # null tensors
     assert "required" in _err()
+    c = _lib.CausalConv1dArgs()
+    c.batch, c.dim, c.seqlen, c.width, c.itype = 1, 4, 8, 9, _lib.F32
+    assert L.lrnnx_causal_conv1d_fwd(c, None) != 0
+    assert "width must be between 1 and 8" in _err()
+    c.width = 4
+    assert L.lrnnx_causal_conv1d_fwd(c, None) != 0   # null tensors
+    assert "required" in _err()
+    assert L.lrnnx_causal_conv1d_workspace_size(c) == 1 * 4 * 5 * 4
 
 
 def test_python_api_refuses_cpu_tensors():

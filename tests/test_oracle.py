@@ -320,3 +320,72 @@ def test_simplified_state_update_scalar_step():
                 yy = 2 * sum(complex(Cm[h, p]) * new[p] for p in range(P)).real
                 yy += sum(float(Dm[h, k]) * float(x[bi, k]) for k in range(H))
                 assert abs(yy - float(y[bi, h])) < 1e-12
+
+
+@pytest.mark.parametrize("width", [1, 2, 4])
+@pytest.mark.parametrize("act", [None, "silu"])
+def test_causal_conv1d_ref_vs_bruteforce(width, act):
+    g = torch.Generator().manual_seed(20 + width)
+    b, d, L = 2, 3, 9
+    x = torch.randn(b, d, L, generator=g, dtype=D64)
+    w = torch.randn(d, width, generator=g, dtype=D64)
+    bias = torch.randn(d, generator=g, dtype=D64)
+    out = R.causal_conv1d_ref(x, w, bias, act, compute_dtype=D64)
+    for bi in range(b):
+        for di in range(d):
+            for t in range(L):
+                acc = float(bias[di])
+                for k in range(width):
+                    tt = t - width + 1 + k
+                    if tt >= 0:
+                        acc += float(w[di, k]) * float(x[bi, di, tt])
+                if act == "silu":
+                    acc = acc / (1.0 + math.exp(-acc))
+                assert abs(acc - float(out[bi, di, t])) < 1e-12
+
+
+@pytest.mark.parametrize("state_len", [4, 6])
+def test_causal_conv1d_update_loop_equals_full_conv(state_len):
+    # token-by-token updates from a zero state == the full causal conv
+    g = torch.Generator().manual_seed(24)
+    b, d, L, w = 2, 5, 11, 4
+    x = torch.randn(b, d, L, generator=g, dtype=D64)
+    wt = torch.randn(d, w, generator=g, dtype=D64)
+    bias = torch.randn(d, generator=g, dtype=D64)
+    full = R.causal_conv1d_ref(x, wt, bias, "silu", compute_dtype=D64)
+    st = torch.zeros(b, d, state_len, dtype=D64)
+    outs = [R.causal_conv1d_update_ref(x[..., t], st, wt, bias, "silu", compute_dtype=D64) for t in range(L)]
+    assert torch.allclose(torch.stack(outs, -1), full, rtol=1e-12, atol=1e-12)
+    # several new steps in one call continue the same state
+    st2 = torch.zeros(b, d, state_len, dtype=D64)
+    first = R.causal_conv1d_update_ref(x[..., :5], st2, wt, bias, "silu", compute_dtype=D64)
+    rest = R.causal_conv1d_update_ref(x[..., 5:], st2, wt, bias, "silu", compute_dtype=D64)
+    assert torch.allclose(torch.cat([first, rest], -1), full, rtol=1e-12, atol=1e-12)
+    assert torch.equal(st2, st)
+
+
+def test_mamba_inner_ref_layout_independent():
+    # the same block computed with (b, l, d) einsums instead of the (b l) d
+    # reshapes of the restatement
+    g = torch.Generator().manual_seed(25)
+    b, dm, d, n, r, L, w = 2, 6, 8, 4, 3, 10, 4
+    xz = torch.randn(b, 2 * d, L, generator=g, dtype=D64)
+    cw = torch.randn(d, 1, w, generator=g, dtype=D64) * 0.5
+    cb = torch.randn(d, generator=g, dtype=D64) * 0.1
+    xpw = torch.randn(r + 2 * n, d, generator=g, dtype=D64) * 0.3
+    dpw = torch.randn(d, r, generator=g, dtype=D64) * 0.3
+    opw = torch.randn(dm, d, generator=g, dtype=D64) * 0.3
+    opb = torch.randn(dm, generator=g, dtype=D64)
+    A = -torch.rand(d, n, generator=g, dtype=D64) - 0.5
+    Dv = torch.randn(d, generator=g, dtype=D64)
+    dbias = torch.randn(d, generator=g, dtype=D64) * 0.1
+    out = R.mamba_inner_ref(xz, cw, cb, xpw, dpw, opw, opb, A, None, None, Dv, dbias, compute_dtype=D64)
+    x, z = xz[:, :d], xz[:, d:]
+    xc = R.causal_conv1d_ref(x, cw[:, 0], cb, "silu", compute_dtype=D64)
+    xdbl = torch.einsum("bdl,ed->ble", xc, xpw)
+    delta = torch.einsum("dr,blr->bdl", dpw, xdbl[..., :r])
+    Bm = xdbl[..., r:r + n].permute(0, 2, 1)
+    Cm = xdbl[..., r + n:].permute(0, 2, 1)
+    y = R.selective_scan_ref(xc, delta, A, Bm, Cm, Dv, z, dbias, None, True, compute_dtype=D64)
+    ref = torch.einsum("bdl,md->blm", y, opw) + opb
+    assert torch.allclose(out, ref, rtol=1e-12, atol=1e-12)
