@@ -230,13 +230,44 @@ int lrnnx_causal_conv1d_bwd(const lrnnx_causal_conv1d_args *a, void *stream);
 /* Replaces causal_conv1d_update (x, conv_state, weight, bias, activation). */
 int lrnnx_causal_conv1d_update(const lrnnx_causal_conv1d_args *a, void *stream);
 
+/* Fused residual-add + LayerNorm / RMSNorm over the last dimension of a
+ * (rows, cols) matrix (reference lrnnx/ops/triton/layer_norm.py: _layer_norm_fwd
+ * :323-470, _layer_norm_bwd :650-805, for the options lrnnx's blocks use:
+ * no dropout, rowscale or second (x1 / weight1) branch).  Views use s0 = row
+ * stride in elements; the columns are contiguous.
+ *   xtype: x, y, dy, dx.   rtype: residual, residual_out, x_saved, dresidual,
+ *   dresidual_in.          wtype: weight, bias, dweight, dbias.
+ * mean (LayerNorm only) and rstd are fp32 per row. */
+typedef struct lrnnx_layer_norm_args {
+  int64_t rows, cols;
+  int32_t xtype, rtype, wtype;
+  int32_t is_rms_norm;
+  float eps;
+  int32_t reserved;
+  lrnnx_view x, residual, weight, bias;  /* forward inputs (residual, bias optional) */
+  lrnnx_view y, residual_out;            /* forward outputs (residual_out optional) */
+  float *mean, *rstd;                    /* written by the forward, read by the backward */
+  lrnnx_view x_saved, dy, dresidual;     /* backward inputs (dresidual optional) */
+  lrnnx_view dx, dresidual_in, dweight, dbias;  /* backward outputs (dresidual_in, dbias optional) */
+  void *workspace;                       /* backward: >= lrnnx_layer_norm_workspace_size() bytes */
+  int64_t workspace_bytes;
+} lrnnx_layer_norm_args;
+
+/* Replaces _layer_norm_fwd (layer_norm.py:323-470): writes y, residual_out (if
+ * given), mean (LayerNorm), rstd. */
+int lrnnx_layer_norm_fwd(const lrnnx_layer_norm_args *a, void *stream);
+int64_t lrnnx_layer_norm_workspace_size(const lrnnx_layer_norm_args *a);
+/* Replaces _layer_norm_bwd (layer_norm.py:650-805): writes dx, dresidual_in (if
+ * given: dx in the residual dtype), dweight, dbias (if given). */
+int lrnnx_layer_norm_bwd(const lrnnx_layer_norm_args *a, void *stream);
+
 /* Last error message of this thread ("" if none). */
 const char *lrnnx_last_error(void);
 
 /* ABI version of this header (bumped on any struct change). */
 int lrnnx_abi_version(void);
 
-#define LRNNX_ABI_VERSION 3
+#define LRNNX_ABI_VERSION 4
 
 #ifdef __cplusplus
 }

@@ -11,6 +11,8 @@ Public API (same names, arguments and return conventions as the reference's
 * ``causal_conv1d_fn``, ``causal_conv1d_update`` and the ``causal_conv1d_fwd_function`` /
   ``causal_conv1d_bwd_function`` pair: the causal-conv1d package's API that lrnnx calls
 * ``mamba_inner_fn`` / ``MambaInnerFn``  (lrnnx/ops/selective_scan.py:389-786)
+* ``layer_norm_fn``, ``rms_norm_fn``, ``LayerNormFn``, ``RMSNorm``: the fused
+  residual-add LayerNorm / RMSNorm (lrnnx/ops/triton/layer_norm.py)
 * ``selective_scan_cuda``, ``simplified_scan_cuda``: drop-in replacements of
   the reference's pybind11 extension modules (``fwd`` / ``bwd``).
 
@@ -21,6 +23,7 @@ include/lrnnx_scan.h).  There is no CPU fallback.
 from . import selective_scan_cuda, simplified_scan_cuda  # noqa: F401
 from .causal_conv1d import (causal_conv1d_bwd_function, causal_conv1d_fn, causal_conv1d_fwd_function,  # noqa: F401
                             causal_conv1d_update)
+from .layer_norm import LayerNormFn, RMSNorm, layer_norm_fn, rms_norm_fn  # noqa: F401
 from .mamba_inner import MambaInnerFn, mamba_inner_fn  # noqa: F401
 from .selective_scan import SelectiveScanFn, selective_scan_fn  # noqa: F401
 from .selective_state_update import selective_state_update  # noqa: F401

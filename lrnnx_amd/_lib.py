@@ -90,6 +90,18 @@ class CausalConv1dArgs(ctypes.Structure):
     )
 
 
+class LayerNormArgs(ctypes.Structure):
+    _fields_ = (
+        [("rows", c_i64), ("cols", c_i64)]
+        + [(n, c_i32) for n in ("xtype", "rtype", "wtype", "is_rms_norm")]
+        + [("eps", ctypes.c_float), ("reserved", c_i32)]
+        + [(n, View) for n in ("x", "residual", "weight", "bias", "y", "residual_out")]
+        + [("mean", c_vp), ("rstd", c_vp)]
+        + [(n, View) for n in ("x_saved", "dy", "dresidual", "dx", "dresidual_in", "dweight", "dbias")]
+        + [("workspace", c_vp), ("workspace_bytes", c_i64)]
+    )
+
+
 EXPORTS = (
     "lrnnx_selective_scan_ckpt_size",
     "lrnnx_selective_scan_workspace_size",
@@ -105,11 +117,14 @@ EXPORTS = (
     "lrnnx_causal_conv1d_bwd",
     "lrnnx_causal_conv1d_update",
     "lrnnx_causal_conv1d_workspace_size",
+    "lrnnx_layer_norm_fwd",
+    "lrnnx_layer_norm_bwd",
+    "lrnnx_layer_norm_workspace_size",
     "lrnnx_last_error",
     "lrnnx_abi_version",
 )
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 def lib():
@@ -145,6 +160,11 @@ def lib():
             getattr(L, fn).restype = ctypes.c_int
         L.lrnnx_causal_conv1d_workspace_size.argtypes = [P(CausalConv1dArgs)]
         L.lrnnx_causal_conv1d_workspace_size.restype = c_i64
+        for fn in ("lrnnx_layer_norm_fwd", "lrnnx_layer_norm_bwd"):
+            getattr(L, fn).argtypes = [P(LayerNormArgs), c_vp]
+            getattr(L, fn).restype = ctypes.c_int
+        L.lrnnx_layer_norm_workspace_size.argtypes = [P(LayerNormArgs)]
+        L.lrnnx_layer_norm_workspace_size.restype = c_i64
         L.lrnnx_last_error.restype = ctypes.c_char_p
         for fn in ("lrnnx_selective_scan_fwd", "lrnnx_selective_scan_bwd", "lrnnx_simplified_scan_fwd",
                    "lrnnx_simplified_scan_bwd", "lrnnx_selective_state_update",

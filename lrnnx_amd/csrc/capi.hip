@@ -45,6 +45,8 @@ int64_t simp_ws_bytes(const lrnnx_simplified_scan_args&, int);
 hipError_t state_update_launch(const lrnnx_state_update_args&, hipStream_t);
 hipError_t simp_state_update_launch(const lrnnx_simplified_state_update_args&, hipStream_t);
 hipError_t cconv_launch(const lrnnx_causal_conv1d_args&, int, float*, hipStream_t);
+hipError_t ln_launch(const lrnnx_layer_norm_args&, bool, float*, hipStream_t);
+int64_t ln_workspace_bytes(const lrnnx_layer_norm_args&);
 
 // defined in ss_bwd_layout.hip (shares ss_bwd_ws with the backward units)
 int64_t ss_bwd_ws_bytes(const lrnnx_selective_scan_args&);
@@ -320,6 +322,40 @@ int lrnnx_simplified_state_update(const lrnnx_simplified_state_update_args* a, v
   if ((a->H + 2 * a->P) * 4 > 64 * 1024) return fail("H + 2 P must fit 64 KiB of LDS (H=%lld, P=%lld)",
                                                      (long long)a->H, (long long)a->P);
   return from_hip(simp_state_update_launch(*a, static_cast<hipStream_t>(stream)), "simplified_state_update");
+}
+
+static int check_ln(const lrnnx_layer_norm_args* a, bool bwd) {
+  if (!a) return fail("null argument struct");
+  for (int t : {a->xtype, a->rtype, a->wtype})
+    if (t != LRNNX_F32 && t != LRNNX_F16 && t != LRNNX_BF16) return fail("unsupported dtype code %d", t);
+  if (a->rows <= 0 || a->cols <= 0) return fail("empty or negative shape");
+  // the reference's one-pass kernel holds a row of x in 64 KiB (layer_norm.py:405-411)
+  if (a->cols * (a->xtype == LRNNX_F32 ? 4 : 2) > 65536)
+    return fail("This layer norm doesn't support feature dim >= 64KB.");
+  if (!a->weight.ptr || !a->rstd || (!a->is_rms_norm && !a->mean)) return fail("weight, rstd and mean are required");
+  if (!bwd) {
+    if (!a->x.ptr || !a->y.ptr) return fail("x and y are required");
+    return 0;
+  }
+  if (!a->x_saved.ptr || !a->dy.ptr || !a->dx.ptr || !a->dweight.ptr) return fail("x, dy, dx, dweight are required");
+  if (a->bias.ptr && !a->dbias.ptr) return fail("dbias is required when bias is given");
+  if (!a->workspace || a->workspace_bytes < ln_workspace_bytes(*a)) return fail("workspace too small");
+  return 0;
+}
+
+int64_t lrnnx_layer_norm_workspace_size(const lrnnx_layer_norm_args* a) {
+  return a ? ln_workspace_bytes(*a) : -1;
+}
+
+int lrnnx_layer_norm_fwd(const lrnnx_layer_norm_args* a, void* stream) {
+  if (check_ln(a, false)) return 1;
+  return from_hip(ln_launch(*a, false, nullptr, static_cast<hipStream_t>(stream)), "layer_norm_fwd");
+}
+
+int lrnnx_layer_norm_bwd(const lrnnx_layer_norm_args* a, void* stream) {
+  if (check_ln(a, true)) return 1;
+  return from_hip(ln_launch(*a, true, static_cast<float*>(a->workspace), static_cast<hipStream_t>(stream)),
+                  "layer_norm_bwd");
 }
 
 }  // extern "C"

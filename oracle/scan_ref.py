@@ -19,6 +19,8 @@ Reference anchors (paths relative to the reference checkout):
   causal_conv1d_ref ......... lrnnx/models/ltv/mamba.py:271 (nn.Conv1d fallback of causal_conv1d_fn)
   causal_conv1d_update_ref .. lrnnx/models/ltv/mamba.py:398-410 (roll-and-sum fallback of causal_conv1d_update)
   mamba_inner_ref ........... lrnnx/ops/selective_scan.py:789-846
+  layer_norm_fwd_ref ........ lrnnx/ops/triton/layer_norm.py:202-322 (kernel), :323-470 (host: which outputs exist)
+  layer_norm_bwd_ref ........ lrnnx/ops/triton/layer_norm.py:490-649 (kernel), :650-805 (host)
   s7_scan_ref ............... lrnnx/ops/s7_scan.py:179-233
   rglru_scan_ref ............ lrnnx/ops/rglru_scan.py:148-203
 """
@@ -519,6 +521,77 @@ def mamba_inner_ref(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_we
 # ----------------------------------------------------------------------------
 # S7 / RG-LRU wrappers (they call selective_scan_cuda with "s7"/"rglru")
 # ----------------------------------------------------------------------------
+
+def layer_norm_fwd_ref(x, weight, bias=None, residual=None, eps=1e-6, residual_dtype=None, is_rms_norm=False,
+                       compute_dtype=None):
+    """Restatement of the fused residual-add LayerNorm / RMSNorm forward as the
+    Triton kernel computes it (layer_norm.py:253-322): the sum x + residual is
+    formed in fp32 (or ``compute_dtype``), stored as residual_out in the
+    residual dtype, and normalised *unrounded*; mean / rstd are per row.
+    Which outputs exist follows the host code (layer_norm.py:339-383):
+    residual_out exists when a residual is given or residual_dtype differs from
+    x's dtype, and otherwise x itself is what the backward reads (:463).
+    x (M, N); returns (y in x's dtype, mean (M,) or None, rstd (M,), x_saved).
+    """
+    rdt = _real(compute_dtype)
+    if residual is not None:
+        residual_dtype = residual.dtype
+    s = x.to(rdt)
+    if residual is not None:
+        s = s + residual.to(rdt)
+    has_res_out = residual is not None or (residual_dtype is not None and residual_dtype != x.dtype)
+    x_saved = s.to(residual_dtype if residual_dtype is not None else x.dtype) if has_res_out else x
+    N = x.shape[-1]
+    if is_rms_norm:
+        mean = None
+        var = (s * s).sum(-1) / N
+        xhat = s * (1.0 / torch.sqrt(var + eps)).unsqueeze(-1)
+    else:
+        mean = s.sum(-1) / N
+        xbar = s - mean.unsqueeze(-1)
+        var = (xbar * xbar).sum(-1) / N
+        xhat = xbar * (1.0 / torch.sqrt(var + eps)).unsqueeze(-1)
+    rstd = 1.0 / torch.sqrt(var + eps)
+    y = xhat * weight.to(rdt)
+    if bias is not None:
+        y = y + bias.to(rdt)
+    out_dt = x.dtype if compute_dtype is None else rdt
+    return y.to(out_dt), mean, rstd, (x_saved if compute_dtype is None else s)
+
+
+def layer_norm_bwd_ref(dy, x_saved, weight, bias, mean, rstd, dresidual=None, has_residual=False,
+                       is_rms_norm=False, x_dtype=None, compute_dtype=None):
+    """Restatement of the backward kernel (layer_norm.py:566-649) and its host
+    code (:650-805) without dropout / rowscale / x1: xhat is recomputed from the
+    saved pre-norm input and the saved mean / rstd, wdy = w dy,
+    dx = (wdy - (xhat c1 + c2)) rstd (+ dresidual) with c1 = mean(xhat wdy),
+    c2 = mean(wdy) (LayerNorm; 0 for RMSNorm); dw = sum_rows dy xhat,
+    db = sum_rows dy.  dx is returned in x_dtype; dresidual_in (when a
+    residual was given) is dx in x_saved's dtype.
+    Returns (dx, dw, db, dresidual_in)."""
+    rdt = _real(compute_dtype)
+    N = x_saved.shape[-1]
+    xs = x_saved.to(rdt)
+    r = rstd.to(rdt).unsqueeze(-1)
+    xhat = xs * r if is_rms_norm else (xs - mean.to(rdt).unsqueeze(-1)) * r
+    g = dy.to(rdt)
+    wdy = weight.to(rdt) * g
+    c1 = (xhat * wdy).sum(-1, keepdim=True) / N
+    if is_rms_norm:
+        dx = (wdy - xhat * c1) * r
+    else:
+        c2 = wdy.sum(-1, keepdim=True) / N
+        dx = (wdy - (xhat * c1 + c2)) * r
+    if dresidual is not None:
+        dx = dx + dresidual.to(rdt)
+    dw = (g * xhat).sum(0)
+    db = g.sum(0) if bias is not None else None
+    if compute_dtype is not None:
+        return dx, dw, db, (dx if has_residual else None)
+    xdt = x_dtype if x_dtype is not None else x_saved.dtype
+    dres_in = dx.to(x_saved.dtype) if has_residual else None
+    return (dx.to(xdt), dw.to(weight.dtype), None if db is None else db.to(bias.dtype), dres_in)
+
 
 def s7_scan_ref(u, A, B, C, bias=None, return_last_state=False, compute_dtype=None):
     """Restatement of ``s7_scan_ref`` (s7_scan.py:179-233)."""

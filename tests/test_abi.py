@@ -55,6 +55,9 @@ int main(void) {
   printf("%zu %zu %zu %zu %zu\n", sizeof(lrnnx_simplified_state_update_args),
          offsetof(lrnnx_simplified_state_update_args, state), offsetof(lrnnx_simplified_state_update_args, A_s0),
          offsetof(lrnnx_simplified_state_update_args, deltaA), offsetof(lrnnx_simplified_state_update_args, out_s1));
+  printf("%zu %zu %zu %zu %zu %zu\n", sizeof(lrnnx_layer_norm_args), offsetof(lrnnx_layer_norm_args, eps),
+         offsetof(lrnnx_layer_norm_args, x), offsetof(lrnnx_layer_norm_args, mean),
+         offsetof(lrnnx_layer_norm_args, x_saved), offsetof(lrnnx_layer_norm_args, workspace_bytes));
   return 0;
 }
 '''
@@ -75,6 +78,9 @@ int main(void) {
     Z = _lib.SimplifiedStateUpdateArgs
     assert got[5].split() == [str(ctypes.sizeof(Z))] + [str(getattr(Z, f).offset)
                                                         for f in ("state", "A_s0", "deltaA", "out_s1")]
+    N = _lib.LayerNormArgs
+    assert got[6].split() == [str(ctypes.sizeof(N))] + [str(getattr(N, f).offset)
+                                                        for f in ("eps", "x", "mean", "x_saved", "workspace_bytes")]
 
 
 def _err():
@@ -126,6 +132,21 @@ def test_argument_checks_mirror_reference_messages():
     assert L.lrnnx_causal_conv1d_fwd(c, None) != 0   # null tensors
     assert "required" in _err()
     assert L.lrnnx_causal_conv1d_workspace_size(c) == 1 * 4 * 5 * 4
+    n = _lib.LayerNormArgs()
+    n.rows, n.cols, n.xtype, n.rtype, n.wtype = 4, 40000, _lib.F16, _lib.F16, _lib.F32
+    assert L.lrnnx_layer_norm_fwd(n, None) != 0
+    assert "feature dim >= 64KB" in _err()   # layer_norm.py:405-411
+    n.cols = 64
+    assert L.lrnnx_layer_norm_fwd(n, None) != 0   # null tensors
+    assert "required" in _err()
+    n.xtype = 7
+    assert L.lrnnx_layer_norm_fwd(n, None) != 0
+    assert "unsupported dtype" in _err()
+    n.xtype = _lib.F16
+    # fast path (cols % 4 == 0, <= 4096): one partial per workgroup (1 row each here)
+    assert L.lrnnx_layer_norm_workspace_size(n) == 1 * 2 * 64 * 4
+    n.cols = 5000   # generic path: min(rows, 64) row blocks
+    assert L.lrnnx_layer_norm_workspace_size(n) == 4 * 2 * 5000 * 4
 
 
 def test_python_api_refuses_cpu_tensors():
@@ -151,6 +172,19 @@ def test_simplified_state_update_refuses_cpu_tensors():
         simplified_state_update(st, torch.zeros(2, 4), torch.ones(3), A, B, B.T.contiguous())
     with pytest.raises(AssertionError):   # the reference's shape assertions
         simplified_state_update(st, torch.zeros(2, 5), torch.ones(3), A, B, B.T.contiguous())
+
+
+def test_layer_norm_refuses_cpu_tensors():
+    from lrnnx_amd import RMSNorm, layer_norm_fn
+
+    x = torch.randn(2, 3, 8)
+    w = torch.ones(8)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        layer_norm_fn(x, w, None, residual=x.clone(), prenorm=True)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        RMSNorm(8)(x)
+    with pytest.raises(NotImplementedError, match="dropout"):
+        layer_norm_fn(x, w, None, dropout_p=0.1)
 
 
 def test_workspace_queries_are_host_only():

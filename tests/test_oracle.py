@@ -389,3 +389,88 @@ def test_mamba_inner_ref_layout_independent():
     y = R.selective_scan_ref(xc, delta, A, Bm, Cm, Dv, z, dbias, None, True, compute_dtype=D64)
     ref = torch.einsum("bdl,md->blm", y, opw) + opb
     assert torch.allclose(out, ref, rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- fused residual-add LayerNorm / RMSNorm
+def _norm_lib(s, w, b, eps, rms):
+    """The library routine of the same normalisation (F.layer_norm / F.rms_norm)."""
+    N = s.shape[-1]
+    if rms:
+        y = F.rms_norm(s, (N,), w, eps)
+        return y + b if b is not None else y
+    return F.layer_norm(s, (N,), w, b, eps)
+
+
+@pytest.mark.parametrize("rms", [False, True])
+@pytest.mark.parametrize("has_res", [False, True])
+@pytest.mark.parametrize("has_bias", [False, True])
+def test_layer_norm_fwd_ref_vs_library(rms, has_res, has_bias):
+    g = torch.Generator().manual_seed(11 + 2 * rms + 4 * has_res + 8 * has_bias)
+    M, N, eps = 7, 37, 1e-5
+    x = torch.randn(M, N, generator=g, dtype=D64) * 3 + 0.5
+    res = torch.randn(M, N, generator=g, dtype=D64) if has_res else None
+    w = torch.randn(N, generator=g, dtype=D64)
+    b = torch.randn(N, generator=g, dtype=D64) if has_bias else None
+    y, mean, rstd, xs = R.layer_norm_fwd_ref(x, w, b, res, eps=eps, is_rms_norm=rms, compute_dtype=D64)
+    s = x + res if has_res else x
+    torch.testing.assert_close(y, _norm_lib(s, w, b, eps, rms), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(xs, s, rtol=0, atol=0)
+    var = (s * s).mean(-1) if rms else s.var(-1, unbiased=False)
+    torch.testing.assert_close(rstd, 1 / torch.sqrt(var + eps), rtol=1e-12, atol=0)
+    if rms:
+        assert mean is None
+    else:
+        torch.testing.assert_close(mean, s.mean(-1), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("rms", [False, True])
+@pytest.mark.parametrize("prenorm", [False, True])
+@pytest.mark.parametrize("has_bias", [False, True])
+def test_layer_norm_bwd_ref_vs_autograd(rms, prenorm, has_bias):
+    """dx, dresidual_in, dw, db of the restated backward equal autograd's
+    gradients of the library routine applied to s = x + residual, with the
+    prenorm output s receiving its own gradient dresidual."""
+    g = torch.Generator().manual_seed(23 + 2 * rms + 4 * prenorm + 8 * has_bias)
+    M, N, eps = 6, 29, 1e-6
+    x = (torch.randn(M, N, generator=g, dtype=D64) * 2).requires_grad_()
+    res = torch.randn(M, N, generator=g, dtype=D64).requires_grad_()
+    w = torch.randn(N, generator=g, dtype=D64).requires_grad_()
+    b = torch.randn(N, generator=g, dtype=D64).requires_grad_() if has_bias else None
+    dy = torch.randn(M, N, generator=g, dtype=D64)
+    dres = torch.randn(M, N, generator=g, dtype=D64) if prenorm else None
+    s = x + res
+    loss = (_norm_lib(s, w, b, eps, rms) * dy).sum() + ((s * dres).sum() if prenorm else 0)
+    loss.backward()
+    _, mean, rstd, xs = R.layer_norm_fwd_ref(x.detach(), w.detach(), None if b is None else b.detach(),
+                                             res.detach(), eps=eps, is_rms_norm=rms, compute_dtype=D64)
+    dx, dw, db, dri = R.layer_norm_bwd_ref(dy, xs, w.detach(), b, mean, rstd, dresidual=dres, has_residual=True,
+                                           is_rms_norm=rms, compute_dtype=D64)
+    torch.testing.assert_close(dx, x.grad, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(dri, res.grad, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(dw, w.grad, rtol=1e-10, atol=1e-10)
+    if has_bias:
+        torch.testing.assert_close(db, b.grad, rtol=1e-10, atol=1e-10)
+
+
+def test_layer_norm_ref_output_dtypes_follow_host_code():
+    """Which pre-norm tensor is saved and in which dtype (layer_norm.py:339-383,
+    :463, :714-730, :793-798)."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 16, generator=g).to(torch.bfloat16)
+    w = torch.ones(16)
+    # no residual, no upcast: x itself is saved
+    _, _, _, xs = R.layer_norm_fwd_ref(x, w, None)
+    assert xs is x
+    # residual_in_fp32 without a residual: residual_out = x in fp32
+    _, _, _, xs = R.layer_norm_fwd_ref(x, w, None, residual_dtype=torch.float32)
+    assert xs.dtype == torch.float32 and torch.equal(xs, x.float())
+    # bf16 residual: the fp32 sum rounded once to bf16
+    r = torch.randn(3, 16, generator=g).to(torch.bfloat16)
+    y, _, rstd, xs = R.layer_norm_fwd_ref(x, w, None, residual=r)
+    assert xs.dtype == torch.bfloat16 and torch.equal(xs, (x.float() + r.float()).to(torch.bfloat16))
+    assert y.dtype == torch.bfloat16 and rstd.dtype == torch.float32
+    # backward: dx in x's dtype, dresidual_in in the saved dtype
+    _, mean, rstd, xs = R.layer_norm_fwd_ref(x, w, None, residual=r.float())
+    dx, dw, db, dri = R.layer_norm_bwd_ref(torch.randn(3, 16, generator=g).to(torch.bfloat16), xs, w, None, mean,
+                                           rstd, has_residual=True, x_dtype=torch.bfloat16)
+    assert dx.dtype == torch.bfloat16 and dri.dtype == torch.float32 and db is None and dw.dtype == torch.float32
