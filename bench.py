@@ -166,6 +166,121 @@ class LRUStep:
         self.L_.check(self.L_.lib().lrnnx_simplified_scan_bwd(self.ba, self.stream.cuda_stream), "lru bwd")
 
 
+class NormStep:
+    """The block's fused residual-add RMSNorm (prenorm, bf16 hidden states, fp32
+    residual stream) on (rows, cols), straight through the C ABI with every
+    output preallocated.  Algorithmic bytes per row element: forward reads x
+    (2) + residual (4), writes y (2) + residual_out (4); backward reads
+    residual_out (4) + dy (2) + dresidual (4), writes dx (2) + dresidual_in (4);
+    plus 4 bytes of rstd per row each way."""
+
+    def __init__(self, dev, torch, L_, rows, cols, seed=5):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        bf = torch.bfloat16
+        self.x = torch.randn(rows, cols, device=dev, generator=g).to(bf)
+        self.res = torch.randn(rows, cols, device=dev, generator=g)
+        self.w = torch.ones(cols, device=dev)
+        self.y, self.ro = torch.empty_like(self.x), torch.empty_like(self.res)
+        self.rstd = torch.empty(rows, device=dev)
+        self.dy = torch.randn(rows, cols, device=dev, generator=g).to(bf)
+        self.dres = torch.randn(rows, cols, device=dev, generator=g)
+        self.dx, self.dri = torch.empty_like(self.x), torch.empty_like(self.res)
+        self.dw = torch.empty(cols, device=dev)
+        self.L_ = L_
+        a = L_.LayerNormArgs()
+        a.rows, a.cols, a.xtype, a.rtype, a.wtype = rows, cols, L_.BF16, L_.F32, L_.F32
+        a.is_rms_norm, a.eps = 1, 1e-5
+        a.x, a.residual, a.weight = L_.view(self.x), L_.view(self.res), L_.view(self.w)
+        a.y, a.residual_out = L_.view(self.y), L_.view(self.ro)
+        a.rstd = self.rstd.data_ptr()
+        a.x_saved, a.dy, a.dresidual = L_.view(self.ro), L_.view(self.dy), L_.view(self.dres)
+        a.dx, a.dresidual_in, a.dweight = L_.view(self.dx), L_.view(self.dri), L_.view(self.dw)
+        n = L_.lib().lrnnx_layer_norm_workspace_size(a)
+        self.ws = torch.empty(max(n, 256), dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
+        self.a = a
+        self.alg = {"fwd": rows * cols * 12 + rows * 4, "bwd": rows * cols * 16 + rows * 4}
+        self.stream = torch.cuda.current_stream(dev)
+
+    def fwd(self):
+        self.L_.check(self.L_.lib().lrnnx_layer_norm_fwd(self.a, self.stream.cuda_stream), "layer_norm fwd")
+
+    def bwd(self):
+        self.L_.check(self.L_.lib().lrnnx_layer_norm_bwd(self.a, self.stream.cuda_stream), "layer_norm bwd")
+
+
+class ConvStep:
+    """The Mamba block's depthwise causal conv1d (width 4, SiLU, bias) on the
+    x half of in_proj's output, bf16, through the C ABI with preallocated
+    outputs.  Algorithmic bytes: forward reads x and writes out (2 bytes
+    each per element); backward reads x and dout, writes dx."""
+
+    def __init__(self, dev, torch, L_, Bt, D, L, W=4, seed=6):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        bf = torch.bfloat16
+        self.x = torch.randn(Bt, D, L, device=dev, generator=g).to(bf)
+        self.w = 0.5 * torch.randn(D, W, device=dev, generator=g)
+        self.b = 0.1 * torch.randn(D, device=dev, generator=g)
+        self.out = torch.empty_like(self.x)
+        self.dout = torch.randn(Bt, D, L, device=dev, generator=g).to(bf)
+        self.dx = torch.empty_like(self.x)
+        self.dw, self.db = torch.empty(D, W, device=dev), torch.empty(D, device=dev)
+        self.L_ = L_
+        a = L_.CausalConv1dArgs()
+        a.batch, a.dim, a.seqlen, a.width, a.itype, a.silu = Bt, D, L, W, L_.BF16, 1
+        a.x, a.weight, a.bias, a.out = (L_.view_full(t) for t in (self.x, self.w, self.b, self.out))
+        a.dout, a.dx, a.dweight, a.dbias = (L_.view_full(t) for t in (self.dout, self.dx, self.dw, self.db))
+        n = L_.lib().lrnnx_causal_conv1d_workspace_size(a)
+        self.ws = torch.empty(max(n, 256), dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
+        self.a = a
+        self.alg = {"fwd": Bt * D * L * 4, "bwd": Bt * D * L * 6}
+        self.stream = torch.cuda.current_stream(dev)
+
+    def fwd(self):
+        self.L_.check(self.L_.lib().lrnnx_causal_conv1d_fwd(self.a, self.stream.cuda_stream), "conv fwd")
+
+    def bwd(self):
+        self.L_.check(self.L_.lib().lrnnx_causal_conv1d_bwd(self.a, self.stream.cuda_stream), "conv bwd")
+
+
+def aux_kernels(torch, L_, dev):
+    """The kernels of the callers either side of the scan (Mamba-1.4B block:
+    d_model 2048, d_inner 4096, batch 8, seqlen 4096): fused residual-add
+    RMSNorm and causal conv1d, fwd and bwd medians against the HBM peak."""
+    res = {}
+    # ceiling of a streaming kernel on this device: torch's elementwise copy, 1 GiB read + 1 GiB written
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ms = []
+    for _ in range(10):
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    ms.sort()
+    res["copy_1GiB_read_1GiB_write"] = {"ms": round(ms[len(ms) // 2], 4),
+                                        "GB_s": round(2 * (1 << 30) / (ms[len(ms) // 2] * 1e-3) / 1e9, 1)}
+    del src, dst
+    torch.cuda.empty_cache()
+    for name, st in (("rms_norm_prenorm_rows32768_d2048", lambda: NormStep(dev, torch, L_, 8 * 4096, 2048)),
+                     ("causal_conv1d_b8_d4096_l4096_w4", lambda: ConvStep(dev, torch, L_, 8, 4096, 4096))):
+        step = st()
+        _, f, b = time_steps(step, torch, 20, 3)
+        fm, bm = f[len(f) // 2], b[len(b) // 2]
+        fg, bg = step.alg["fwd"] / (fm * 1e-3) / 1e9, step.alg["bwd"] / (bm * 1e-3) / 1e9
+        res[name] = {"fwd_ms": round(fm, 4), "bwd_ms": round(bm, 4), "fwd_GB_s": round(fg, 1),
+                     "bwd_GB_s": round(bg, 1), "fwd_pct_hbm": round(100 * fg / HBM_PEAK_GBS, 2),
+                     "bwd_pct_hbm": round(100 * bg / HBM_PEAK_GBS, 2), "alg_bytes": step.alg}
+        del step
+        torch.cuda.empty_cache()
+    return res
+
+
 def time_steps(step, torch, steps, warmup):
     for _ in range(warmup):
         step.fwd()
@@ -246,6 +361,9 @@ def other_configs(torch, ss, L_, dev):
                                "pct_hbm": round(100 * alg / t / 1e9 / HBM_PEAK_GBS, 2),
                                "elem_per_s": round(Bt * P * L / t, 1),
                                "alg_bytes": alg}
+    del st
+    torch.cuda.empty_cache()
+    res.update(aux_kernels(torch, L_, dev))
     return res
 
 

@@ -10,7 +10,7 @@
 //
 // One wave per (b, d) row; the row is walked in chunks of 512 steps, 8
 // consecutive steps per lane (16-byte loads / stores for 16-bit types when
-// the row is aligned).  The W - 1 steps of history a lane needs come from the
+// the row is aligned), 4 chunks loaded together ahead of their compute.  The W - 1 steps of history a lane needs come from the
 // previous lane through ds_bpermute, and lane 0 takes them from the previous
 // chunk (forward) or from a few extra loads (backward, which walks right to
 // left so that the W - 1 steps of g to the right come from the chunk just
@@ -27,10 +27,13 @@ constexpr int kCCh = kCE * kWave;      // steps per chunk
 __device__ __forceinline__ float shfl_f(float v, int src) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute((src & 63) << 2, __float_as_int(v)));
 }
-__device__ __forceinline__ float silu_f(float p) { return p / (1.f + __expf(-p)); }
+// sigmoid through v_exp_f32 and v_rcp_f32 (<= 1 ulp each) instead of an IEEE
+// division; exp(-p) = inf for p << 0 gives sigmoid 0, silu -0 and silu' 0.
+__device__ __forceinline__ float sigmoid_f(float p) { return __builtin_amdgcn_rcpf(1.f + __expf(-p)); }
+__device__ __forceinline__ float silu_f(float p) { return p * sigmoid_f(p); }
 // d silu(p) / dp = s (1 + p (1 - s)), s = sigmoid(p)
 __device__ __forceinline__ float silu_grad(float p) {
-  const float s = 1.f / (1.f + __expf(-p));
+  const float s = sigmoid_f(p);
   return s * (1.f + p * (1.f - s));
 }
 
@@ -74,6 +77,46 @@ __device__ __forceinline__ void store_row8(IT* p, int64_t t, int64_t L, bool vec
 }
 }  // namespace
 
+// 8 consecutive elements as raw 16-byte words (one for 16-bit types, two for fp32)
+template <typename IT>
+struct Raw8 {
+  uint4 v[sizeof(IT) == 4 ? 2 : 1];
+};
+template <typename IT>
+__device__ __forceinline__ Raw8<IT> ld_raw8(const IT* p) {
+  Raw8<IT> r;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(r.v) / sizeof(uint4)); ++i) r.v[i] = reinterpret_cast<const uint4*>(p)[i];
+  return r;
+}
+template <typename IT>
+__device__ __forceinline__ void cvt_raw8(const Raw8<IT>& r, float* v) {
+  if constexpr (sizeof(IT) == 4) {
+    const uint32_t* u = reinterpret_cast<const uint32_t*>(r.v);
+#pragma unroll
+    for (int j = 0; j < kCE; ++j) v[j] = __uint_as_float(u[j]);
+  } else {
+    raw_to_f32<IT>(r.v[0], v);
+  }
+}
+
+// 8 elements starting at t with those outside [0, L) as zero, element by element
+template <typename IT>
+__device__ __forceinline__ Raw8<IT> ld_raw8_guarded(const IT* p, int64_t t, int64_t L) {
+  Raw8<IT> r;
+  IT* e = reinterpret_cast<IT*>(r.v);
+#pragma unroll
+  for (int j = 0; j < kCE; ++j) {
+    e[j] = from_f32<IT>(0.f);
+    if (t + j >= 0 && t + j < L) e[j] = p[t + j];
+  }
+  return r;
+}
+
+// Chunks of a row loaded together before any of them is used (more bytes in
+// flight per wave: kCU x 16 (or 32) bytes per lane per array).
+constexpr int kCU = 4;
+
 template <typename IT, int W, bool kSilu>
 __global__ void __launch_bounds__(256) cconv_fwd_kernel(const lrnnx_causal_conv1d_args a) {
   const int lane = threadIdx.x & 63;
@@ -91,31 +134,45 @@ __global__ void __launch_bounds__(256) cconv_fwd_kernel(const lrnnx_causal_conv1
   float prev[W > 1 ? W - 1 : 1];   // the W - 1 inputs before the chunk
 #pragma unroll
   for (int i = 0; i < W - 1; ++i) prev[i] = 0.f;
-  for (int64_t t0 = 0; t0 < L; t0 += kCCh) {
-    const int64_t t = t0 + kCE * lane;
-    float xx[W - 1 + kCE];
-    load_row8<IT>(x, t, L, vec, xx + W - 1);
+  for (int64_t t0 = 0; t0 < L; t0 += kCU * kCCh) {
+    // raw 16-byte words of the group's chunks, converted only when used
+    Raw8<IT> raw[kCU];
+    if (vec && t0 + kCU * kCCh <= L) {
 #pragma unroll
-    for (int i = 0; i < W - 1; ++i) {
-      const float h = shfl_f(xx[W - 1 + kCE - (W - 1) + i], lane - 1);
-      xx[i] = lane == 0 ? prev[i] : h;
+      for (int u = 0; u < kCU; ++u) raw[u] = ld_raw8<IT>(x + t0 + u * kCCh + kCE * lane);
+    } else {
+#pragma unroll
+      for (int u = 0; u < kCU; ++u) raw[u] = ld_raw8_guarded<IT>(x, t0 + u * kCCh + kCE * lane, L);
     }
-    float y[kCE];
 #pragma unroll
-    for (int j = 0; j < kCE; ++j) {
-      float acc = bias;
+    for (int u = 0; u < kCU; ++u) {
+      if (t0 + u * kCCh >= L) break;
+      const int64_t t = t0 + u * kCCh + kCE * lane;
+      float xx[W - 1 + kCE];
+      cvt_raw8<IT>(raw[u], xx + W - 1);
 #pragma unroll
-      for (int k = 0; k < W; ++k) acc = fmaf(w[k], xx[j + k], acc);
-      y[j] = kSilu ? silu_f(acc) : acc;
+      for (int i = 0; i < W - 1; ++i) {
+        const float h = shfl_f(xx[W - 1 + kCE - (W - 1) + i], lane - 1);
+        xx[i] = lane == 0 ? prev[i] : h;
+      }
+      float y[kCE];
+#pragma unroll
+      for (int j = 0; j < kCE; ++j) {
+        float acc = bias;
+#pragma unroll
+        for (int k = 0; k < W; ++k) acc = fmaf(w[k], xx[j + k], acc);
+        y[j] = kSilu ? silu_f(acc) : acc;
+      }
+      if (t < L) store_row8<IT>(out, t, L, vec, y);
+#pragma unroll
+      for (int i = 0; i < W - 1; ++i)
+        prev[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xx[W - 1 + kCE - (W - 1) + i]), 63));
     }
-    if (t < L) store_row8<IT>(out, t, L, vec, y);
-#pragma unroll
-    for (int i = 0; i < W - 1; ++i)
-      prev[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xx[W - 1 + kCE - (W - 1) + i]), 63));
   }
 }
 
-// dx (row) and per-row partials of dw[W], dbias -> part[row * (W + 1) + k]
+// dx (row) and per-row partials of dw[W], dbias -> part[row * (W + 1) + k].
+// Walks the row right to left, kCU chunks per group (loaded together).
 template <typename IT, int W, bool kSilu>
 __global__ void __launch_bounds__(256) cconv_bwd_kernel(const lrnnx_causal_conv1d_args a, float* __restrict__ part) {
   const int lane = threadIdx.x & 63;
@@ -139,52 +196,83 @@ __global__ void __launch_bounds__(256) cconv_bwd_kernel(const lrnnx_causal_conv1
 #pragma unroll
   for (int k = 0; k < W; ++k) dw[k] = 0.f;
   const int64_t n_chunks = (L + kCCh - 1) / kCCh;
-  for (int64_t c = n_chunks - 1; c >= 0; --c) {
-    const int64_t t = c * kCCh + kCE * lane;
-    float xx[W - 1 + kCE], go[kCE];
-    load_row8<IT>(x, t, L, vec, xx + W - 1);
-    load_row8<IT>(dout, t, L, vec, go);
+  for (int64_t c = n_chunks - 1; c >= 0; c -= kCU) {
+    // group: chunks c, c - 1, ..., c - kCU + 1 (those >= 0), processed in that order
+    // raw 16-byte words of the group's chunks, converted only when used
+    Raw8<IT> rx[kCU], rg[kCU];
+    float hist[kCU][W > 1 ? W - 1 : 1];
+    if (vec && c - kCU + 1 >= 0 && (c + 1) * kCCh <= L) {
 #pragma unroll
-    for (int i = 0; i < W - 1; ++i) {
-      const float h = shfl_f(xx[W - 1 + kCE - (W - 1) + i], lane - 1);
-      const int64_t tt = t - (W - 1) + i;   // lane 0: the steps before the chunk
-      float hv = 0.f;
-      if (lane == 0 && tt >= 0 && tt < L) hv = to_f32(x[tt]);
-      xx[i] = lane == 0 ? hv : h;
-    }
-    // g = dout act'(pre) (zero past L: dout loads as zero there)
-    float g[kCE + (W > 1 ? W - 1 : 0)];
-#pragma unroll
-    for (int j = 0; j < kCE; ++j) {
-      float gj = go[j];
-      if constexpr (kSilu) {
-        float pre = bias;
-#pragma unroll
-        for (int k = 0; k < W; ++k) pre = fmaf(w[k], xx[j + k], pre);
-        gj *= silu_grad(pre);
+      for (int u = 0; u < kCU; ++u) {
+        const int64_t t = (c - u) * kCCh + kCE * lane;
+        rx[u] = ld_raw8<IT>(x + t);
+        rg[u] = ld_raw8<IT>(dout + t);
       }
-      g[j] = gj;
-      db += gj;
+    } else {
 #pragma unroll
-      for (int k = 0; k < W; ++k) dw[k] = fmaf(gj, xx[j + k], dw[k]);
+      for (int u = 0; u < kCU; ++u) {
+        // chunks before the row (c - u < 0) load as zeros
+        const int64_t t = (c - u) * kCCh + kCE * lane;
+        rx[u] = ld_raw8_guarded<IT>(x, t, L);
+        rg[u] = ld_raw8_guarded<IT>(dout, t, L);
+      }
     }
-    // the W - 1 values of g after the lane's steps: the next lane's first ones
+    // lane 0: the W - 1 inputs before each chunk
 #pragma unroll
-    for (int i = 0; i < W - 1; ++i) {
-      const float h = shfl_f(g[i], lane + 1);
-      g[kCE + i] = lane == 63 ? gnext[i] : h;
+    for (int u = 0; u < kCU; ++u) {
+#pragma unroll
+      for (int i = 0; i < W - 1; ++i) {
+        const int64_t tt = (c - u) * kCCh - (W - 1) + i;
+        hist[u][i] = 0.f;
+        if (lane == 0 && tt >= 0 && tt < L) hist[u][i] = to_f32(x[tt]);
+      }
     }
-    float dxv[kCE];
 #pragma unroll
-    for (int j = 0; j < kCE; ++j) {
-      float acc = 0.f;
+    for (int u = 0; u < kCU; ++u) {
+      if (c - u < 0) break;
+      const int64_t t = (c - u) * kCCh + kCE * lane;
+      float xx[W - 1 + kCE], go[kCE];
+      cvt_raw8<IT>(rx[u], xx + W - 1);
+      cvt_raw8<IT>(rg[u], go);
 #pragma unroll
-      for (int k = 0; k < W; ++k) acc = fmaf(w[k], g[j + W - 1 - k], acc);
-      dxv[j] = acc;
+      for (int i = 0; i < W - 1; ++i) {
+        const float h = shfl_f(xx[W - 1 + kCE - (W - 1) + i], lane - 1);
+        xx[i] = lane == 0 ? hist[u][i] : h;
+      }
+      // g = dout act'(pre) (zero past L: dout loads as zero there)
+      float g[kCE + (W > 1 ? W - 1 : 0)];
+#pragma unroll
+      for (int j = 0; j < kCE; ++j) {
+        float gj = go[j];
+        if constexpr (kSilu) {
+          float pre = bias;
+#pragma unroll
+          for (int k = 0; k < W; ++k) pre = fmaf(w[k], xx[j + k], pre);
+          gj *= silu_grad(pre);
+        }
+        g[j] = gj;
+        db += gj;
+#pragma unroll
+        for (int k = 0; k < W; ++k) dw[k] = fmaf(gj, xx[j + k], dw[k]);
+      }
+      // the W - 1 values of g after the lane's steps: the next lane's first ones
+#pragma unroll
+      for (int i = 0; i < W - 1; ++i) {
+        const float h = shfl_f(g[i], lane + 1);
+        g[kCE + i] = lane == 63 ? gnext[i] : h;
+      }
+      float dxv[kCE];
+#pragma unroll
+      for (int j = 0; j < kCE; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < W; ++k) acc = fmaf(w[k], g[j + W - 1 - k], acc);
+        dxv[j] = acc;
+      }
+      if (t < L) store_row8<IT>(dx, t, L, vec, dxv);
+#pragma unroll
+      for (int i = 0; i < W - 1; ++i) gnext[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g[i]), 0));
     }
-    if (t < L) store_row8<IT>(dx, t, L, vec, dxv);
-#pragma unroll
-    for (int i = 0; i < W - 1; ++i) gnext[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g[i]), 0));
   }
 #pragma unroll
   for (int k = 0; k < W; ++k) dw[k] = wave_allreduce_sum(dw[k]);

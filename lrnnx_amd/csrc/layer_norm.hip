@@ -21,8 +21,15 @@
 // * generic (any cols up to the 64 KiB row limit, any alignment): one wave per
 //   row, element-strided, re-reading the row per pass (from L2); dw / db come
 //   from a column kernel (thread per column, rows split over blockIdx.y).
-// Both finish dw / db with the same reduce over the partials, in a fixed order
-// (deterministic).
+// Both finish dw / db with the same two-stage reduce over the partials, in a
+// fixed order (deterministic).  The row loops' grids are sized to the number of
+// workgroups resident on the device (occupancy query), so the chip is filled
+// once with no partial second round.
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "common.h"
 
 namespace lrnnx {
@@ -30,9 +37,9 @@ namespace lrnnx {
 namespace {
 constexpr int kLnThreads = 256;
 constexpr int kLnWaves = kLnThreads / kWave;
-constexpr int kLnFwdMaxWG = 2048;
-constexpr int kLnBwdMaxWG = 512;
+constexpr int kLnBwdMaxWG = 1024;     // fast backward: at most this many dw / db partials
 constexpr int kLnColRowSplit = 64;   // generic dw / db: row blocks per column
+constexpr int kLnRedSplit = 16;      // first stage of the dw / db reduce: partial-row blocks
 
 template <typename T>
 __device__ __forceinline__ float ld_f(const void* p, int64_t i) {
@@ -371,10 +378,12 @@ __global__ void __launch_bounds__(kLnThreads) ln_wb_cols(const lrnnx_layer_norm_
   part[((int64_t)blockIdx.y * 2 + 1) * N + col] = db;
 }
 
-// dweight[col], dbias[col] = sum of the G partials; wave k of the workgroup
-// sums partials k, k + 4, ..., then the 4 wave sums are added in order.
-__global__ void __launch_bounds__(kLnThreads) ln_wb_reduce(const lrnnx_layer_norm_args a, const float* __restrict__ part,
-                                                           int64_t G) {
+// First stage of the dw / db reduce: workgroup (x, y) sums, for the 64
+// columns 64 x .. 64 x + 63, the partial rows g = 4 y + k, 4 y + k + 4 S, ...
+// (wave k, S = gridDim.y), adds its 4 waves in order and writes
+// out[(y * 2 + {0, 1}) * cols + col].
+__global__ void __launch_bounds__(kLnThreads) ln_wb_stage1(const lrnnx_layer_norm_args a, const float* __restrict__ part,
+                                                           int64_t G, float* __restrict__ out) {
   __shared__ float red[2][kLnWaves][64];
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -382,7 +391,7 @@ __global__ void __launch_bounds__(kLnThreads) ln_wb_reduce(const lrnnx_layer_nor
   const int64_t col = (int64_t)blockIdx.x * 64 + lane;
   float sw = 0.f, sb = 0.f;
   if (col < N) {
-    for (int64_t g = wid; g < G; g += kLnWaves) {
+    for (int64_t g = (int64_t)blockIdx.y * kLnWaves + wid; g < G; g += (int64_t)gridDim.y * kLnWaves) {
       sw += part[(g * 2) * N + col];
       sb += part[(g * 2 + 1) * N + col];
     }
@@ -390,11 +399,24 @@ __global__ void __launch_bounds__(kLnThreads) ln_wb_reduce(const lrnnx_layer_nor
   red[0][wid][lane] = sw;
   red[1][wid][lane] = sb;
   __syncthreads();
-  if (wid == 0 && col < N) {
-    st_any(a.wtype, a.dweight.ptr, col, (red[0][0][lane] + red[0][1][lane]) + (red[0][2][lane] + red[0][3][lane]));
-    if (a.dbias.ptr)
-      st_any(a.wtype, a.dbias.ptr, col, (red[1][0][lane] + red[1][1][lane]) + (red[1][2][lane] + red[1][3][lane]));
+  if (wid < 2 && col < N)
+    out[((int64_t)blockIdx.y * 2 + wid) * N + col] =
+        (red[wid][0][lane] + red[wid][1][lane]) + (red[wid][2][lane] + red[wid][3][lane]);
+}
+
+// dweight[col], dbias[col] = sum of the S first-stage rows, in order.
+__global__ void __launch_bounds__(kLnThreads) ln_wb_stage2(const lrnnx_layer_norm_args a, const float* __restrict__ part,
+                                                           int64_t S) {
+  const int64_t col = (int64_t)blockIdx.x * kLnThreads + threadIdx.x;
+  const int64_t N = a.cols;
+  if (col >= N) return;
+  float sw = 0.f, sb = 0.f;
+  for (int64_t g = 0; g < S; ++g) {
+    sw += part[(g * 2) * N + col];
+    sb += part[(g * 2 + 1) * N + col];
   }
+  st_any(a.wtype, a.dweight.ptr, col, sw);
+  if (a.dbias.ptr) st_any(a.wtype, a.dbias.ptr, col, sb);
 }
 
 // ------------------------------------------------------------------ host side
@@ -419,67 +441,114 @@ bool fast_ok(const lrnnx_layer_norm_args& a, bool bwd) {
          al4(a.dresidual_in, a.rtype);
 }
 
-// workgroups for `rows` rows at `per_wg` rows per workgroup and iteration
-int64_t wg_for(int64_t rows, int64_t per_wg, int64_t cap) {
-  const int64_t wg = (rows + per_wg - 1) / per_wg;
-  return wg < 1 ? 1 : (wg < cap ? wg : cap);
+// Workgroups of `kernel` (256 threads) resident on the current device at once:
+// the grid of the row loops is sized to fill the chip exactly once, so that
+// no partial second round of workgroups runs at the end.  Cached per device.
+int64_t resident_wgs(const void* kernel) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, int64_t> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1024;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find({dev, kernel});
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  int64_t n = 1024;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kLnThreads, 0) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && per_cu > 0 &&
+      cus > 0)
+    n = (int64_t)per_cu * cus;
+  cache[{dev, kernel}] = n;
+  return n;
 }
 
-int64_t n_partials(const lrnnx_layer_norm_args& a) {
-  if (fast_ok(a, true)) return wg_for(a.rows, kLnWaves / fast_wpr(a.cols), kLnBwdMaxWG);
+// row-group units of work (one workgroup iteration each)
+int64_t units(int64_t rows, int64_t per_wg) { return (rows + per_wg - 1) / per_wg; }
+
+int64_t clamp_grid(int64_t u, int64_t cap) { return u < 1 ? 1 : (u < cap ? u : cap); }
+
+// Partials of the fast backward: one per workgroup, at most kLnBwdMaxWG (an
+// upper bound independent of the device; the launch may use fewer).
+int64_t fast_bwd_partials_max(const lrnnx_layer_norm_args& a) {
+  return clamp_grid(units(a.rows, kLnWaves / fast_wpr(a.cols)), kLnBwdMaxWG);
+}
+
+int64_t generic_partials(const lrnnx_layer_norm_args& a) {
   return a.rows < kLnColRowSplit ? (a.rows < 1 ? 1 : a.rows) : kLnColRowSplit;
 }
 
+int64_t partial_rows_max(const lrnnx_layer_norm_args& a) {
+  return fast_ok(a, true) ? fast_bwd_partials_max(a) : generic_partials(a);
+}
+
 template <typename XT, typename RT, bool kRms>
-void launch_fast(const lrnnx_layer_norm_args& a, bool bwd, float* part, hipStream_t st) {
+int64_t launch_fast(const lrnnx_layer_norm_args& a, bool bwd, float* part, hipStream_t st) {
   const int64_t nch = (a.cols + 255) / 256;   // 256-column chunks per row
   const dim3 blk(kLnThreads);
-#define LN_CASE(K, W)                                                                              \
-  if (nch <= K * W) {                                                                              \
-    const dim3 grid((unsigned)wg_for(a.rows, kLnWaves / W, bwd ? kLnBwdMaxWG : kLnFwdMaxWG));      \
-    if (bwd) hipLaunchKernelGGL((ln_bwd_fast<XT, RT, K, W, kRms>), grid, blk, 0, st, a, part);     \
-    else hipLaunchKernelGGL((ln_fwd_fast<XT, RT, K, W, kRms>), grid, blk, 0, st, a);               \
-    return;                                                                                        \
+#define LN_CASE(K, W)                                                                                 \
+  if (nch <= K * W) {                                                                                 \
+    const int64_t u = units(a.rows, kLnWaves / W);                                                    \
+    if (bwd) {                                                                                        \
+      auto k = ln_bwd_fast<XT, RT, K, W, kRms>;                                                       \
+      const int64_t g = clamp_grid(u, std::min<int64_t>(kLnBwdMaxWG, resident_wgs((const void*)k))); \
+      hipLaunchKernelGGL(k, dim3((unsigned)g), blk, 0, st, a, part);                                  \
+      return g;                                                                                       \
+    }                                                                                                 \
+    auto k = ln_fwd_fast<XT, RT, K, W, kRms>;                                                         \
+    const int64_t g = clamp_grid(u, resident_wgs((const void*)k));                                    \
+    hipLaunchKernelGGL(k, dim3((unsigned)g), blk, 0, st, a);                                          \
+    return g;                                                                                         \
   }
   LN_CASE(1, 1) LN_CASE(2, 1) LN_CASE(4, 1) LN_CASE(4, 2) LN_CASE(4, 4)
 #undef LN_CASE
+  return 0;
 }
 
 template <bool kRms>
-void launch_fast_t(const lrnnx_layer_norm_args& a, bool bwd, float* part, hipStream_t st) {
+int64_t launch_fast_t(const lrnnx_layer_norm_args& a, bool bwd, float* part, hipStream_t st) {
   const bool same = a.rtype == a.xtype;
   switch (a.xtype) {
-    case LRNNX_F32: launch_fast<float, float, kRms>(a, bwd, part, st); break;
+    case LRNNX_F32: return launch_fast<float, float, kRms>(a, bwd, part, st);
     case LRNNX_BF16:
-      same ? launch_fast<bf16, bf16, kRms>(a, bwd, part, st) : launch_fast<bf16, float, kRms>(a, bwd, part, st);
-      break;
+      return same ? launch_fast<bf16, bf16, kRms>(a, bwd, part, st) : launch_fast<bf16, float, kRms>(a, bwd, part, st);
     default:
-      same ? launch_fast<f16, f16, kRms>(a, bwd, part, st) : launch_fast<f16, float, kRms>(a, bwd, part, st);
-      break;
+      return same ? launch_fast<f16, f16, kRms>(a, bwd, part, st) : launch_fast<f16, float, kRms>(a, bwd, part, st);
   }
 }
 
 template <bool kRms>
 hipError_t ln_launch_r(const lrnnx_layer_norm_args& a, bool bwd, float* part, hipStream_t st) {
   const dim3 blk(kLnThreads);
+  int64_t G = 0;   // dw / db partial rows written by the backward
   if (fast_ok(a, bwd)) {
-    launch_fast_t<kRms>(a, bwd, part, st);
+    G = launch_fast_t<kRms>(a, bwd, part, st);
   } else if (!bwd) {
-    hipLaunchKernelGGL(ln_fwd_generic<kRms>, dim3((unsigned)wg_for(a.rows, kLnWaves, kLnFwdMaxWG)), blk, 0, st, a);
+    auto k = ln_fwd_generic<kRms>;
+    hipLaunchKernelGGL(k, dim3((unsigned)clamp_grid(units(a.rows, kLnWaves), resident_wgs((const void*)k))), blk,
+                       0, st, a);
   } else {
-    hipLaunchKernelGGL(ln_bwd_generic<kRms>, dim3((unsigned)wg_for(a.rows, kLnWaves, kLnFwdMaxWG)), blk, 0, st, a);
-    hipLaunchKernelGGL(ln_wb_cols<kRms>, dim3((unsigned)((a.cols + kLnThreads - 1) / kLnThreads),
-                                              (unsigned)n_partials(a)), blk, 0, st, a, part);
+    auto k = ln_bwd_generic<kRms>;
+    hipLaunchKernelGGL(k, dim3((unsigned)clamp_grid(units(a.rows, kLnWaves), resident_wgs((const void*)k))), blk,
+                       0, st, a);
+    G = generic_partials(a);
+    hipLaunchKernelGGL(ln_wb_cols<kRms>, dim3((unsigned)((a.cols + kLnThreads - 1) / kLnThreads), (unsigned)G),
+                       blk, 0, st, a, part);
   }
-  if (bwd)
-    hipLaunchKernelGGL(ln_wb_reduce, dim3((unsigned)((a.cols + 63) / 64)), blk, 0, st, a,
-                       static_cast<const float*>(part), n_partials(a));
+  if (bwd) {
+    // two-stage fixed-order reduce; the first stage's rows follow the partials
+    const int64_t S = std::min<int64_t>(kLnRedSplit, (G + kLnWaves - 1) / kLnWaves);
+    float* part2 = part + partial_rows_max(a) * 2 * a.cols;
+    hipLaunchKernelGGL(ln_wb_stage1, dim3((unsigned)((a.cols + 63) / 64), (unsigned)S), blk, 0, st, a,
+                       static_cast<const float*>(part), G, part2);
+    hipLaunchKernelGGL(ln_wb_stage2, dim3((unsigned)((a.cols + kLnThreads - 1) / kLnThreads)), blk, 0, st, a,
+                       static_cast<const float*>(part2), S);
+  }
   return hipGetLastError();
 }
 }  // namespace
 
 int64_t ln_workspace_bytes(const lrnnx_layer_norm_args& a) {
-  return n_partials(a) * 2 * a.cols * (int64_t)sizeof(float);
+  return (partial_rows_max(a) + kLnRedSplit) * 2 * a.cols * (int64_t)sizeof(float);
 }
 
 hipError_t ln_launch(const lrnnx_layer_norm_args& a, bool bwd, float* part, hipStream_t st) {

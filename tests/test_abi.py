@@ -144,9 +144,9 @@ def test_argument_checks_mirror_reference_messages():
     assert "unsupported dtype" in _err()
     n.xtype = _lib.F16
     # fast path (cols % 4 == 0, <= 4096): one partial per workgroup (1 row each here)
-    assert L.lrnnx_layer_norm_workspace_size(n) == 1 * 2 * 64 * 4
+    assert L.lrnnx_layer_norm_workspace_size(n) == (1 + 16) * 2 * 64 * 4
     n.cols = 5000   # generic path: min(rows, 64) row blocks
-    assert L.lrnnx_layer_norm_workspace_size(n) == 4 * 2 * 5000 * 4
+    assert L.lrnnx_layer_norm_workspace_size(n) == (4 + 16) * 2 * 5000 * 4
 
 
 def test_python_api_refuses_cpu_tensors():
