@@ -244,6 +244,68 @@ class ConvStep:
         self.L_.check(self.L_.lib().lrnnx_causal_conv1d_bwd(self.a, self.stream.cuda_stream), "conv bwd")
 
 
+def decode_cfg4(torch, dev, n_layer=24, reps=50):
+    """Config 4's decode step on the scan side: ``selective_state_update`` at the
+    Mamba-130m decode shape (batch 64, d_inner 1536, d_state 16, bf16 state,
+    z gate, dt_bias + softplus) for each of 24 layers, run eagerly and as one
+    captured HIP graph per token.  Algorithmic bytes per layer: the state read
+    and written (2 x 64 x 1536 x 16 x 2) plus x, dt, z read and out written
+    (4 x 64 x 1536 x 2) plus B, C (2 x 64 x 16 x 2)."""
+    from lrnnx_amd import selective_state_update
+    g = torch.Generator(device=dev).manual_seed(4)
+    Bt, D, N = 64, 1536, 16
+    bf = torch.bfloat16
+    layers = []
+    for _ in range(n_layer):
+        layers.append(dict(
+            state=(0.1 * torch.randn(Bt, D, N, device=dev, generator=g)).to(bf),
+            x=torch.randn(Bt, D, device=dev, generator=g).to(bf),
+            dt=torch.randn(Bt, D, device=dev, generator=g).to(bf),
+            A=-torch.rand(D, N, device=dev, generator=g) - 0.5,
+            B=torch.randn(Bt, N, device=dev, generator=g).to(bf),
+            C=torch.randn(Bt, N, device=dev, generator=g).to(bf),
+            D=torch.ones(D, device=dev),
+            z=torch.randn(Bt, D, device=dev, generator=g).to(bf),
+            dt_bias=0.1 * torch.randn(D, device=dev, generator=g)))
+
+    def step():
+        for p in layers:
+            selective_state_update(p["state"], p["x"], p["dt"], p["A"], p["B"], p["C"], D=p["D"], z=p["z"],
+                                   dt_bias=p["dt_bias"], dt_softplus=True)
+
+    def timed(fn):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps   # us per token step
+
+    for _ in range(3):
+        step()
+    eager_us = timed(step)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(3):
+        graph.replay()
+    graph_us = timed(graph.replay)
+    per_layer = 2 * Bt * D * N * 2 + 4 * Bt * D * 2 + 2 * Bt * N * 2
+    tok_bytes = n_layer * per_layer
+    return {"layers": n_layer, "batch": Bt, "d_inner": D, "d_state": N,
+            "eager_us_per_token": round(eager_us, 2), "graph_us_per_token": round(graph_us, 2),
+            "graph_tokens_per_s": round(Bt * 1e6 / graph_us, 1),
+            "graph_GB_s": round(tok_bytes / (graph_us * 1e-6) / 1e9, 1), "alg_bytes_per_token": tok_bytes}
+
+
 def aux_kernels(torch, L_, dev):
     """The kernels of the callers either side of the scan (Mamba-1.4B block:
     d_model 2048, d_inner 4096, batch 8, seqlen 4096): fused residual-add
@@ -364,6 +426,7 @@ def other_configs(torch, ss, L_, dev):
     del st
     torch.cuda.empty_cache()
     res.update(aux_kernels(torch, L_, dev))
+    res["cfg4_decode_state_update"] = decode_cfg4(torch, dev)
     return res
 
 

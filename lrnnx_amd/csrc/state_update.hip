@@ -9,9 +9,10 @@
 //           (bilinear), B (dirac, s7), B sqrt(1 - A_bar^2) (rglru);
 //   state <- state * A_bar + B_bar * x   (stored in the state dtype, in place)
 //   out = sum_n state_n C_n (+ D x), times silu(z).
-// One thread owns one (batch, head, channel) row of `state` and walks its
-// d_state entries; consecutive threads own consecutive channels, so the
-// state rows they touch are contiguous in memory.
+// General kernel: one thread owns one (batch, head, channel) row of `state`;
+// consecutive threads own consecutive channels.  At d_state 16 with unit-stride
+// aligned rows a row is split over 2 (16-bit state) or 4 (fp32) lanes of one
+// quad, each reading and writing 16 bytes after all its operands are loaded.
 #include "common.h"
 
 namespace lrnnx {
@@ -27,6 +28,97 @@ __device__ __forceinline__ float ld_any(const void* p, int64_t i, int ty) {
   }
 }
 
+// exp through v_exp_f32 (a few ulp; the state is stored in its own dtype)
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+
+// Discretised (A_bar, B_bar) of one state entry (the method formulas above).
+template <int kMethod>
+__device__ __forceinline__ void discretize1(float An, float Bn, float dt, float dAv, float& Ab, float& Bb) {
+  if constexpr (kMethod == LRNNX_RGLRU) {
+    const float x = dAv * logf(An);
+    Ab = expf(x);
+    Bb = Bn * sqrtf(-expm1f(2.f * x));  // sqrt(1 - A_bar^2) without cancellation
+  } else if constexpr (kMethod == LRNNX_S7) {
+    Ab = 1.f - 1.f / (dt * dt + 0.5f);
+    Bb = Bn;
+  } else {
+    Ab = exp_fast(dAv * An);
+    if constexpr (kMethod == LRNNX_ZOH) Bb = Bn * (expf(dt * An) - 1.f) / An;
+    else if constexpr (kMethod == LRNNX_BILINEAR) Bb = Bn * (1.f / (1.f - 0.5f * dt * An)) * dt;
+    else if constexpr (kMethod == LRNNX_DIRAC) Bb = Bn;
+    else Bb = Bn * dt;
+  }
+}
+
+// Row-at-once update for d_state == kN with unit-stride, 16-byte aligned state
+// / A rows and unit-stride B / C (checked on the host).  A row is split over
+// kSplit = kN / kV adjacent lanes, each owning kV entries = 16 bytes of state,
+// so every state access of a wave is one contiguous 1 KiB; the lanes' partial
+// outputs are summed with quad DPP.  All types are compile-time (ST: state;
+// XT: x, dt, z, deltaA, B, C and out), and a lane loads all its operands
+// before it computes and stores, so a row costs one round trip to memory.
+template <typename ST, typename XT, int kMethod, int kN>
+__global__ void __launch_bounds__(256) state_update_rows(const lrnnx_state_update_args a) {
+  constexpr int kV = 16 / sizeof(ST);   // state entries per lane (one 16-byte access)
+  constexpr int kSplit = kN / kV;       // lanes per row: 2 (16-bit state) or 4 (fp32)
+  static_assert(kSplit == 2 || kSplit == 4, "a row spans 2 or 4 lanes of one quad");
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t d = t / kSplit;
+  const int part = (int)(t % kSplit);
+  // the kSplit lanes of a row sit in one quad and share d, so they leave together
+  if (d >= a.dim) return;
+  const int64_t b = blockIdx.y, hd = blockIdx.z;
+  const int64_t g = hd / (a.nheads / a.ngroups);
+  const int64_t sb = a.state_batch_indices ? (int64_t)a.state_batch_indices[b] : b;
+  ST* __restrict__ state = static_cast<ST*>(a.state) + sb * a.state_s0 + hd * a.state_s1 + d * a.state_s2 + part * kV;
+  const float* __restrict__ A = static_cast<const float*>(a.A) + hd * a.A_s0 + d * a.A_s1 + part * kV;
+  const XT* __restrict__ Bp = static_cast<const XT*>(a.B) + b * a.B_s0 + g * a.B_s1 + part * kV;
+  const XT* __restrict__ Cp = static_cast<const XT*>(a.C) + b * a.C_s0 + g * a.C_s1 + part * kV;
+  float sv[kV], Av[kV], Bv[kV], Cv[kV];
+  {
+    const uint4 raw = *reinterpret_cast<const uint4*>(state);
+    const ST* e = reinterpret_cast<const ST*>(&raw);
+#pragma unroll
+    for (int v = 0; v < kV; ++v) sv[v] = to_f32(e[v]);
+  }
+#pragma unroll
+  for (int q = 0; q < kV / 4; ++q) {
+    const float4 f = reinterpret_cast<const float4*>(A)[q];
+    Av[4 * q] = f.x; Av[4 * q + 1] = f.y; Av[4 * q + 2] = f.z; Av[4 * q + 3] = f.w;
+  }
+#pragma unroll
+  for (int v = 0; v < kV; ++v) {
+    Bv[v] = to_f32(Bp[v]);
+    Cv[v] = to_f32(Cp[v]);
+  }
+  const float x = to_f32(static_cast<const XT*>(a.x)[b * a.x_s0 + hd * a.x_s1 + d * a.x_s2]);
+  float dt = to_f32(static_cast<const XT*>(a.dt)[b * a.dt_s0 + hd * a.dt_s1 + d * a.dt_s2]);
+  if (a.dt_bias) dt += static_cast<const float*>(a.dt_bias)[hd * a.dtb_s0 + d * a.dtb_s1];
+  if (a.dt_softplus) dt = softplus20(dt);
+  const float dAv =
+      a.deltaA ? to_f32(static_cast<const XT*>(a.deltaA)[b * a.dA_s0 + hd * a.dA_s1 + d * a.dA_s2]) : dt;
+  float acc = 0.f;
+  {
+    uint4 raw;
+    ST* e = reinterpret_cast<ST*>(&raw);
+#pragma unroll
+    for (int v = 0; v < kV; ++v) {
+      float Ab, Bb;
+      discretize1<kMethod>(Av[v], Bv[v], dt, dAv, Ab, Bb);
+      e[v] = from_f32<ST>(fmaf(sv[v], Ab, Bb * x));
+      acc = fmaf(to_f32(e[v]), Cv[v], acc);
+    }
+    *reinterpret_cast<uint4*>(state) = raw;
+  }
+  acc += dpp_mov<kDppQuadXor1>(acc);
+  if constexpr (kSplit == 4) acc += dpp_mov<kDppQuadXor2>(acc);
+  if (part != 0) return;
+  if (a.D) acc += x * static_cast<const float*>(a.D)[hd * a.D_s0 + d * a.D_s1];
+  if (a.z) acc *= silu(to_f32(static_cast<const XT*>(a.z)[b * a.z_s0 + hd * a.z_s1 + d * a.z_s2]));
+  static_cast<XT*>(a.out)[b * a.out_s0 + hd * a.out_s1 + d * a.out_s2] = from_f32<XT>(acc);
+}
+
+// Entry-by-entry update: any strides, runtime dtypes.
 template <typename ST, int kMethod>
 __global__ void __launch_bounds__(256) state_update_kernel(const lrnnx_state_update_args a) {
   const int64_t d = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -34,37 +126,24 @@ __global__ void __launch_bounds__(256) state_update_kernel(const lrnnx_state_upd
   if (d >= a.dim) return;
   const int64_t g = hd / (a.nheads / a.ngroups);
   const int64_t sb = a.state_batch_indices ? (int64_t)a.state_batch_indices[b] : b;
-  ST* state = static_cast<ST*>(a.state) + sb * a.state_s0 + hd * a.state_s1 + d * a.state_s2;
+  ST* __restrict__ state = static_cast<ST*>(a.state) + sb * a.state_s0 + hd * a.state_s1 + d * a.state_s2;
   const float x = ld_any(a.x, b * a.x_s0 + hd * a.x_s1 + d * a.x_s2, a.x_type);
   float dt = ld_any(a.dt, b * a.dt_s0 + hd * a.dt_s1 + d * a.dt_s2, a.x_type);
   if (a.dt_bias) dt += static_cast<const float*>(a.dt_bias)[hd * a.dtb_s0 + d * a.dtb_s1];
   if (a.dt_softplus) dt = softplus20(dt);
   const bool has_dA = a.deltaA != nullptr;
   const float dAv = has_dA ? ld_any(a.deltaA, b * a.dA_s0 + hd * a.dA_s1 + d * a.dA_s2, a.x_type) : dt;
-  const float* A = static_cast<const float*>(a.A) + hd * a.A_s0 + d * a.A_s1;
+  const float* __restrict__ A = static_cast<const float*>(a.A) + hd * a.A_s0 + d * a.A_s1;
   float acc = 0.f;
+#pragma unroll 4
   for (int64_t n = 0; n < a.dstate; ++n) {
     const float An = A[n * a.A_s2];
     const float Bn = ld_any(a.B, b * a.B_s0 + g * a.B_s1 + n * a.B_s2, a.bc_type);
     const float Cn = ld_any(a.C, b * a.C_s0 + g * a.C_s1 + n * a.C_s2, a.bc_type);
     float Ab, Bb;
-    if constexpr (kMethod == LRNNX_RGLRU) {
-      const float x = dAv * logf(An);
-      Ab = expf(x);
-      Bb = Bn * sqrtf(-expm1f(2.f * x));  // sqrt(1 - A_bar^2) without cancellation
-    } else if constexpr (kMethod == LRNNX_S7) {
-      Ab = 1.f - 1.f / (dt * dt + 0.5f);
-      Bb = Bn;
-    } else {
-      Ab = expf(dAv * An);
-      if constexpr (kMethod == LRNNX_ZOH) Bb = Bn * (expf(dt * An) - 1.f) / An;
-      else if constexpr (kMethod == LRNNX_BILINEAR) Bb = Bn * (1.f / (1.f - 0.5f * dt * An)) * dt;
-      else if constexpr (kMethod == LRNNX_DIRAC) Bb = Bn;
-      else Bb = Bn * dt;
-    }
+    discretize1<kMethod>(An, Bn, dt, dAv, Ab, Bb);
     const int64_t si = n * a.state_s3;
-    const float s_new = to_f32(state[si]) * Ab + Bb * x;
-    const ST stored = from_f32<ST>(s_new);
+    const ST stored = from_f32<ST>(fmaf(to_f32(state[si]), Ab, Bb * x));
     state[si] = stored;
     acc = fmaf(to_f32(stored), Cn, acc);
   }
@@ -78,16 +157,51 @@ __global__ void __launch_bounds__(256) state_update_kernel(const lrnnx_state_upd
   }
 }
 
+// the d_state == 16 fast path's layout requirements
+template <typename ST>
+static bool su_rows_ok(const lrnnx_state_update_args& a) {
+  const int64_t es = sizeof(ST);
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  return a.dstate == 16 && a.state_s3 == 1 && a.A_s2 == 1 && a.B_s2 == 1 && a.C_s2 == 1 && al16(a.state) &&
+         al16(a.A) && (a.state_s0 * es) % 16 == 0 && (a.state_s1 * es) % 16 == 0 && (a.state_s2 * es) % 16 == 0 &&
+         (a.A_s0 * 4) % 16 == 0 && (a.A_s1 * 4) % 16 == 0;
+}
+
+template <typename ST, int kMethod>
+static void su_launch(const lrnnx_state_update_args& a, dim3 grid, hipStream_t st) {
+  if (su_rows_ok<ST>(a) && a.bc_type == a.x_type) {
+    // kSplit lanes per row (16 entries of 16 / sizeof(ST) per lane)
+    constexpr int64_t kSplit = 16 / (16 / sizeof(ST));
+    const dim3 rg((unsigned)((a.dim * kSplit + 255) / 256), grid.y, grid.z);
+    // x / B / C types of the row-at-once kernel: the state's own, or 16-bit with an fp32 state
+    if (a.x_type == a.state_type) {
+      hipLaunchKernelGGL((state_update_rows<ST, ST, kMethod, 16>), rg, dim3(256), 0, st, a);
+      return;
+    }
+    if constexpr (sizeof(ST) == 4) {
+      if (a.x_type == LRNNX_BF16) {
+        hipLaunchKernelGGL((state_update_rows<ST, bf16, kMethod, 16>), rg, dim3(256), 0, st, a);
+        return;
+      }
+      if (a.x_type == LRNNX_F16) {
+        hipLaunchKernelGGL((state_update_rows<ST, f16, kMethod, 16>), rg, dim3(256), 0, st, a);
+        return;
+      }
+    }
+  }
+  hipLaunchKernelGGL((state_update_kernel<ST, kMethod>), grid, dim3(256), 0, st, a);
+}
+
 template <typename ST>
 static hipError_t su_m(const lrnnx_state_update_args& a, hipStream_t st) {
   dim3 grid((unsigned)((a.dim + 255) / 256), (unsigned)a.batch, (unsigned)a.nheads);
   switch (a.method) {
-    case LRNNX_MAMBA: hipLaunchKernelGGL((state_update_kernel<ST, LRNNX_MAMBA>), grid, dim3(256), 0, st, a); break;
-    case LRNNX_ZOH: hipLaunchKernelGGL((state_update_kernel<ST, LRNNX_ZOH>), grid, dim3(256), 0, st, a); break;
-    case LRNNX_BILINEAR: hipLaunchKernelGGL((state_update_kernel<ST, LRNNX_BILINEAR>), grid, dim3(256), 0, st, a); break;
-    case LRNNX_DIRAC: hipLaunchKernelGGL((state_update_kernel<ST, LRNNX_DIRAC>), grid, dim3(256), 0, st, a); break;
-    case LRNNX_S7: hipLaunchKernelGGL((state_update_kernel<ST, LRNNX_S7>), grid, dim3(256), 0, st, a); break;
-    case LRNNX_RGLRU: hipLaunchKernelGGL((state_update_kernel<ST, LRNNX_RGLRU>), grid, dim3(256), 0, st, a); break;
+    case LRNNX_MAMBA: su_launch<ST, LRNNX_MAMBA>(a, grid, st); break;
+    case LRNNX_ZOH: su_launch<ST, LRNNX_ZOH>(a, grid, st); break;
+    case LRNNX_BILINEAR: su_launch<ST, LRNNX_BILINEAR>(a, grid, st); break;
+    case LRNNX_DIRAC: su_launch<ST, LRNNX_DIRAC>(a, grid, st); break;
+    case LRNNX_S7: su_launch<ST, LRNNX_S7>(a, grid, st); break;
+    case LRNNX_RGLRU: su_launch<ST, LRNNX_RGLRU>(a, grid, st); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -65,3 +65,47 @@ def test_state_update_batch_indices(dev):
     torch.cuda.synchronize()
     close("state", st_dev, st_ref, 1e-4, 1e-5)
     close("out", out, out_ref, 1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("layout", ["rows16_batch_indices", "strided_state16", "dstate32", "f16_state"])
+def test_state_update_layouts(dev, layout):
+    """Both kernels of the update: the row-at-once path (d_state 16, unit-stride
+    aligned rows; here with state_batch_indices and an fp16 state) and the
+    entry-by-entry path (a state view with stride 2 along d_state, d_state 32)."""
+    g = torch.Generator().manual_seed(5)
+    b, d = 4, 200
+    n = 32 if layout == "dstate32" else 16
+    sdt = torch.float16 if layout == "f16_state" else torch.bfloat16
+    pool = 6 if layout == "rows16_batch_indices" else b
+    if layout == "strided_state16":
+        big = torch.randn(pool, d, 2 * n, generator=g).to(sdt)
+        state_cpu = big[..., ::2]
+    else:
+        state_cpu = torch.randn(pool, d, n, generator=g).to(sdt)
+    idx = torch.tensor([5, 0, 3, 1], dtype=torch.int32) if layout == "rows16_batch_indices" else None
+    x = torch.randn(b, d, generator=g).to(torch.bfloat16)
+    dt = (0.5 * torch.randn(b, d, generator=g)).to(torch.bfloat16)
+    A = -torch.rand(d, n, generator=g) - 0.5
+    Bm, Cm = torch.randn(b, n, generator=g).to(torch.bfloat16), torch.randn(b, n, generator=g).to(torch.bfloat16)
+    D = torch.randn(d, generator=g)
+    z = torch.randn(b, d, generator=g).to(torch.bfloat16)
+    dt_bias = 0.1 * torch.randn(d, generator=g)
+    st_ref = state_cpu.clone().double()
+    sel = idx.long() if idx is not None else torch.arange(b)
+    sub = st_ref[sel]
+    out_ref = R.selective_state_update_ref(sub, x.double(), dt.double(), A.double(), Bm.double(), Cm.double(),
+                                           D.double(), z.double(), dt_bias.double(), True, None, "mamba",
+                                           compute_dtype=torch.float64)
+    st_ref[sel] = sub
+    if layout == "strided_state16":
+        big_dev = big.to(dev)
+        st_dev = big_dev[..., ::2]
+    else:
+        st_dev = state_cpu.to(dev)
+    out = selective_state_update(st_dev, x.to(dev), dt.to(dev), A.to(dev), Bm.to(dev), Cm.to(dev), D.to(dev),
+                                 z.to(dev), dt_bias.to(dev), True, None, idx.to(dev) if idx is not None else None)
+    torch.cuda.synchronize()
+    close(f"state {layout}", st_dev, st_ref, 2e-2, 1e-2)
+    close(f"out {layout}", out, out_ref, 2e-2, 1e-2)
+    if layout == "strided_state16":   # the entries between the view's are untouched
+        assert torch.equal(big_dev[..., 1::2].cpu(), big[..., 1::2])
