@@ -51,12 +51,12 @@ def alg_bytes(Bt, D, L, N, G, s):
     return fwd, bwd
 
 
-def make_cfg3(dev, torch, R, Bt=8, D=4096, L=4096, N=16, seed=3):
+def make_cfg3(dev, torch, R, Bt=8, D=4096, L=4096, N=16, seed=3, io=None):
     """Config-3 inputs generated on the GPU (same distributions as the oracle's
     make_selective_inputs; the full tensors are too large to create on the CPU
-    quickly)."""
+    quickly).  io: the I/O dtype (bf16 unless given)."""
     g = torch.Generator(device=dev).manual_seed(seed)
-    bf = torch.bfloat16
+    bf = io if io is not None else torch.bfloat16
     u = torch.randn(Bt, D, L, device=dev, generator=g).to(bf)
     delta = (0.5 * torch.randn(Bt, D, L, device=dev, generator=g)).to(bf)
     z = torch.randn(Bt, D, L, device=dev, generator=g).to(bf)
@@ -368,6 +368,17 @@ def time_steps(step, torch, steps, warmup):
     return total_ms, fwd_ms, bwd_ms
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(torch, R, D_slice=8, Bt=8, L=4096, N=16, D_full=4096):
     """fp32 restated reference (oracle) fwd + autograd bwd on a channel slice of
     config 3; extrapolated linearly in D (channels are independent)."""
@@ -394,14 +405,91 @@ def cpu_baseline(torch, R, D_slice=8, Bt=8, L=4096, N=16, D_full=4096):
         "sample": (f"oracle selective_scan_ref (fp32, restated reference) fwd+autograd bwd on a D-slice: "
                    f"B={Bt}, D={D_slice} of {D_full}, L={L}, N={N}; fwd {t1 - t0:.2f}s bwd {t2 - t1:.2f}s; "
                    f"full-D time extrapolated {sec * D_full / D_slice:.1f}s"),
-        "host_cpu": platform.processor() or platform.machine(),
+        "host_cpu": _cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "torch_threads": torch.get_num_threads(),
+        "torch_version": torch.__version__,
     }
+
+
+def cpu_configs(torch, R):
+    """The oracle (fp32 restatement of the reference's CPU path) at the other
+    named shapes, timed on this host: config 0 at full shape (forward only,
+    median of 5 after 2 warm-ups), config 1 and config 2 fwd + autograd bwd on
+    a channel slice, extrapolated linearly (channels are independent)."""
+    res = {}
+    inp = R.make_selective_inputs(2, 256, 512, 16, seed=0)
+    args = (inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"], inp["delta_bias"], None, True,
+            False, "mamba")
+    for _ in range(2):
+        R.selective_scan_ref(*args)
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        R.selective_scan_ref(*args)
+        ts.append(time.perf_counter() - t0)
+    t = sorted(ts)[2]
+    fb, _ = alg_bytes(2, 256, 512, 16, 1, 4)
+    res["cfg0_selective_fwd"] = {"s": round(t, 4), "elem_per_s": round(2 * 256 * 512 / t, 1),
+                                 "GB_s": round(fb / t / 1e9, 4), "sample": "full shape B=2 D=256 L=512 N=16 fp32"}
+    # config 1: LRU kernel semantics (dirac, delta = 1, identity B / C), P-slice
+    Bt, L, P, Ps = 8, 4096, 256, 32
+    d = R.make_lru_inputs(Bt, L, Ps, seed=1)
+    A = torch.log(d["Lambda"]).to(torch.complex64).unsqueeze(-1)
+    ones = torch.ones(Ps, 1, dtype=torch.complex64)
+    Bu = d["Bu"].clone().requires_grad_(True)
+    g = torch.Generator().manual_seed(2)
+    dh = torch.complex(torch.randn(Bt, Ps, L, generator=g), torch.randn(Bt, Ps, L, generator=g)) / math.sqrt(2.0)
+    t0 = time.perf_counter()
+    out, _ = R.simplified_scan_kernel_ref(Bu, torch.ones(Bt, Ps, L), A, ones, ones, None, "dirac")
+    out.backward(dh)
+    t = time.perf_counter() - t0
+    tf = t * P / Ps
+    alg1 = Bt * P * L * 8 * 5
+    res["cfg1_lru_fwd_bwd"] = {"slice_s": round(t, 3), "extrapolated_s": round(tf, 3),
+                               "elem_per_s": round(Bt * P * L / tf, 1), "GB_s": round(alg1 / tf / 1e9, 4),
+                               "sample": f"B={Bt} P={Ps} of {P} L={L} complex64, fwd + autograd bwd"}
+    # config 2: D-slice
+    Bt, D, L, N, Ds = 8, 1536, 2048, 16, 16
+    inp = R.make_selective_inputs(Bt, Ds, L, N, seed=2, itype=torch.float32)
+    leaves = {k: v.clone().requires_grad_(True) for k, v in inp.items() if isinstance(v, torch.Tensor)}
+    dout = torch.randn(Bt, Ds, L, generator=g)
+    t0 = time.perf_counter()
+    o = R.selective_scan_ref(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"],
+                             leaves["z"], leaves["delta_bias"], None, True, False, "mamba")
+    o.backward(dout)
+    t = time.perf_counter() - t0
+    tf = t * D / Ds
+    fb, bb = alg_bytes(Bt, D, L, N, 1, 2)
+    res["cfg2_selective_fwd_bwd"] = {"slice_s": round(t, 3), "extrapolated_s": round(tf, 2),
+                                     "elem_per_s": round(Bt * D * L / tf, 1), "GB_s": round((fb + bb) / tf / 1e9, 4),
+                                     "sample": f"B={Bt} D={Ds} of {D} L={L} N={N} fp32 (bf16-byte accounting)"}
+    return res
 
 
 def other_configs(torch, ss, L_, dev):
     """Config 2 (Mamba-130m layer, fwd+bwd) and config 1 (LRU complex scan,
     fwd+bwd) timings, reported beside the headline line."""
     res = {}
+    # config 0: fp32 forward only at the reference's CPU-runnable shape (launch-bound on a GPU)
+    inp0 = make_cfg3(dev, torch, None, Bt=2, D=256, L=512, N=16, seed=0, io=torch.float32)
+    fwd0 = lambda: ss.fwd(inp0["u"], inp0["delta"], inp0["A"], inp0["B"], inp0["C"], inp0["D"], inp0["z"],
+                          inp0["delta_bias"], None, True, "mamba")
+    for _ in range(3):
+        fwd0()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ms0 = []
+    for _ in range(20):
+        e0.record()
+        fwd0()
+        e1.record()
+        torch.cuda.synchronize()
+        ms0.append(e0.elapsed_time(e1))
+    t0 = sorted(ms0)[len(ms0) // 2] * 1e-3
+    fb0, _ = alg_bytes(2, 256, 512, 16, 1, 4)
+    res["cfg0_selective_fwd"] = {"ms": round(t0 * 1e3, 4), "GB_s": round(fb0 / t0 / 1e9, 1),
+                                 "elem_per_s": round(2 * 256 * 512 / t0, 1), "dtype": "f32"}
+    del inp0
     inp = make_cfg3(dev, torch, None, Bt=8, D=1536, L=2048, N=16, seed=2)
     st = SelectiveStep(inp, torch, ss, L_)
     tot, f, b = time_steps(st, torch, 10, 2)
@@ -621,6 +709,8 @@ def main():
         from oracle import scan_ref as R
         _log("timing the CPU baseline (oracle) on a channel slice")
         result["cpu_baseline"] = cpu_baseline(torch, R)
+        _log("timing the oracle at configs 0, 1, 2 (slices)")
+        result["cpu_baseline"]["other_configs"] = cpu_configs(torch, R)
     print(json.dumps(result), flush=True)
 
 
