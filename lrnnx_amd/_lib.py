@@ -198,27 +198,45 @@ def require_gpu(*tensors):
 def view(t, ndim_lead: int | None = None) -> View:
     """View of a tensor: pointer + element strides of the leading dims.
     Strides of complex tensors count complex elements (as torch does)."""
-    v = View()
     if t is None:
-        return v
-    v.ptr = t.data_ptr()
+        return View()
     st = t.stride()
     lead = st[:-1] if ndim_lead is None else st[:ndim_lead]
-    for i, s in enumerate(lead[:3]):
-        setattr(v, f"s{i}", s)
-    return v
+    return View(t.data_ptr(), *lead[:3])
 
 
 def view_full(t) -> View:
     """All strides (up to 3) of a tensor, including the last one."""
-    v = View()
     if t is None:
-        return v
-    v.ptr = t.data_ptr()
-    for i, s in enumerate(t.stride()[:3]):
-        setattr(v, f"s{i}", s)
-    return v
+        return View()
+    return View(t.data_ptr(), *t.stride()[:3])
+
+
+class _NoGuard:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_GUARD = _NoGuard()
+
+
+def on_device(t):
+    """Device guard for a launch on t's device: a no-op when that device is
+    already current (the common case), torch.cuda.device otherwise."""
+    idx = t.device.index
+    if idx is None or idx == torch.cuda.current_device():
+        return _NO_GUARD
+    return torch.cuda.device(idx)
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def stream_of(t) -> int:
+    """The current stream of t's device (a hipStream_t as an integer)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream

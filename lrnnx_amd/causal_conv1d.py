@@ -60,7 +60,7 @@ def causal_conv1d_fwd_function(x, weight, bias, seq_idx, initial_states, final_s
     a, keep = _args(x, weight, bias, bool(silu_activation))
     out = torch.empty_like(x, memory_format=torch.contiguous_format)
     a.out = _lib.view_full(out)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         _lib.check(_lib.lib().lrnnx_causal_conv1d_fwd(a, _lib.stream_of(x)), "causal_conv1d_fwd")
     return out
 
@@ -85,7 +85,7 @@ def causal_conv1d_bwd_function(x, weight, bias, dout, seq_idx, initial_states, d
     n = _lib.lib().lrnnx_causal_conv1d_workspace_size(a)
     ws = torch.empty(max(n, 256), dtype=torch.uint8, device=x.device)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         _lib.check(_lib.lib().lrnnx_causal_conv1d_bwd(a, _lib.stream_of(x)), "causal_conv1d_bwd")
     return dx, dweight, dbias, None
 
@@ -133,6 +133,6 @@ def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None, cach
     a.out = _lib.view_full(out)
     a.state_len = conv_state.shape[-1]
     a.conv_state = _lib.view_full(conv_state)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         _lib.check(_lib.lib().lrnnx_causal_conv1d_update(a, _lib.stream_of(x)), "causal_conv1d_update")
     return out.squeeze(-1) if squeeze else out

@@ -104,7 +104,7 @@ def _layer_norm_fwd(x, weight, bias, eps, residual=None, x1=None, weight1=None, 
         a.residual_out = _lib.view(residual_out)
         a.mean = mean.data_ptr() if mean is not None else None
         a.rstd = rstd.data_ptr()
-        with torch.cuda.device(x.device):
+        with _lib.on_device(x):
             _lib.check(_lib.lib().lrnnx_layer_norm_fwd(a, _lib.stream_of(x)), "layer_norm_fwd")
     if out_dtype is not None and out_dtype != y.dtype:
         y = y.to(out_dtype)
@@ -163,7 +163,7 @@ def _layer_norm_bwd(dy, x, weight, bias, eps, mean, rstd, dresidual=None, dy1=No
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
         a.workspace = ws.data_ptr()
         a.workspace_bytes = ws_bytes
-        with torch.cuda.device(x.device):
+        with _lib.on_device(x):
             _lib.check(L.lrnnx_layer_norm_bwd(a, _lib.stream_of(x)), "layer_norm_bwd")
     else:
         dw.zero_()

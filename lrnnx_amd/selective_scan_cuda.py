@@ -122,7 +122,7 @@ def run_fwd(a, u, delta, A, z, want_out=True, want_ckpt=False):
         n = _lib.lib().lrnnx_selective_scan_ckpt_size(a)
         ckpt = torch.empty(max(n, 4) // 4, dtype=torch.float32, device=u.device)
         a.ckpt = ckpt.data_ptr()
-    with torch.cuda.device(u.device):
+    with _lib.on_device(u):
         _lib.check(_lib.lib().lrnnx_selective_scan_fwd(a, _lib.stream_of(u)), "selective_scan_fwd")
     return out, x, out_z, ckpt
 
@@ -162,7 +162,7 @@ def run_bwd(a, u, delta, A, B, C, D, z, delta_bias, deltaA, dout, out, ckpt, dz=
     nws = L.lrnnx_selective_scan_workspace_size(a, 1)
     ws = torch.empty(max(nws, 256), dtype=torch.uint8, device=u.device)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-    with torch.cuda.device(u.device):
+    with _lib.on_device(u):
         _lib.check(L.lrnnx_selective_scan_bwd(a, _lib.stream_of(u)), "selective_scan_bwd")
     res = [du, ddelta, dA, dB, dC, dD, ddb]
     if deltaA is not None:

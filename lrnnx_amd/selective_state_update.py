@@ -16,6 +16,16 @@ from . import _lib
 _DISC = {"zoh": 0, "bilinear": 1, "dirac": 2, "mamba": 3, "s7": 4, "rglru": 5}
 
 
+# stride fields of each pointer in lrnnx_state_update_args (include/lrnnx_scan.h)
+_STRIDE_FIELDS = {
+    "state": ("state_s0", "state_s1", "state_s2", "state_s3"),
+    "x": ("x_s0", "x_s1", "x_s2"), "dt": ("dt_s0", "dt_s1", "dt_s2"), "A": ("A_s0", "A_s1", "A_s2"),
+    "B": ("B_s0", "B_s1", "B_s2"), "C": ("C_s0", "C_s1", "C_s2"), "D": ("D_s0", "D_s1"),
+    "z": ("z_s0", "z_s1", "z_s2"), "dt_bias": ("dtb_s0", "dtb_s1"), "deltaA": ("dA_s0", "dA_s1", "dA_s2"),
+    "out": ("out_s0", "out_s1", "out_s2"),
+}
+
+
 def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None, dt_softplus=False, deltaA=None,
                            state_batch_indices=None, discretization="mamba"):
     """state: (batch, dim, dstate) or (batch, nheads, dim, dstate), updated in place.
@@ -85,27 +95,15 @@ def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None, 
     a.method = _DISC.get(discretization.lower(), 3)
     a.dt_softplus = int(bool(dt_softplus))
 
-    def put(name, t, n, prefix=None):
-        prefix = prefix or name
+    for name, t in (("state", state), ("x", x), ("dt", dt), ("A", A), ("B", B), ("C", C), ("D", D), ("z", z),
+                    ("dt_bias", dt_bias), ("deltaA", deltaA), ("out", out)):
         if t is None:
-            return
+            continue
         setattr(a, name, t.data_ptr())
-        for i in range(n):
-            setattr(a, f"{prefix}_s{i}", t.stride(i))
-
-    put("state", state, 4)
-    put("x", x, 3)
-    put("dt", dt, 3)
-    put("A", A, 3)
-    put("B", B, 3)
-    put("C", C, 3)
-    put("D", D, 2)
-    put("z", z, 3)
-    put("dt_bias", dt_bias, 2, "dtb")
-    put("deltaA", deltaA, 3, "dA")
+        for f, st in zip(_STRIDE_FIELDS[name], t.stride()):
+            setattr(a, f, st)
     if sbi is not None:
         a.state_batch_indices = sbi.data_ptr()
-    put("out", out, 3)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         _lib.check(_lib.lib().lrnnx_selective_state_update(a, _lib.stream_of(x)), "selective_state_update")
     return out if has_heads else out.squeeze(1)

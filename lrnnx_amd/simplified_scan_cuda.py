@@ -71,7 +71,7 @@ def run_fwd(a, u, want_ckpt=False):
         ckpt = torch.empty(max(n, 8) // 8, dtype=torch.complex64, device=u.device)
         a.ckpt = ckpt.data_ptr()
     ws = _workspace(a, False, u.device)
-    with torch.cuda.device(u.device):
+    with _lib.on_device(u):
         _lib.check(_lib.lib().lrnnx_simplified_scan_fwd(a, _lib.stream_of(u)), "simplified_scan_fwd")
     del ws
     return out, x, ckpt
@@ -94,7 +94,7 @@ def run_bwd(a, u, delta, A, B, C, deltaA, dout, ckpt=None, need_ddelta=True):
     a.dA, a.dB, a.dC = _lib.view(dA, 2), _lib.view(dB, 2), _lib.view(dC, 2)
     a.ckpt = ckpt.data_ptr() if ckpt is not None else None
     ws = _workspace(a, True, u.device)
-    with torch.cuda.device(u.device):
+    with _lib.on_device(u):
         _lib.check(_lib.lib().lrnnx_simplified_scan_bwd(a, _lib.stream_of(u)), "simplified_scan_bwd")
     del ws
     res = [du, ddelta, dA, dB, dC]

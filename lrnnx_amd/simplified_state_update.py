@@ -87,6 +87,6 @@ def simplified_state_update(state, x, dt, A, B, C, D=None, deltaA=None, discreti
     put("D", D)
     put("deltaA", deltaA, "dA")
     put("out", out)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x):
         _lib.check(_lib.lib().lrnnx_simplified_state_update(a, _lib.stream_of(x)), "simplified_state_update")
     return out
