@@ -23,6 +23,25 @@ Reference anchors (paths relative to the reference checkout):
   layer_norm_bwd_ref ........ lrnnx/ops/triton/layer_norm.py:490-649 (kernel), :650-805 (host)
   s7_scan_ref ............... lrnnx/ops/s7_scan.py:179-233
   rglru_scan_ref ............ lrnnx/ops/rglru_scan.py:148-203
+
+How each function is pinned (tests/test_oracle.py; no function here is left
+"parity unpinned"):
+  selective_scan_ref / _fwd_ref  scalar fp64 brute force (oracle/brute.py) for every method,
+                                 complex and real, constant / variable B, C, deltaA; closed forms
+                                 (geometric series, cumsum at A = 0, D u at delta = 0, L = 1,
+                                 scipy.signal.lfilter); invariants (z gate, D skip, groups,
+                                 deltaA == delta, chunk continuation through x); fp64 gradcheck
+  simplified_scan_kernel_ref /   scalar brute force per state; complex IIR via lfilter (LRU);
+    simplified_scan_ref          last state == final h
+  s5_inner_ref                   equals L decode steps of simplified_state_update_ref
+  selective_state_update_ref     one step == the scan over a length-1 sequence from the state
+  simplified_state_update_ref    one step == scalar cmath arithmetic; L steps == s5_inner_ref
+  s7_scan_ref / rglru_scan_ref   equal selective_scan_ref with the kernel's discretisation
+  causal_conv1d_ref              scalar fp64 loop of the definition
+  causal_conv1d_update_ref       token-by-token decode from zero == the full conv
+  mamba_inner_ref                the same block recomputed with (b, l, d) einsums
+  layer_norm_fwd_ref             F.layer_norm / F.rms_norm of x + residual; closed-form mean, rstd
+  layer_norm_bwd_ref             fp64 autograd of the same library routines (prenorm included)
 """
 
 from __future__ import annotations
@@ -435,8 +454,8 @@ def simplified_state_update_ref(state, x, dt, A, B, C, D=None, deltaA=None, disc
 
 # ----------------------------------------------------------------------------
 # Causal conv1d (the causal-conv1d package, an optional dependency of the
-# reference, pyproject.toml:33, unpinned; its semantics are the reference's own
-# fallbacks in the Mamba layer)
+# reference whose version pyproject.toml:33 does not pin; the semantics restated
+# here are the reference's own fallbacks in the Mamba layer)
 # ----------------------------------------------------------------------------
 
 def causal_conv1d_ref(x, weight, bias=None, activation=None, compute_dtype=None):
