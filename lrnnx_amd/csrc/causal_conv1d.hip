@@ -10,7 +10,7 @@
 //
 // One wave per (b, d) row; the row is walked in chunks of 512 steps, 8
 // consecutive steps per lane (16-byte loads / stores for 16-bit types when
-// the row is aligned), 4 chunks loaded together ahead of their compute.  The W - 1 steps of history a lane needs come from the
+// the row is aligned), several chunks loaded together ahead of their compute.  The W - 1 steps of history a lane needs come from the
 // previous lane through ds_bpermute, and lane 0 takes them from the previous
 // chunk (forward) or from a few extra loads (backward, which walks right to
 // left so that the W - 1 steps of g to the right come from the chunk just
@@ -113,9 +113,21 @@ __device__ __forceinline__ Raw8<IT> ld_raw8_guarded(const IT* p, int64_t t, int6
   return r;
 }
 
-// Chunks of a row loaded together before any of them is used (more bytes in
-// flight per wave: kCU x 16 (or 32) bytes per lane per array).
-constexpr int kCU = 4;
+// A chunk that is not wholly inside the row: per lane, 16-byte words when the
+// lane's 8 elements are, element by element otherwise (only the lane holding
+// the row's end, and lanes before the row's start, take that path)
+template <typename IT>
+__device__ __forceinline__ Raw8<IT> ld_raw8_part(const IT* p, int64_t t, int64_t L, bool vec) {
+  if (vec && t >= 0 && t + kCE <= L) return ld_raw8<IT>(p + t);
+  return ld_raw8_guarded<IT>(p, t, L);
+}
+
+// Chunks of a row loaded together before any of them is used: bytes in flight
+// per wave against registers (occupancy).  Measured at B 8, D 4096, L 4096,
+// W 4, bf16: the forward is fastest at 8, the backward (two arrays, more
+// registers per chunk) at 1.
+constexpr int kCUf = 8;
+constexpr int kCUb = 1;
 
 template <typename IT, int W, bool kSilu>
 __global__ void __launch_bounds__(256) cconv_fwd_kernel(const lrnnx_causal_conv1d_args a) {
@@ -134,18 +146,19 @@ __global__ void __launch_bounds__(256) cconv_fwd_kernel(const lrnnx_causal_conv1
   float prev[W > 1 ? W - 1 : 1];   // the W - 1 inputs before the chunk
 #pragma unroll
   for (int i = 0; i < W - 1; ++i) prev[i] = 0.f;
-  for (int64_t t0 = 0; t0 < L; t0 += kCU * kCCh) {
+  for (int64_t t0 = 0; t0 < L; t0 += kCUf * kCCh) {
     // raw 16-byte words of the group's chunks, converted only when used
-    Raw8<IT> raw[kCU];
-    if (vec && t0 + kCU * kCCh <= L) {
+    // a chunk wholly inside the row loads as 16-byte words, a partial one element by element
+    // (the condition is uniform over the wave)
+    Raw8<IT> raw[kCUf];
 #pragma unroll
-      for (int u = 0; u < kCU; ++u) raw[u] = ld_raw8<IT>(x + t0 + u * kCCh + kCE * lane);
-    } else {
-#pragma unroll
-      for (int u = 0; u < kCU; ++u) raw[u] = ld_raw8_guarded<IT>(x, t0 + u * kCCh + kCE * lane, L);
+    for (int u = 0; u < kCUf; ++u) {
+      const int64_t t = t0 + u * kCCh + kCE * lane;
+      if (vec && t0 + (u + 1) * kCCh <= L) raw[u] = ld_raw8<IT>(x + t);
+      else raw[u] = ld_raw8_part<IT>(x, t, L, vec);
     }
 #pragma unroll
-    for (int u = 0; u < kCU; ++u) {
+    for (int u = 0; u < kCUf; ++u) {
       if (t0 + u * kCCh >= L) break;
       const int64_t t = t0 + u * kCCh + kCE * lane;
       float xx[W - 1 + kCE];
@@ -172,7 +185,7 @@ __global__ void __launch_bounds__(256) cconv_fwd_kernel(const lrnnx_causal_conv1
 }
 
 // dx (row) and per-row partials of dw[W], dbias -> part[row * (W + 1) + k].
-// Walks the row right to left, kCU chunks per group (loaded together).
+// Walks the row right to left, kCUb chunks per group (loaded together).
 template <typename IT, int W, bool kSilu>
 __global__ void __launch_bounds__(256) cconv_bwd_kernel(const lrnnx_causal_conv1d_args a, float* __restrict__ part) {
   const int lane = threadIdx.x & 63;
@@ -196,30 +209,27 @@ __global__ void __launch_bounds__(256) cconv_bwd_kernel(const lrnnx_causal_conv1
 #pragma unroll
   for (int k = 0; k < W; ++k) dw[k] = 0.f;
   const int64_t n_chunks = (L + kCCh - 1) / kCCh;
-  for (int64_t c = n_chunks - 1; c >= 0; c -= kCU) {
-    // group: chunks c, c - 1, ..., c - kCU + 1 (those >= 0), processed in that order
+  for (int64_t c = n_chunks - 1; c >= 0; c -= kCUb) {
+    // group: chunks c, c - 1, ..., c - kCUb + 1 (those >= 0), processed in that order
     // raw 16-byte words of the group's chunks, converted only when used
-    Raw8<IT> rx[kCU], rg[kCU];
-    float hist[kCU][W > 1 ? W - 1 : 1];
-    if (vec && c - kCU + 1 >= 0 && (c + 1) * kCCh <= L) {
+    Raw8<IT> rx[kCUb], rg[kCUb];
+    float hist[kCUb][W > 1 ? W - 1 : 1];
+    // a chunk wholly inside the row loads as 16-byte words, a partial one (or one
+    // before the row, c - u < 0: zeros) element by element; uniform over the wave
 #pragma unroll
-      for (int u = 0; u < kCU; ++u) {
-        const int64_t t = (c - u) * kCCh + kCE * lane;
+    for (int u = 0; u < kCUb; ++u) {
+      const int64_t t = (c - u) * kCCh + kCE * lane;
+      if (vec && c - u >= 0 && (c - u + 1) * kCCh <= L) {
         rx[u] = ld_raw8<IT>(x + t);
         rg[u] = ld_raw8<IT>(dout + t);
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < kCU; ++u) {
-        // chunks before the row (c - u < 0) load as zeros
-        const int64_t t = (c - u) * kCCh + kCE * lane;
-        rx[u] = ld_raw8_guarded<IT>(x, t, L);
-        rg[u] = ld_raw8_guarded<IT>(dout, t, L);
+      } else {
+        rx[u] = ld_raw8_part<IT>(x, t, L, vec);
+        rg[u] = ld_raw8_part<IT>(dout, t, L, vec);
       }
     }
     // lane 0: the W - 1 inputs before each chunk
 #pragma unroll
-    for (int u = 0; u < kCU; ++u) {
+    for (int u = 0; u < kCUb; ++u) {
 #pragma unroll
       for (int i = 0; i < W - 1; ++i) {
         const int64_t tt = (c - u) * kCCh - (W - 1) + i;
@@ -228,7 +238,7 @@ __global__ void __launch_bounds__(256) cconv_bwd_kernel(const lrnnx_causal_conv1
       }
     }
 #pragma unroll
-    for (int u = 0; u < kCU; ++u) {
+    for (int u = 0; u < kCUb; ++u) {
       if (c - u < 0) break;
       const int64_t t = (c - u) * kCCh + kCE * lane;
       float xx[W - 1 + kCE], go[kCE];
