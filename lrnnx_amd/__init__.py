@@ -13,6 +13,8 @@ Public API (same names, arguments and return conventions as the reference's
 * ``mamba_inner_fn`` / ``MambaInnerFn``  (lrnnx/ops/selective_scan.py:389-786)
 * ``layer_norm_fn``, ``rms_norm_fn``, ``LayerNormFn``, ``RMSNorm``: the fused
   residual-add LayerNorm / RMSNorm (lrnnx/ops/triton/layer_norm.py)
+* ``s7_scan_fn`` / ``S7ScanFn``, ``s7_inner_fn``  (lrnnx/ops/s7_scan.py)
+* ``rglru_scan_fn`` / ``RGLRUScanFn``, ``rglru_inner_fn``  (lrnnx/ops/rglru_scan.py)
 * ``selective_scan_cuda``, ``simplified_scan_cuda``: drop-in replacements of
   the reference's pybind11 extension modules (``fwd`` / ``bwd``).
 
@@ -25,6 +27,8 @@ from .causal_conv1d import (causal_conv1d_bwd_function, causal_conv1d_fn, causal
                             causal_conv1d_update)
 from .layer_norm import LayerNormFn, RMSNorm, layer_norm_fn, rms_norm_fn  # noqa: F401
 from .mamba_inner import MambaInnerFn, mamba_inner_fn  # noqa: F401
+from .rglru_scan import RGLRUScanFn, rglru_inner_fn, rglru_scan_fn  # noqa: F401
+from .s7_scan import S7ScanFn, s7_inner_fn, s7_scan_fn  # noqa: F401
 from .selective_scan import SelectiveScanFn, selective_scan_fn  # noqa: F401
 from .selective_state_update import selective_state_update  # noqa: F401
 from .simplified_state_update import simplified_state_update  # noqa: F401

@@ -23,6 +23,8 @@ Reference anchors (paths relative to the reference checkout):
   layer_norm_bwd_ref ........ lrnnx/ops/triton/layer_norm.py:490-649 (kernel), :650-805 (host)
   s7_scan_ref ............... lrnnx/ops/s7_scan.py:179-233
   rglru_scan_ref ............ lrnnx/ops/rglru_scan.py:148-203
+  s7_inner_ref .............. lrnnx/ops/s7_scan.py:512-552
+  rglru_inner_ref ........... lrnnx/ops/rglru_scan.py:577-679
 
 How each function is pinned (tests/test_oracle.py; no function here is left
 "parity unpinned"):
@@ -42,6 +44,7 @@ How each function is pinned (tests/test_oracle.py; no function here is left
   mamba_inner_ref                the same block recomputed with (b, l, d) einsums
   layer_norm_fwd_ref             F.layer_norm / F.rms_norm of x + residual; closed-form mean, rstd
   layer_norm_bwd_ref             fp64 autograd of the same library routines (prenorm included)
+  s7_inner_ref / rglru_inner_ref scalar Python loops of the blocks' definitions on tiny shapes
 """
 
 from __future__ import annotations
@@ -644,6 +647,56 @@ def rglru_scan_ref(u, delta, A, return_last_state=False, compute_dtype=None):
     y = torch.stack(hs, dim=-1).sum(dim=2)
     out = y.to(u.dtype) if compute_dtype is None else y
     return (out, h) if return_last_state else out
+
+
+def s7_inner_ref(hidden_states, in_proj_weight, x_proj_weight, gate_proj_weight, d_state, base_params,
+                 compute_dtype=None):
+    """Restatement of ``s7_inner_ref`` (s7_scan.py:512-552): in_proj, x_proj
+    split into A (+ base_params), B, C, D, bias; the S7 scan; D skip; exact GELU
+    and sigmoid gate; residual.  hidden_states (b, L, d_model)."""
+    cast = (lambda t: t) if compute_dtype is None else (lambda t: t.to(compute_dtype))
+    hs, Wi, Wx, Wg, base = (cast(t) for t in (hidden_states, in_proj_weight, x_proj_weight, gate_proj_weight,
+                                               base_params))
+    b, L, dm = hs.shape
+    n = d_state
+    x = F.linear(hs, Wi)
+    x_dbl = F.linear(x.reshape(b * L, dm), Wx)
+    A, B, C, D, bias = torch.split(x_dbl, [n, dm * n, dm * n, dm, n], dim=-1)
+    A = A.reshape(b, L, n).permute(0, 2, 1) + base[None, :, None]
+    B = B.reshape(b, L, dm, n).permute(0, 3, 2, 1)
+    C = C.reshape(b, L, dm, n).permute(0, 2, 3, 1)
+    D_tv = D.reshape(b, L, dm).permute(0, 2, 1)
+    bias = bias.reshape(b, L, n).permute(0, 2, 1)
+    u = x.permute(0, 2, 1)
+    y = s7_scan_ref(u, A, B, C, bias=bias, compute_dtype=compute_dtype) + D_tv * u
+    y_t = y.permute(0, 2, 1)
+    gate = torch.sigmoid(F.linear(F.gelu(y_t), Wg))
+    return gate * y_t + hs
+
+
+def rglru_inner_ref(x, conv1d_weight, conv1d_bias, a, recurrent_gate_weight, recurrent_gate_bias, input_gate_weight,
+                    input_gate_bias, out_proj_weight, out_proj_bias, gate, c=8.0, compute_dtype=None):
+    """Restatement of ``rglru_inner_ref`` (rglru_scan.py:577-679): causal conv
+    (no activation), sigmoid recurrence / input gates, delta = c r, u = i x,
+    the RG-LRU scan, stream-1 gate, output projection.  x (b, d, L)."""
+    rdt = _real(compute_dtype)
+    cast = lambda t: None if t is None else t.to(rdt)
+    dtype_in = x.dtype
+    xf, af, g = cast(x), cast(a), cast(gate)
+    if af.dim() == 1:
+        af = af.unsqueeze(-1)
+    w = cast(conv1d_weight)
+    w = w[:, 0, :] if w.dim() == 3 else w
+    xc = causal_conv1d_ref(xf, w, cast(conv1d_bias), None, compute_dtype=rdt)
+    b, d, L = xc.shape
+    flat = xc.permute(0, 2, 1).reshape(b * L, d)
+    r = torch.sigmoid(F.linear(flat, cast(recurrent_gate_weight), cast(recurrent_gate_bias)))
+    i = torch.sigmoid(F.linear(flat, cast(input_gate_weight), cast(input_gate_bias)))
+    r = r.reshape(b, L, d).permute(0, 2, 1)
+    i = i.reshape(b, L, d).permute(0, 2, 1)
+    y = rglru_scan_ref(i * xc, c * r, af, compute_dtype=rdt).permute(0, 2, 1)
+    out = F.linear(g * y, cast(out_proj_weight), cast(out_proj_bias))
+    return out.to(dtype_in) if compute_dtype is None else out
 
 
 # ----------------------------------------------------------------------------

@@ -474,3 +474,77 @@ def test_layer_norm_ref_output_dtypes_follow_host_code():
     dx, dw, db, dri = R.layer_norm_bwd_ref(torch.randn(3, 16, generator=g).to(torch.bfloat16), xs, w, None, mean,
                                            rstd, has_residual=True, x_dtype=torch.bfloat16)
     assert dx.dtype == torch.bfloat16 and dri.dtype == torch.float32 and db is None and dw.dtype == torch.float32
+
+
+# ---------------------------------------------------------------- S7 / RG-LRU blocks
+def _gelu(v):
+    return 0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0)))
+
+
+def _sig(v):
+    return 1.0 / (1.0 + math.exp(-v))
+
+
+def test_s7_inner_ref_vs_scalar_loop():
+    g = torch.Generator().manual_seed(41)
+    b, L, dm, n = 2, 4, 3, 2
+    hs = torch.randn(b, L, dm, generator=g, dtype=D64)
+    Wi = torch.randn(dm, dm, generator=g, dtype=D64) * 0.5
+    Wx = torch.randn(n + 2 * dm * n + dm + n, dm, generator=g, dtype=D64) * 0.5
+    Wg = torch.randn(dm, dm, generator=g, dtype=D64) * 0.5
+    base = torch.randn(n, generator=g, dtype=D64)
+    out = R.s7_inner_ref(hs, Wi, Wx, Wg, n, base, compute_dtype=D64)
+    for bi in range(b):
+        h = [0.0] * n
+        for t in range(L):
+            x = [sum(float(Wi[o, k]) * float(hs[bi, t, k]) for k in range(dm)) for o in range(dm)]
+            xd = [sum(float(Wx[o, k]) * x[k] for k in range(dm)) for o in range(Wx.shape[0])]
+            A = xd[:n]
+            Bm = xd[n:n + dm * n]              # (h n), n fastest
+            Cm = xd[n + dm * n:n + 2 * dm * n]
+            Dm = xd[n + 2 * dm * n:n + 2 * dm * n + dm]
+            bias = xd[n + 2 * dm * n + dm:]
+            for k in range(n):
+                a = A[k] + float(base[k])
+                ab = 1.0 - 1.0 / (a * a + 0.5)
+                bu = sum(Bm[hh * n + k] * x[hh] for hh in range(dm)) + bias[k]
+                h[k] = ab * h[k] + bu
+            y = [sum(Cm[hh * n + k] * h[k] for k in range(n)) + Dm[hh] * x[hh] for hh in range(dm)]
+            gy = [_gelu(v) for v in y]
+            for o in range(dm):
+                gate = _sig(sum(float(Wg[o, k]) * gy[k] for k in range(dm)))
+                ref = gate * y[o] + float(hs[bi, t, o])
+                assert abs(ref - float(out[bi, t, o])) < 1e-10
+
+
+def test_rglru_inner_ref_vs_scalar_loop():
+    g = torch.Generator().manual_seed(42)
+    b, d, L, w, n, dm, c = 2, 3, 5, 3, 2, 2, 8.0
+    x = torch.randn(b, d, L, generator=g, dtype=D64)
+    cw = torch.randn(d, 1, w, generator=g, dtype=D64) * 0.5
+    cb = torch.randn(d, generator=g, dtype=D64) * 0.1
+    a = torch.rand(d, n, generator=g, dtype=D64) * 0.5 + 0.45
+    Wr, Wi = (torch.randn(d, d, generator=g, dtype=D64) * 0.5 for _ in range(2))
+    br, bi_ = (torch.randn(d, generator=g, dtype=D64) * 0.1 for _ in range(2))
+    Wo = torch.randn(dm, d, generator=g, dtype=D64) * 0.5
+    bo = torch.randn(dm, generator=g, dtype=D64)
+    gate = torch.randn(b, L, d, generator=g, dtype=D64)
+    out = R.rglru_inner_ref(x, cw, cb, a, Wr, br, Wi, bi_, Wo, bo, gate, c, compute_dtype=D64)
+    for bb in range(b):
+        h = [[0.0] * n for _ in range(d)]
+        for t in range(L):
+            xc = [float(cb[dd]) + sum(float(cw[dd, 0, k]) * float(x[bb, dd, t - w + 1 + k])
+                                      for k in range(w) if t - w + 1 + k >= 0) for dd in range(d)]
+            r = [_sig(sum(float(Wr[o, k]) * xc[k] for k in range(d)) + float(br[o])) for o in range(d)]
+            ig = [_sig(sum(float(Wi[o, k]) * xc[k] for k in range(d)) + float(bi_[o])) for o in range(d)]
+            y = []
+            for dd in range(d):
+                acc = 0.0
+                for k in range(n):
+                    ab = float(a[dd, k]) ** (c * r[dd])
+                    h[dd][k] = ab * h[dd][k] + math.sqrt(1.0 - ab * ab) * ig[dd] * xc[dd]
+                    acc += h[dd][k]
+                y.append(acc * float(gate[bb, t, dd]))
+            for o in range(dm):
+                ref = sum(float(Wo[o, k]) * y[k] for k in range(d)) + float(bo[o])
+                assert abs(ref - float(out[bb, t, o])) < 1e-10
