@@ -16,9 +16,15 @@ Differences from the reference, each where the reference cannot run or is wrong:
 * ``out_proj_bias``'s gradient is the sum over batch and length per output
   channel (the reference sums ``dout`` after reshaping it to (e, b l) over both
   dimensions, which gives a scalar);
-* the B / C / dt RMSNorm options raise NotImplementedError: the reference's
-  backward re-normalises the already normalised B / C and drops their RMSNorm
-  gradient, and the Mamba layer never passes them (mamba.py:246-259).
+* the B / C / dt RMSNorm options (selective_scan.py:501-518: RMSNorm over
+  d_state of variable B / C after their projection bias, over the channels of
+  delta) run in this package's fused norm kernels with their full backward:
+  the gradients of B / C / delta pass through the norm, and the norm weights
+  get gradients.  The reference's backward re-normalises the already
+  normalised B / C (:608-630), passes dB / dC / ddelta through without the
+  norm's Jacobian and returns no gradient for the weights (:731).  They are
+  supported for real A and variable B / C (the reference's rearrange cannot
+  take the complex layout).
 """
 
 from __future__ import annotations
@@ -28,6 +34,32 @@ import torch.nn.functional as F
 
 from . import selective_scan_cuda as _ss
 from .causal_conv1d import causal_conv1d_bwd_function, causal_conv1d_fwd_function
+from .layer_norm import _layer_norm_bwd, _layer_norm_fwd
+
+
+def _rms_rows(X, w, eps):
+    """RMSNorm over the last dim of a (rows, n) matrix -> (normalised, rstd)."""
+    y, _, _, rstd, _, _, _, _ = _layer_norm_fwd(X, w.contiguous(), None, eps, is_rms_norm=True)
+    return y, rstd
+
+
+def _rms_rows_bwd(dY, X, w, rstd, eps):
+    """Gradients of _rms_rows: (dX, dw)."""
+    dX, dw, _, _, _, _, _ = _layer_norm_bwd(dY.contiguous(), X, w.contiguous(), None, eps, None, rstd,
+                                            is_rms_norm=True)
+    return dX, dw
+
+
+def _delta_rows(delta):
+    # b d l -> (b l) d
+    b, d, L = delta.shape
+    return delta.transpose(1, 2).reshape(b * L, d).contiguous()
+
+
+def _delta_from_rows(rows, b):
+    # (b l) d -> b d l (unit stride along l)
+    bl, d = rows.shape
+    return rows.reshape(b, bl // b, d).transpose(1, 2).contiguous()
 
 
 def _bc_from_xdbl(X, L, complex_A):
@@ -57,12 +89,14 @@ class MambaInnerFn(torch.autograd.Function):
                 b_c_dt_rms_eps=1e-6):
         """xz: (batch, 2 * dim, seqlen)"""
         assert checkpoint_lvl in [0, 1]
-        if b_rms_weight is not None or c_rms_weight is not None or dt_rms_weight is not None:
-            raise NotImplementedError("mamba_inner_fn: the B / C / dt RMSNorm options are not supported")
         L = xz.shape[-1]
         delta_rank = delta_proj_weight.shape[1]
         complex_A = A.is_complex()
         d_state = A.shape[-1] * (2 if complex_A else 1)
+        if complex_A and (b_rms_weight is not None or c_rms_weight is not None or dt_rms_weight is not None):
+            raise NotImplementedError("mamba_inner_fn: the B / C / dt RMSNorm options need a real A")
+        if (b_rms_weight is not None and B is not None) or (c_rms_weight is not None and C is not None):
+            raise NotImplementedError("mamba_inner_fn: the B / C RMSNorm options apply to variable B / C")
         if torch.is_autocast_enabled():
             dt_ = torch.get_autocast_gpu_dtype()
             x_proj_weight = x_proj_weight.to(dtype=dt_)
@@ -78,12 +112,23 @@ class MambaInnerFn(torch.autograd.Function):
         b = xz.shape[0]
         x_dbl = F.linear(conv1d_out.transpose(1, 2).reshape(b * L, -1), x_proj_weight)   # (b l) (r + 2n)
         delta = (delta_proj_weight @ x_dbl[:, :delta_rank].t()).reshape(-1, b, L).transpose(0, 1)   # b d l
+        eps = b_c_dt_rms_eps
+        rms_saved = [None] * 6   # B rows, B rstd, C rows, C rstd, delta rows, delta rstd
+        if dt_rms_weight is not None:
+            rows = _delta_rows(delta)
+            normed, rstd = _rms_rows(rows, dt_rms_weight, eps)
+            delta = _delta_from_rows(normed, b)
+            rms_saved[4], rms_saved[5] = (rows if checkpoint_lvl == 0 else None), rstd
         ctx.is_variable_B, ctx.is_variable_C = B is None, C is None
         ctx.B_proj_bias_is_None, ctx.C_proj_bias_is_None = B_proj_bias is None, C_proj_bias is None
         if B is None:
             Bx = x_dbl[:, delta_rank:delta_rank + d_state]
             if B_proj_bias is not None:
                 Bx = Bx + B_proj_bias.to(dtype=Bx.dtype)
+            if b_rms_weight is not None:
+                Bx = Bx.contiguous()
+                rms_saved[0] = Bx
+                Bx, rms_saved[1] = _rms_rows(Bx, b_rms_weight, eps)
             B = _bc_from_xdbl(Bx, L, complex_A)
         elif B.stride(-1) != 1:
             B = B.contiguous()
@@ -91,6 +136,10 @@ class MambaInnerFn(torch.autograd.Function):
             Cx = x_dbl[:, -d_state:]
             if C_proj_bias is not None:
                 Cx = Cx + C_proj_bias.to(dtype=Cx.dtype)
+            if c_rms_weight is not None:
+                Cx = Cx.contiguous()
+                rms_saved[2] = Cx
+                Cx, rms_saved[3] = _rms_rows(Cx, c_rms_weight, eps)
             C = _bc_from_xdbl(Cx, L, complex_A)
         elif C.stride(-1) != 1:
             C = C.contiguous()
@@ -103,8 +152,10 @@ class MambaInnerFn(torch.autograd.Function):
         ctx.checkpoint_lvl = checkpoint_lvl
         if checkpoint_lvl >= 1:   # recomputed in the backward
             conv1d_out, delta = None, None
+        ctx.eps = eps
         ctx.save_for_backward(xz, conv1d_weight, conv1d_bias, x_dbl, x_proj_weight, delta_proj_weight,
-                              out_proj_weight, conv1d_out, delta, A, B, C, D, delta_bias, ckpt, out)
+                              out_proj_weight, conv1d_out, delta, A, B, C, D, delta_bias, ckpt, out,
+                              b_rms_weight, c_rms_weight, dt_rms_weight, *rms_saved)
         return F.linear(out_z.transpose(1, 2), out_proj_weight, out_proj_bias)
 
     @staticmethod
@@ -112,7 +163,8 @@ class MambaInnerFn(torch.autograd.Function):
     def backward(ctx, dout):
         # dout: (batch, seqlen, dim_model)
         (xz, conv1d_weight, conv1d_bias, x_dbl, x_proj_weight, delta_proj_weight, out_proj_weight, conv1d_out,
-         delta, A, B, C, D, delta_bias, ckpt, out) = ctx.saved_tensors
+         delta, A, B, C, D, delta_bias, ckpt, out, b_rms_weight, c_rms_weight, dt_rms_weight,
+         B_rows, B_rstd, C_rows, C_rstd, dt_rows, dt_rstd) = ctx.saved_tensors
         L = xz.shape[-1]
         b = xz.shape[0]
         delta_rank = delta_proj_weight.shape[1]
@@ -124,6 +176,9 @@ class MambaInnerFn(torch.autograd.Function):
         if ctx.checkpoint_lvl == 1:
             conv1d_out = causal_conv1d_fwd_function(x, conv1d_weight, conv1d_bias, None, None, None, True)
             delta = (delta_proj_weight @ x_dbl[:, :delta_rank].t()).reshape(-1, b, L).transpose(0, 1)
+            if dt_rms_weight is not None:   # the forward's normalisation, with its saved rstd
+                dt_rows = _delta_rows(delta)
+                delta = _delta_from_rows(_rms_rows(dt_rows, dt_rms_weight, ctx.eps)[0], b)
         dxz = torch.empty_like(xz)
         dx, dz = dxz.chunk(2, dim=1)
         dout2 = dout.reshape(b * L, -1).t()                                   # e (b l)
@@ -139,16 +194,26 @@ class MambaInnerFn(torch.autograd.Function):
         dD = dD if D is not None else None
         dx_dbl = torch.empty_like(x_dbl)
         dB_proj_bias = dC_proj_bias = None
+        db_rms = dc_rms = ddt_rms = None
         if ctx.is_variable_B:
             dBx = _bc_to_xdbl(dB, complex_A).to(x_dbl.dtype)
+            if b_rms_weight is not None:
+                dBx, db_rms = _rms_rows_bwd(dBx, B_rows, b_rms_weight, B_rstd, ctx.eps)
+                dBx = dBx.to(x_dbl.dtype)
             dB_proj_bias = dBx.sum(0) if not ctx.B_proj_bias_is_None else None
             dx_dbl[:, delta_rank:delta_rank + d_state] = dBx
             dB = None
         if ctx.is_variable_C:
             dCx = _bc_to_xdbl(dC, complex_A).to(x_dbl.dtype)
+            if c_rms_weight is not None:
+                dCx, dc_rms = _rms_rows_bwd(dCx, C_rows, c_rms_weight, C_rstd, ctx.eps)
+                dCx = dCx.to(x_dbl.dtype)
             dC_proj_bias = dCx.sum(0) if not ctx.C_proj_bias_is_None else None
             dx_dbl[:, -d_state:] = dCx
             dC = None
+        if dt_rms_weight is not None:
+            drows, ddt_rms = _rms_rows_bwd(_delta_rows(ddelta), dt_rows, dt_rms_weight, dt_rstd, ctx.eps)
+            ddelta = _delta_from_rows(drows.to(ddelta.dtype), b)
         ddelta2 = ddelta.transpose(0, 1).reshape(ddelta.shape[1], -1)        # d (b l)
         ddelta_proj_weight = ddelta2 @ x_dbl[:, :delta_rank]                  # d r
         dx_dbl[:, :delta_rank] = ddelta2.t() @ delta_proj_weight              # (b l) r
@@ -161,7 +226,10 @@ class MambaInnerFn(torch.autograd.Function):
         dconv1d_bias = dconv1d_bias.to(conv1d_bias.dtype) if conv1d_bias is not None else None
         return (dxz, dconv1d_weight, dconv1d_bias, dx_proj_weight, ddelta_proj_weight, dout_proj_weight,
                 dout_proj_bias, dA, dB, dC, dD, ddelta_bias if delta_bias is not None else None, dB_proj_bias,
-                dC_proj_bias, None, None, None, None, None, None)
+                dC_proj_bias, None, None,
+                db_rms.to(b_rms_weight.dtype) if db_rms is not None else None,
+                dc_rms.to(c_rms_weight.dtype) if dc_rms is not None else None,
+                ddt_rms.to(dt_rms_weight.dtype) if ddt_rms is not None else None, None)
 
 
 def mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight, out_proj_bias,

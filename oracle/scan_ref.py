@@ -506,12 +506,21 @@ def causal_conv1d_update_ref(x, conv_state, weight, bias=None, activation=None, 
     return out.squeeze(-1) if squeeze else out
 
 
+def _rms_last(X, w, eps):
+    """RMSNorm over the last dimension: X / sqrt(mean(X^2) + eps) * w."""
+    return X / torch.sqrt((X * X).mean(-1, keepdim=True) + eps) * w
+
+
 def mamba_inner_ref(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
                     out_proj_bias, A, B=None, C=None, D=None, delta_bias=None, B_proj_bias=None,
-                    C_proj_bias=None, delta_softplus=True, compute_dtype=None):
+                    C_proj_bias=None, delta_softplus=True, b_rms_weight=None, c_rms_weight=None,
+                    dt_rms_weight=None, b_c_dt_rms_eps=1e-6, compute_dtype=None):
     """Restatement of ``mamba_inner_ref`` (selective_scan.py:789-846): causal
     conv (silu) -> x_proj -> delta_proj -> selective scan (variable B / C from
-    x_proj) -> out_proj.  xz (b, 2d, l); conv1d_weight (d, 1, w)."""
+    x_proj) -> out_proj.  xz (b, 2d, l); conv1d_weight (d, 1, w).  The optional
+    RMSNorms of MambaInnerFn's forward (selective_scan.py:501-518) apply over
+    d_state to the variable B / C after their projection bias and over the
+    channels to delta."""
     rdt = _real(compute_dtype)
     L = xz.shape[-1]
     delta_rank = delta_proj_weight.shape[1]
@@ -522,15 +531,21 @@ def mamba_inner_ref(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_we
     x_dbl = xt @ x_proj_weight.to(rdt).t()                                        # (b l) (r + 2n)
     delta = (delta_proj_weight.to(rdt) @ x_dbl[:, :delta_rank].t())               # d (b l)
     delta = delta.reshape(-1, xz.shape[0], L).transpose(0, 1)                     # b d l
+    if dt_rms_weight is not None:
+        delta = _rms_last(delta.transpose(1, 2), dt_rms_weight.to(rdt), b_c_dt_rms_eps).transpose(1, 2)
     if B is None:
         B = x_dbl[:, delta_rank:delta_rank + d_state]
         if B_proj_bias is not None:
             B = B + B_proj_bias.to(rdt)
+        if b_rms_weight is not None:
+            B = _rms_last(B, b_rms_weight.to(rdt), b_c_dt_rms_eps)
         B = B.reshape(xz.shape[0], L, d_state).transpose(1, 2).contiguous()
     if C is None:
         C = x_dbl[:, -d_state:]
         if C_proj_bias is not None:
             C = C + C_proj_bias.to(rdt)
+        if c_rms_weight is not None:
+            C = _rms_last(C, c_rms_weight.to(rdt), b_c_dt_rms_eps)
         C = C.reshape(xz.shape[0], L, d_state).transpose(1, 2).contiguous()
     y = selective_scan_ref(x.to(rdt), delta, A, B, C, D, z=z.to(rdt), delta_bias=delta_bias,
                            delta_softplus=delta_softplus, compute_dtype=compute_dtype)

@@ -389,6 +389,17 @@ def test_mamba_inner_ref_layout_independent():
     y = R.selective_scan_ref(xc, delta, A, Bm, Cm, Dv, z, dbias, None, True, compute_dtype=D64)
     ref = torch.einsum("bdl,md->blm", y, opw) + opb
     assert torch.allclose(out, ref, rtol=1e-12, atol=1e-12)
+    # the B / C / dt RMSNorm options against the library routine (F.rms_norm)
+    bw, cw2 = torch.rand(n, generator=g, dtype=D64) + 0.5, torch.rand(n, generator=g, dtype=D64) + 0.5
+    dw = torch.rand(d, generator=g, dtype=D64) + 0.5
+    out = R.mamba_inner_ref(xz, cw, cb, xpw, dpw, opw, opb, A, None, None, Dv, dbias, b_rms_weight=bw,
+                            c_rms_weight=cw2, dt_rms_weight=dw, b_c_dt_rms_eps=1e-5, compute_dtype=D64)
+    delta_n = F.rms_norm(delta.permute(0, 2, 1), (d,), dw, 1e-5).permute(0, 2, 1)
+    Bn = F.rms_norm(xdbl[..., r:r + n], (n,), bw, 1e-5).permute(0, 2, 1)
+    Cn = F.rms_norm(xdbl[..., r + n:], (n,), cw2, 1e-5).permute(0, 2, 1)
+    y = R.selective_scan_ref(xc, delta_n, A, Bn, Cn, Dv, z, dbias, None, True, compute_dtype=D64)
+    ref = torch.einsum("bdl,md->blm", y, opw) + opb
+    assert torch.allclose(out, ref, rtol=1e-12, atol=1e-12)
 
 
 # ---------------------------------------------------------------- fused residual-add LayerNorm / RMSNorm
