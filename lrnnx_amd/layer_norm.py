@@ -14,13 +14,16 @@ recomputes xhat from residual_out.
 
 Not supported (each raises NotImplementedError; lrnnx never passes them):
 dropout_p > 0, rowscale, the parallel second norm (x1 / weight1 / bias1) and
-``recompute_output``.  ``LayerNormLinearFn`` (layer_norm.py:1120-1260) has no
-caller in lrnnx and is not provided.
+``recompute_output``.  ``LayerNormLinearFn`` / ``layer_norm_linear_fn``
+(layer_norm.py:1097-1260; no caller in lrnnx) are the norm followed by a
+linear layer, computed as that composition and differentiated by autograd (the
+reference recomputes y in its backward instead of keeping it).
 """
 
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 
@@ -269,3 +272,28 @@ class RMSNorm(torch.nn.Module):
         return rms_norm_fn(x, self.weight, self.bias, residual=residual, eps=self.eps,
                            dropout_p=self.drop.p if self.drop is not None and self.training else 0.0,
                            prenorm=prenorm, residual_in_fp32=residual_in_fp32)
+
+
+def _layer_norm_linear(x, norm_weight, norm_bias, linear_weight, linear_bias, residual=None, eps=1e-6,
+                       prenorm=False, residual_in_fp32=False, is_rms_norm=False):
+    y, residual_out = LayerNormFn.apply(x, norm_weight, norm_bias, residual, None, None, None, eps, 0.0, None, True,
+                                        residual_in_fp32, is_rms_norm, False)
+    # the linear layer runs in the autocast dtype when autocast is on (layer_norm.py:1135-1150)
+    dtype = torch.get_autocast_gpu_dtype() if torch.is_autocast_enabled() else y.dtype
+    out = F.linear(y.to(dtype), linear_weight.to(dtype), linear_bias.to(dtype) if linear_bias is not None else None)
+    return out if not prenorm else (out, residual_out)
+
+
+class LayerNormLinearFn:
+    """Reference ``LayerNormLinearFn`` (layer_norm.py:1097-1217): ``apply`` with the
+    same arguments returns linear(norm(x + residual)) (and residual_out when
+    prenorm)."""
+
+    apply = staticmethod(_layer_norm_linear)
+
+
+def layer_norm_linear_fn(x, norm_weight, norm_bias, linear_weight, linear_bias, residual=None, eps=1e-6,
+                         prenorm=False, residual_in_fp32=False, is_rms_norm=False):
+    """Reference ``layer_norm_linear_fn`` (layer_norm.py:1220-1245)."""
+    return _layer_norm_linear(x, norm_weight, norm_bias, linear_weight, linear_bias, residual, eps, prenorm,
+                              residual_in_fp32, is_rms_norm)

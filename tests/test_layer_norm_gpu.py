@@ -17,6 +17,7 @@ an empty input.
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 from lrnnx_amd import RMSNorm, layer_norm_fn, rms_norm_fn
 from lrnnx_amd.layer_norm import _layer_norm_bwd, _layer_norm_fwd
@@ -191,3 +192,30 @@ def test_empty_rows(dev):
     dx, dw, db, _, _, _, _ = _layer_norm_bwd(torch.empty(0, 64, device=dev), xs, w, None, 1e-5, mean, rstd)
     torch.cuda.synchronize()
     assert dx.shape == (0, 64) and torch.equal(dw.cpu(), torch.zeros(64))
+
+
+@pytest.mark.parametrize("prenorm", [False, True])
+def test_layer_norm_linear_fn(dev, prenorm):
+    """linear(norm(x + residual)) against the library routines in fp64."""
+    from lrnnx_amd import layer_norm_linear_fn
+
+    g = torch.Generator().manual_seed(27)
+    x = torch.randn(2, 9, 128, generator=g)
+    res = torch.randn(2, 9, 128, generator=g)
+    w, b = 1 + 0.1 * torch.randn(128, generator=g), 0.1 * torch.randn(128, generator=g)
+    lw, lb = torch.randn(64, 128, generator=g) / 11, torch.randn(64, generator=g)
+    dy = torch.randn(2, 9, 64, generator=g)
+    ref_l = [t.double().requires_grad_() for t in (x, res, w, b, lw, lb)]
+    s = ref_l[0] + ref_l[1]
+    ref = F.linear(F.layer_norm(s, (128,), ref_l[2], ref_l[3], 1e-5), ref_l[4], ref_l[5])
+    ref.backward(dy.double())
+    dv = [t.to(dev).requires_grad_() for t in (x, res, w, b, lw, lb)]
+    out = layer_norm_linear_fn(dv[0], dv[2], dv[3], dv[4], dv[5], residual=dv[1], eps=1e-5, prenorm=prenorm)
+    if prenorm:
+        out, ro = out
+        assert torch.allclose(ro.detach().cpu(), (x + res))
+    out.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    close("out", out, ref.detach(), 1e-4, 1e-5)
+    for name, got, r in zip(("dx", "dres", "dw", "db", "dlw", "dlb"), dv, ref_l):
+        close(name, got.grad, r.grad, 1e-4, 1e-4)
