@@ -371,7 +371,7 @@ static SimpParams simp_params(const lrnnx_simplified_scan_args& a) {
 }
 
 bool simpf_fwd(const lrnnx_simplified_scan_args& a, hipStream_t st, hipError_t* err);
-bool simpf_bwd(const lrnnx_simplified_scan_args& a, float* part, hipStream_t st, hipError_t* err);
+bool simpf_bwd(const lrnnx_simplified_scan_args& a, float* part, float* ckpt_ws, hipStream_t st, hipError_t* err);
 bool fast_paths_enabled();
 
 hipError_t simp_fwd_launch(const lrnnx_simplified_scan_args& a, hipStream_t st) {
@@ -419,7 +419,7 @@ hipError_t simp_bwd_launch(const lrnnx_simplified_scan_args& a, hipStream_t st) 
   simp_ws(a, true, a.ckpt == nullptr, agg, carry, ck, part, total);
   float* ws = static_cast<float*>(a.workspace);
   hipError_t e = hipSuccess;
-  if (fast_paths_enabled() && simpf_bwd(a, ws + part, st, &e)) return e;
+  if (fast_paths_enabled() && simpf_bwd(a, ws + part, a.ckpt ? nullptr : ws + ck, st, &e)) return e;
   P.agg = ws + agg;
   P.carry = ws + carry;
   P.ckpt = a.ckpt ? static_cast<float*>(a.ckpt) : ws + ck;

@@ -190,3 +190,53 @@ def test_simplified_fast_matches_generic(dev, method, monkeypatch):
         res.append([y.detach(), last.detach()] + [t.grad for t in dl])
     for n, a, b in zip(("y", "last", "du", "ddelta", "dA", "dB", "dC"), res[0], res[1]):
         close(n, a, b.cpu().to(torch.complex128 if b.is_complex() else torch.float64), 1e-5, 1e-5)
+
+
+@pytest.mark.parametrize("method", ["bilinear", "zoh", "dirac"])
+@pytest.mark.parametrize("use_deltaA", [False, True])
+def test_simplified_kernel_time_varying_delta(dev, method, use_deltaA):
+    """The binding's fwd / bwd (reference boundary, chunk carries x, no
+    checkpoints handed to the backward) with delta varying along L."""
+    d = R.make_lru_inputs(2, 4500, 8, seed=4)
+    A = torch.log(d["Lambda"]).to(torch.complex64).unsqueeze(-1)
+    g = torch.Generator().manual_seed(5)
+    Bw = torch.complex(torch.randn(8, 1, generator=g), torch.randn(8, 1, generator=g))
+    Cw = torch.complex(torch.randn(8, 1, generator=g), torch.randn(8, 1, generator=g))
+    delta = 0.2 + torch.rand(2, 8, 4500, generator=g)
+    deltaA = (0.2 + torch.rand(2, 8, 4500, generator=g)) if use_deltaA else None
+    dout = torch.complex(torch.randn(2, 8, 4500, generator=g), torch.randn(2, 8, 4500, generator=g))
+    leaves = [d["Bu"].to(torch.complex128), delta.double(), A.to(torch.complex128), Bw.to(torch.complex128),
+              Cw.to(torch.complex128)]
+    for t in leaves:
+        t.requires_grad_(True)
+    dA_leaf = deltaA.double().requires_grad_(True) if use_deltaA else None
+    ref_out, ref_x = R.simplified_scan_kernel_ref(*leaves, dA_leaf, method, compute_dtype=torch.float64)
+    ref_out.backward(dout.to(torch.complex128))
+    dv = lambda t: t.to(dev) if t is not None else None
+    out, x = simplified_scan_cuda.fwd(dv(d["Bu"]), dv(delta), dv(A), dv(Bw), dv(Cw), dv(deltaA), method)
+    grads = simplified_scan_cuda.bwd(dv(d["Bu"]), dv(delta), dv(A), dv(Bw), dv(Cw), dv(deltaA), dv(dout), x, method)
+    torch.cuda.synchronize()
+    close("out", out, ref_out.detach(), 1e-4, 1e-5)
+    close("x", x, ref_x.detach(), 1e-4, 1e-5)
+    for name, got, ref in zip(("du", "ddelta", "dA", "dB", "dC"), grads, leaves):
+        close(name, got, ref.grad, 1e-4, 1e-5 if name == "du" else 1e-4)
+    if use_deltaA:
+        close("ddeltaA", grads[5], dA_leaf.grad, 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("method", ["bilinear", "zoh", "dirac"])
+@pytest.mark.parametrize("use_deltaA", [False, True])
+def test_simplified_fast_matches_generic_time_varying(dev, method, use_deltaA, monkeypatch):
+    A, Bm, Cm, u, delta, deltaA, D, dout = _inputs(2, 8, 16, 1300, seed=22)
+    res = []
+    for generic in ("0", "1"):
+        monkeypatch.setenv("LRNNX_SCAN_GENERIC", generic)
+        dl = [t.to(dev).requires_grad_(True) for t in (u, delta, A, Bm, Cm)]
+        dA_dev = deltaA.to(dev).requires_grad_(True) if use_deltaA else None
+        y, last = simplified_scan_fn(*dl, deltaA=dA_dev, return_last_state=True, discretization=method)
+        y.backward(dout.to(dev))
+        torch.cuda.synchronize()
+        res.append([y.detach(), last.detach()] + [t.grad for t in dl] + ([dA_dev.grad] if use_deltaA else []))
+    names = ("y", "last", "du", "ddelta", "dA", "dB", "dC", "ddeltaA")
+    for n, a, b in zip(names, res[0], res[1]):
+        close(n, a, b.cpu().to(torch.complex128 if b.is_complex() else torch.float64), 1e-4, 1e-5)
