@@ -74,6 +74,12 @@ __device__ __forceinline__ void store_vec(T* __restrict__ p, int n, const float*
 // ---------------------------------------------------------------- math
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// An empty asm that takes and returns v in a VGPR: the computation of v
+// cannot move past this point.  Used to keep an accumulation chain at its
+// step when only its final value is read later: machine sinking would
+// otherwise move the chain to that read and keep every step's operands live.
+__device__ __forceinline__ void pin_vgpr(float& v) { asm volatile("" : "+v"(v)); }
+
 // softplus with the reference's threshold: identity above 20
 // (selective_scan.cuh:172-174; F.softplus default threshold).
 __device__ __forceinline__ float softplus20(float x) { return x <= 20.f ? log1pf(expf(x)) : x; }

@@ -112,6 +112,9 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   constexpr int kNV = kS * kCk;         // dB/dC values per lane per sub-chunk (<= 64)
   constexpr int kV = kCk < 4 ? kCk : 4; // steps per LDS vector access
   constexpr bool kP3 = needs_p3<kMethod>();
+  // A_bar of the interval kept in VGPRs (s7's is one value per step; mamba
+  // and dirac keep it up to kS = 4 and re-derive it, one exp, above)
+  constexpr bool kAbLive = kMethod == LRNNX_S7 || (!kP3 && kS <= 4);
   constexpr int kNWmax = fwd_nw_max(kS);
   constexpr int kNPmax = kNWmax * kS;
   constexpr int kRawArr = kWave * kTB * (int)sizeof(IT);
@@ -184,7 +187,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   // checkpoint rows: state n of interval kk at ckp[((b * n_ck + kk) * N + n) * D + d]
   const float* gck = ckp + b * n_ck * N * D + d0;
 
-  float a2[kS], Araw[kS], bcst[kS], ccst[kS], cout_c[kS];
+  float a2[kS], Araw[kS], invA[kS], bcst[kS], ccst[kS], cout_c[kS];
   // dh: gradient of the state at the current step; gn: A_bar_{t+1} dh_{t+1}
   float dh[kS], gn[kS], dA_acc[kS], dBc_acc[kS], dCc_acc[kS];
   {
@@ -197,6 +200,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
       const bool ok = lane_ok && n < N;
       const float Av = ok ? Ap[d * a.A.s0 + n * a.A.s1] : (kMethod == LRNNX_RGLRU ? 0.5f : -1.f);
       Araw[k] = Av;
+      invA[k] = 1.f / Av;
       a2[k] = prep_a2<kMethod>(Av);
       bcst[k] = (!kVarB && ok) ? Bp[d * a.B.s0 + n * a.B.s1] : 1.f;
       ccst[k] = (!kVarC && ok) ? Cp[d * a.C.s0 + n * a.C.s1] : 1.f;
@@ -427,8 +431,11 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
         h0[k] = (kk > 0 && lane_ok && n0 + k < N) ? ckp[((b * n_ck + kk - 1) * N + n0 + k) * D + d] : 0.f;
       }
     }
-    // recompute A_bar and h over the interval
-    float Ab[kCk][kS], H[kCk][kS];
+    // recompute h (and, where kAbLive, A_bar) over the interval.  Otherwise
+    // the reverse walk re-derives A_bar (zoh, bilinear and rglru recompute
+    // the same discretisation there for their input-term gradients anyway);
+    // keeping it live as well would take kS * kCk more VGPRs and spill.
+    float Ab[kAbLive ? kCk : 1][kS], H[kCk][kS];
     {
       float hc[kS];
 #pragma unroll
@@ -453,14 +460,14 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
 #pragma unroll
             for (int k = 0; k < kS; ++k) {
               float beta;
-              const float ab = disc_real<kMethod>(dt, dlv[i], a2[k], Araw[k], beta);
+              const float ab = disc_real<kMethod, kDA>(dt, dlv[i], a2[k], Araw[k], invA[k], beta);
               const float bin = kVarB ? bv[k] : 1.f;
               float inc;
               if constexpr (kMethod == LRNNX_MAMBA) inc = du_ * bin;
               else if constexpr (uses_B_input<kMethod>()) inc = beta * uvv[i] * bin;
               else inc = beta * uvv[i];
               hc[k] = fmaf(ab, hc[k], inc);
-              Ab[j][k] = ab;
+              if constexpr (kAbLive) Ab[j][k] = ab;
               H[j][k] = hc[k];
             }
           }
@@ -504,29 +511,34 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
             }
             const float bin = kVarB ? bv[k] : 1.f;
             dh[k] = fmaf(dy, cc, gn[k]);
-            const float ab = Ab[j][k];
+            float beta_r = 0.f;  // input factor of this step (methods that re-derive A_bar)
+            float ab;
+            if constexpr (kAbLive) ab = Ab[j][k];
+            else ab = disc_real<kMethod, kDA>(dt, dl, a2[k], Araw[k], invA[k], beta_r);
             const float hp = j > 0 ? H[j - 1][k] : h0[k];
             const float hcur = H[j][k];
             const float gk = ab * dh[k];  // carried to step t-1
             gn[k] = gk;
+            float rA = 0.f;  // bilinear: 1 / (1 - dtA A / 2)
             // through A_bar: dh * hp * dA_bar/d(.)
             if constexpr (kMethod == LRNNX_MAMBA || kMethod == LRNNX_DIRAC || kMethod == LRNNX_ZOH) {
               const float wv = gk * hp;
               p2 = fmaf(wv, Araw[k], p2);
               dA_acc[k] = fmaf(wv, dt, dA_acc[k]);
             } else if constexpr (kMethod == LRNNX_BILINEAR) {
-              const float vA = 0.5f * dt * Araw[k];
-              const float qv = dh[k] * hp / ((1.f - vA) * (1.f - vA));
+              // dA_bar/d(dtA A) = 1 / (1 - dtA A / 2)^2
+              rA = __builtin_amdgcn_rcpf(1.f - 0.5f * dt * Araw[k]);
+              const float qv = dh[k] * hp * (rA * rA);
               p2 = fmaf(qv, Araw[k], p2);
               dA_acc[k] = fmaf(qv, dt, dA_acc[k]);
             } else if constexpr (kMethod == LRNNX_S7) {
-              const float den = dl * dl + 0.5f;
-              p2 = fmaf(dh[k] * hp, 2.f * dl / (den * den), p2);
+              const float r = __builtin_amdgcn_rcpf(fmaf(dl, dl, 0.5f));
+              p2 = fmaf(dh[k] * hp, 2.f * dl * (r * r), p2);
             } else {  // RGLRU: dA_bar/ddelta = A_bar ln A, dA_bar/dA = delta A_bar / A
               const float wv = gk * hp;
               const float lnA = a2[k] * kLn2;
               p2 = fmaf(wv, lnA, p2);
-              dA_acc[k] = fmaf(wv, dl / Araw[k], dA_acc[k]);
+              dA_acc[k] = fmaf(wv, dl * invA[k], dA_acc[k]);
             }
             // through the input term
             if constexpr (kMethod == LRNNX_MAMBA) {
@@ -536,16 +548,17 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
               p1 = fmaf(dh[k], bin, p1);
               if constexpr (kVarB) vB[k] = dh[k] * uu;
             } else if constexpr (kMethod == LRNNX_ZOH) {
-              const float e1 = expf(dl * Araw[k]);
-              const float beta = expm1f(dl * Araw[k]) / Araw[k];
+              // beta = expm1(delta' A) / A; without deltaA, exp(delta' A) is A_bar
+              const float e1 = kDA ? fast_exp2(dl * a2[k]) : ab;
+              const float beta = beta_r;
               const float g = dh[k] * bin;
               p1 = fmaf(g, beta, p1);
               p3 = fmaf(g * uu, e1, p3);
-              dA_acc[k] = fmaf(g * uu, (dl * e1 - beta) / Araw[k], dA_acc[k]);
+              dA_acc[k] = fmaf(g * uu, (dl * e1 - beta) * invA[k], dA_acc[k]);
               if constexpr (kVarB) vB[k] = dh[k] * beta * uu;
             } else if constexpr (kMethod == LRNNX_BILINEAR) {
-              const float vB_ = 0.5f * dl * Araw[k];
-              const float inv = 1.f / (1.f - vB_);
+              // beta = delta' / (1 - delta' A / 2); without deltaA the same reciprocal as A_bar's
+              const float inv = kDA ? __builtin_amdgcn_rcpf(1.f - 0.5f * dl * Araw[k]) : rA;
               const float beta = dl * inv;
               const float g = dh[k] * bin;
               p1 = fmaf(g, beta, p1);
@@ -553,13 +566,13 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
               dA_acc[k] = fmaf(g * uu, 0.5f * dl * dl * inv * inv, dA_acc[k]);
               if constexpr (kVarB) vB[k] = dh[k] * beta * uu;
             } else {  // RGLRU: beta = sqrt(1 - ab^2), B unused on the input side
-              const float beta = sqrtf(-expm1f(dl * a2[k] * kLn2) * (1.f + ab));
+              const float beta = beta_r;
               const float g = dh[k];
               p1 = fmaf(g, beta, p1);
-              const float dbeta_dab = -ab / beta;
+              const float dbeta_dab = -ab * __builtin_amdgcn_rcpf(beta);
               const float lnA = a2[k] * kLn2;
               p3 = fmaf(g * uu * dbeta_dab, ab * lnA, p3);
-              dA_acc[k] = fmaf(g * uu * dbeta_dab, ab * dl / Araw[k], dA_acc[k]);
+              dA_acc[k] = fmaf(g * uu * dbeta_dab, ab * dl * invA[k], dA_acc[k]);
               if constexpr (kVarB) vB[k] = 0.f;
             }
             // output side: y = sum_n cout h  (cout = C * B_const)
@@ -592,6 +605,15 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
           } else {
             accB[j] = 0.f; accC[j] = 0.f;
           }
+        }
+        // keep the per-lane accumulations at their step: only their final
+        // values are read after the walk, and sinking the chains there keeps
+        // every step's operands live across the walk (spills past 256 VGPRs)
+#pragma unroll
+        for (int k = 0; k < kS; ++k) {
+          pin_vgpr(dA_acc[k]);
+          if constexpr (!kVarB) pin_vgpr(dBc_acc[k]);
+          if constexpr (!kVarC) pin_vgpr(dCc_acc[k]);
         }
       }
       const int op = ((w * kG + (t >> 2)) * kWave + lane) * 4 + (t & 3);

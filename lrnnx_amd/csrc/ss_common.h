@@ -37,14 +37,29 @@ inline int pick_kS(int64_t N) {
   return 32;
 }
 
+__host__ __device__ constexpr bool exp_family_m(int m) {
+  return m == LRNNX_MAMBA || m == LRNNX_DIRAC || m == LRNNX_ZOH;
+}
+
+// expm1(x) given e = exp(x): a degree-5 Taylor polynomial where |x| < 1/16
+// (truncation error < 2e-9 relative), e - 1 elsewhere (cancellation costs at
+// most ~2e-6 relative at |x| = 1/16, where |e - 1| > 0.06).
+__device__ __forceinline__ float expm1_from(float x, float e) {
+  const float p = x * fmaf(x, fmaf(x, fmaf(x, fmaf(x, 1.f / 120.f, 1.f / 24.f), 1.f / 6.f), 0.5f), 1.f);
+  return fabsf(x) < 0.0625f ? p : e - 1.f;
+}
+
 // Per-(t, n) discretisation of a real state.  `dtA` is the step used for
-// A_bar (deltaA or delta'), `dl` the post-bias/softplus delta', `a2` the
-// per-(d, n) prepared eigenvalue:
-//   exp-based methods: A * log2(e);  bilinear, zoh: A;  rglru: log2(A);  s7: unused.
-// Returns A_bar; writes the input factor beta so that the increment is
-// beta * B_in * u (selective_scan.cuh:272-302).
-template <int kMethod>
-__device__ __forceinline__ float disc_real(float dtA, float dl, float a2, float Araw, float& beta) {
+// A_bar (deltaA when kDA, else equal to `dl`), `dl` the post-bias/softplus
+// delta', `a2` the per-(d, n) prepared eigenvalue:
+//   exp-based methods (mamba, dirac, zoh): A * log2(e);  bilinear: A;
+//   rglru: log2(A);  s7: unused.
+// `invA` is 1 / A (used by zoh).  Returns A_bar; writes the input factor beta
+// so that the increment is beta * B_in * u (selective_scan.cuh:272-302).
+// The exponentials are v_exp_f32 on a base-2 argument and the quotients
+// v_rcp_f32 products (1 ulp each), well inside the fp32 parity tolerance.
+template <int kMethod, bool kDA>
+__device__ __forceinline__ float disc_real(float dtA, float dl, float a2, float Araw, float invA, float& beta) {
   if constexpr (kMethod == LRNNX_MAMBA) {
     beta = dl;
     return fast_exp2(dtA * a2);
@@ -52,26 +67,28 @@ __device__ __forceinline__ float disc_real(float dtA, float dl, float a2, float 
     beta = 1.f;
     return fast_exp2(dtA * a2);
   } else if constexpr (kMethod == LRNNX_ZOH) {
-    beta = expm1f(dl * Araw) / Araw;
-    return expf(dtA * Araw);
+    const float ab = fast_exp2(dtA * a2);
+    const float eb = kDA ? fast_exp2(dl * a2) : ab;  // exp(delta' A)
+    beta = expm1_from(dl * Araw, eb) * invA;
+    return ab;
   } else if constexpr (kMethod == LRNNX_BILINEAR) {
     const float vA = 0.5f * dtA * Araw;
-    const float vB = 0.5f * dl * Araw;
-    beta = dl / (1.f - vB);
-    return (1.f + vA) / (1.f - vA);
+    const float rA = __builtin_amdgcn_rcpf(1.f - vA);
+    beta = dl * (kDA ? __builtin_amdgcn_rcpf(1.f - 0.5f * dl * Araw) : rA);
+    return (1.f + vA) * rA;
   } else if constexpr (kMethod == LRNNX_S7) {
     beta = 1.f;
-    return 1.f - 1.f / (dl * dl + 0.5f);
+    return 1.f - __builtin_amdgcn_rcpf(fmaf(dl, dl, 0.5f));
   } else {  // RGLRU: A_bar = A^delta, beta = sqrt(1 - A_bar^2)
     const float ab = fast_exp2(dl * a2);
-    beta = sqrtf(-expm1f(dl * a2 * kLn2) * (1.f + ab));  // 1 - ab^2 without cancellation
+    beta = __builtin_amdgcn_sqrtf(-expm1_from(dl * a2 * kLn2, ab) * (1.f + ab));  // 1 - ab^2 without cancellation
     return ab;
   }
 }
 
 template <int kMethod>
 __device__ __forceinline__ float prep_a2(float A) {
-  if constexpr (kMethod == LRNNX_MAMBA || kMethod == LRNNX_DIRAC) return A * kLog2e;
+  if constexpr (exp_family_m(kMethod)) return A * kLog2e;
   else if constexpr (kMethod == LRNNX_RGLRU) return __log2f(A);
   else return A;
 }
@@ -80,7 +97,7 @@ __device__ __forceinline__ float prep_a2(float A) {
 // A_bar over a chunk is exp(A * sum dtA) and needs no per-step multiply).
 template <int kMethod>
 __host__ __device__ constexpr bool exp_family() {
-  return kMethod == LRNNX_MAMBA || kMethod == LRNNX_DIRAC || kMethod == LRNNX_ZOH;
+  return exp_family_m(kMethod);
 }
 
 // Whether B (variable or constant) multiplies the input term

@@ -103,7 +103,7 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   const uint32_t so = (uint32_t)a.out.s1, soz = (uint32_t)a.out_z.s1;
 
   // per-lane constants
-  float a2[kS], Araw[kS], cout_c[kS], h[kS], prodA[kS];
+  float a2[kS], Araw[kS], invA[kS], cout_c[kS], h[kS], prodA[kS];
   {
     const float* Ap = static_cast<const float*>(a.A.ptr);
     const float* Bp = static_cast<const float*>(a.B.ptr);
@@ -114,6 +114,7 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
       const bool ok = lane_ok && n < N;
       const float Av = ok ? Ap[d * a.A.s0 + n * a.A.s1] : (kMethod == LRNNX_RGLRU ? 0.5f : -1.f);
       Araw[k] = Av;
+      invA[k] = 1.f / Av;
       a2[k] = prep_a2<kMethod>(Av);
       const float bc = (!kVarB && ok) ? Bp[d * a.B.s0 + n * a.B.s1] : 1.f;
       const float cc = (!kVarC && ok) ? Cp[d * a.C.s0 + n * a.C.s1] : 1.f;
@@ -272,7 +273,7 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
 #pragma unroll
     for (int k = 0; k < kS; ++k) {
       float beta;
-      const float ab = disc_real<kMethod>(dt, dl, a2[k], Araw[k], beta);
+      const float ab = disc_real<kMethod, kDA>(dt, dl, a2[k], Araw[k], invA[k], beta);
       float inc;
       if constexpr (kMethod == LRNNX_MAMBA) inc = xx * bin[k];           // xx = delta' u
       else if constexpr (uses_B_input<kMethod>()) inc = beta * xx * bin[k];
@@ -298,7 +299,7 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
       if (lane_ok && n0 + k < N) {
         float ac;
         if constexpr (exp_family<kMethod>())
-          ac = (kMethod == LRNNX_ZOH) ? expf(Araw[k] * sumdt) : fast_exp2(a2[k] * sumdt);
+          ac = fast_exp2(a2[k] * sumdt);
         else
           ac = prodA[k];
         float* xr = xp + ((b * D + d) * n_xc + c) * 2 * N;
