@@ -110,6 +110,47 @@ def test_rglru_fp32(dev):
          softplus=False, A_override=A)
 
 
+@pytest.mark.parametrize("L,has_D", [(7, False), (513, True), (2100, False), (4100, True)])
+def test_rglru_fast_path_lengths(dev, L, has_D):
+    # one state per channel takes the lanes-along-L kernels: lengths inside one
+    # lane, across the 512-step chunk, and across the 2048-step carries (last_state)
+    A = torch.rand(64, 1, generator=torch.Generator().manual_seed(L)) * 0.5 + 0.45
+    _run(dev, 2, 64, L, 1, method="rglru", varB=False, varC=False, has_z=False, has_D=has_D, has_bias=False,
+         softplus=False, A_override=A, seed=L)
+
+
+def _rglru_leaves(dev, L, seed):
+    inp = R.make_selective_inputs(2, 48, L, 1, seed=seed, varB=False, varC=False, has_z=False, has_D=True,
+                                  has_bias=False)
+    inp["A"] = torch.rand(48, 1, generator=torch.Generator().manual_seed(seed)) * 0.5 + 0.45
+    inp["delta"] = inp["delta"].float().abs() * 0.2 + 1e-3
+    d = to_dev(inp, dev)
+    return {k: d[k].clone().requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D")}
+
+
+@pytest.mark.parametrize("fwd_generic,bwd_generic", [("0", "1"), ("1", "0"), ("1", "1")])
+def test_rglru_fast_path_matches_generic(dev, monkeypatch, fwd_generic, bwd_generic):
+    """The rglru fast kernels write and read the general path's checkpoint
+    layout: a forward on one path followed by a backward on the other gives
+    the results of the fast path on both."""
+    L = 1100
+    dout = torch.randn(2, 48, L, generator=torch.Generator().manual_seed(3)).to(dev)
+    res = []
+    for fg, bg in (("0", "0"), (fwd_generic, bwd_generic)):
+        lv = _rglru_leaves(dev, L, 11)
+        monkeypatch.setenv("LRNNX_SCAN_GENERIC", fg)
+        out, last = selective_scan_fn(lv["u"], lv["delta"], lv["A"], lv["B"], lv["C"], lv["D"], None, None, None,
+                                      False, True, "rglru")
+        monkeypatch.setenv("LRNNX_SCAN_GENERIC", bg)
+        out.backward(dout)
+        torch.cuda.synchronize()
+        res.append([out.detach(), last.detach()] + [lv[k].grad for k in lv])
+    names = ["out", "last_state"] + ["d" + k for k in ("u", "delta", "A", "B", "C", "D")]
+    for n, a, b in zip(names, res[0], res[1]):
+        # same fp32 math; the scan across lanes and the sums run in another order
+        close(n, a, b.cpu().double(), 1e-4, 1e-4 if n in ("dA", "dB", "dC", "dD") else 1e-5)
+
+
 @pytest.mark.parametrize("itype", [torch.bfloat16, torch.float16])
 def test_mamba_low_precision(dev, itype):
     _run(dev, 2, 64, 128, 16, itype=itype)
