@@ -1,12 +1,16 @@
-// RG-LRU scan, fast path for one state per channel (A of shape (D, 1), the
-// RG-LRU layer's `a`): the selective scan's "rglru" discretisation
-// (reference csrc/selective_scan/selective_scan.cuh:296-302, backward
+// RG-LRU and S7 scans, fast path for one state per channel: the selective
+// scan's "rglru" and "s7" discretisations (reference
+// csrc/selective_scan/selective_scan.cuh:272-302, backward
 // selective_scan_backward.cuh) with constant B / C, fp32,
-//   A_bar_t = A^delta_t,  beta_t = sqrt(1 - A_bar_t^2),
-//   h_t = A_bar_t h_{t-1} + beta_t u_t,  out_t = B C h_t + D u_t.
+//   h_t = A_bar_t h_{t-1} + beta_t u_t,  out_t = B C h_t + D u_t,
+//   rglru: A_bar_t = A^delta_t, beta_t = sqrt(1 - A_bar_t^2)  (A of shape
+//          (D, 1): the RG-LRU layer's `a`, rglru_scan.py:39);
+//   s7:    A_bar_t = 1 - 1 / (delta_t^2 + 1/2), beta_t = 1  (S7ScanFn runs one
+//          state per S7 state index with the time-varying A as delta,
+//          s7_scan.py:49-74).
 //
 // With one state per channel the general kernels hold one wave per 64
-// channels, far fewer waves than the chip has SIMDs at the layer's shapes.
+// channels, far fewer waves than the chip has SIMDs at the layers' shapes.
 // Here one wave owns one (b, d) sequence and walks it in chunks of 512 steps,
 // 8 consecutive steps per lane (coalesced 16-byte accesses):
 //   forward   a serial pass over the lane's steps from zero (local state s_j
@@ -63,25 +67,35 @@ __device__ __forceinline__ void st8(float* q, int n, const float* v) {
   }
 }
 
-// A_bar and beta of one step; la = log2(A).  The same operations as the
-// general kernels' rglru discretisation.
+// A_bar and beta of one step; la = log2(A) (rglru).  The same operations as
+// the general kernels' discretisation (disc_real).
+template <int kMethod>
 __device__ __forceinline__ void rg_disc(float dl, float la, float& ab, float& beta) {
-  const float x = dl * la;
-  ab = fast_exp2(x);
-  beta = __builtin_amdgcn_sqrtf(-expm1_from(x * kLn2, ab) * (1.f + ab));  // 1 - ab^2 without cancellation
+  if constexpr (kMethod == LRNNX_S7) {
+    ab = 1.f - __builtin_amdgcn_rcpf(fmaf(dl, dl, 0.5f));
+    beta = 1.f;
+  } else {
+    const float x = dl * la;
+    ab = fast_exp2(x);
+    beta = __builtin_amdgcn_sqrtf(-expm1_from(x * kLn2, ab) * (1.f + ab));  // 1 - ab^2 without cancellation
+  }
 }
 
 // Local pass over the lane's steps and the cross-lane scan: returns the
 // state before the lane's first step given `hin`, the state before the chunk;
 // P[j] = prod of A_bar over the lane's steps 0..j, s[j] the state from zero.
 // Also returns the chunk's total A_bar product (lane 63's inclusive value).
+// Steps past L load delta 0 and u 0: for rglru they are the identity
+// (A_bar 1, beta 0); for s7 A_bar is -1 there, which only reaches states and
+// lanes past L (never stored) and the carry out of the last chunk (unused).
+template <int kMethod>
 __device__ __forceinline__ float chunk_states(const float* dl, const float* u, float la, float hin, int lane,
                                               float* ab, float* be, float* P, float* h, float& Pchunk,
                                               float& Ain) {
   float s[kE];
 #pragma unroll
   for (int j = 0; j < kE; ++j) {
-    rg_disc(dl[j], la, ab[j], be[j]);
+    rg_disc<kMethod>(dl[j], la, ab[j], be[j]);
     const float v = be[j] * u[j];
     s[j] = j == 0 ? v : fmaf(ab[j], s[j - 1], v);
     P[j] = j == 0 ? ab[j] : ab[j] * P[j - 1];
@@ -111,12 +125,13 @@ __device__ __forceinline__ float chunk_states(const float* dl, const float* u, f
 
 }  // namespace
 
+template <int kMethod>
 __global__ void __launch_bounds__(256) rgf_fwd_kernel(const lrnnx_selective_scan_args a, int64_t n_ck, int64_t n_x) {
   const int lane = threadIdx.x & 63;
   const int64_t seq = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // b * D + d
   if (seq >= a.batch * a.dim) return;
   const int64_t D = a.dim, b = seq / D, d = seq % D, L = a.seqlen;
-  const float la = __log2f(static_cast<const float*>(a.A.ptr)[d * a.A.s0]);
+  const float la = kMethod == LRNNX_S7 ? 0.f : __log2f(static_cast<const float*>(a.A.ptr)[d * a.A.s0]);
   const float bc = static_cast<const float*>(a.B.ptr)[d * a.B.s0] * static_cast<const float*>(a.C.ptr)[d * a.C.s0];
   const float Dv = a.D.ptr ? static_cast<const float*>(a.D.ptr)[d * a.D.s0] : 0.f;
   const float* u = static_cast<const float*>(a.u.ptr) + b * a.u.s0 + d * a.u.s1;
@@ -131,9 +146,8 @@ __global__ void __launch_bounds__(256) rgf_fwd_kernel(const lrnnx_selective_scan
     float uu[kE], dl[kE];
     ld8(u + tl, n, uu);
     ld8(dlr + tl, n, dl);
-    // steps past L: delta 0 gives A_bar 1 and beta 0, so they change nothing
     float ab[kE], be[kE], P[kE], h[kE], Pc, Ain;
-    chunk_states(dl, uu, la, hin, lane, ab, be, P, h, Pc, Ain);
+    chunk_states<kMethod>(dl, uu, la, hin, lane, ab, be, P, h, Pc, Ain);
     if (out && n > 0) {
       float y[kE];
 #pragma unroll
@@ -161,6 +175,7 @@ __global__ void __launch_bounds__(256) rgf_fwd_kernel(const lrnnx_selective_scan
 
 // Per-sequence partials into the general backward's workspace sections
 // (dA, constant dB / dC, dD: one value per (b, d)); du, ddelta written.
+template <int kMethod>
 __global__ void __launch_bounds__(256) rgf_bwd_kernel(const lrnnx_selective_scan_args a, int64_t n_ck,
                                                       const float* __restrict__ ckp, float* __restrict__ ws,
                                                       const SSBwdWs wo) {
@@ -168,8 +183,8 @@ __global__ void __launch_bounds__(256) rgf_bwd_kernel(const lrnnx_selective_scan
   const int64_t seq = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (seq >= a.batch * a.dim) return;
   const int64_t D = a.dim, b = seq / D, d = seq % D, L = a.seqlen;
-  const float Araw = static_cast<const float*>(a.A.ptr)[d * a.A.s0];
-  const float la = __log2f(Araw), lnA = la * kLn2, invA = 1.f / Araw;
+  const float Araw = static_cast<const float*>(a.A.ptr)[d * a.A.s0];   // unused by s7
+  const float la = kMethod == LRNNX_S7 ? 0.f : __log2f(Araw), lnA = la * kLn2, invA = 1.f / Araw;
   const float B0 = static_cast<const float*>(a.B.ptr)[d * a.B.s0];
   const float C0 = static_cast<const float*>(a.C.ptr)[d * a.C.s0];
   const float w = B0 * C0;
@@ -192,7 +207,7 @@ __global__ void __launch_bounds__(256) rgf_bwd_kernel(const lrnnx_selective_scan
     // forward recompute from the state before the chunk (t0 is a multiple of 16)
     const float hin = t0 > 0 ? ckp[(b * n_ck + t0 / kCk1 - 1) * D + d] : 0.f;
     float ab[kE], be[kE], P[kE], h[kE], Pc, Ain;
-    const float cin = chunk_states(dl, x, la, hin, lane, ab, be, P, h, Pc, Ain);
+    const float cin = chunk_states<kMethod>(dl, x, la, hin, lane, ab, be, P, h, Pc, Ain);
     // adjoint: e_j = A_bar_j (w dout_j + e_{j+1}), the gradient carried from
     // step j to j - 1; local values from e = 0 past the lane, Q_j = prod_{i >= j} A_bar_i
     float el[kE], Q[kE];
@@ -226,11 +241,17 @@ __global__ void __launch_bounds__(256) rgf_bwd_kernel(const lrnnx_selective_scan
       const float g = fmaf(w, dy[j], enext);  // dL/dh_j
       dx[j] = fmaf(be[j], g, Dv * dy[j]);
       const float hp = j > 0 ? h[j - 1] : cin;
-      // dL/dA_bar_j through h_j = A_bar h_{j-1} + beta(A_bar) u_j, dbeta/dA_bar = -A_bar / beta;
-      // steps past L are excluded (their beta is 0)
-      const float q = j < n ? g * fmaf(-x[j] * ab[j], __builtin_amdgcn_rcpf(be[j]), hp) : 0.f;
-      ddv[j] = q * ab[j] * lnA;                          // dA_bar/ddelta = A_bar ln A
-      dAacc = fmaf(q, ab[j] * dl[j] * invA, dAacc);     // dA_bar/dA = delta A_bar / A
+      if constexpr (kMethod == LRNNX_S7) {
+        // dA_bar/ddelta = 2 delta / (delta^2 + 1/2)^2; A does not enter (dA = 0)
+        const float r = __builtin_amdgcn_rcpf(fmaf(dl[j], dl[j], 0.5f));
+        ddv[j] = g * hp * (2.f * dl[j] * (r * r));
+      } else {
+        // dL/dA_bar_j through h_j = A_bar h_{j-1} + beta(A_bar) u_j, dbeta/dA_bar = -A_bar / beta;
+        // steps past L are excluded (their beta is 0)
+        const float q = j < n ? g * fmaf(-x[j] * ab[j], __builtin_amdgcn_rcpf(be[j]), hp) : 0.f;
+        ddv[j] = q * ab[j] * lnA;                          // dA_bar/ddelta = A_bar ln A
+        dAacc = fmaf(q, ab[j] * dl[j] * invA, dAacc);     // dA_bar/dA = delta A_bar / A
+      }
       SHd = fmaf(h[j], dy[j], SHd);
       SDu = fmaf(x[j], dy[j], SDu);
     }
@@ -251,10 +272,11 @@ __global__ void __launch_bounds__(256) rgf_bwd_kernel(const lrnnx_selective_scan
   }
 }
 
-// The fast path covers rglru with one state, constant B / C, and no z, delta
-// bias, softplus or deltaA (RGLRUScanFn's call, rglru_scan.py:39).
+// The fast path covers rglru and s7 with one state, constant B / C, and no z,
+// delta bias, softplus or deltaA (RGLRUScanFn's and S7ScanFn's calls,
+// rglru_scan.py:39, s7_scan.py:59).
 bool rgf_ok(const lrnnx_selective_scan_args& a) {
-  return a.method == LRNNX_RGLRU && a.wtype == LRNNX_F32 && a.itype == LRNNX_F32 && a.dstate == 1 && !a.var_B &&
+  return (a.method == LRNNX_RGLRU || a.method == LRNNX_S7) && a.wtype == LRNNX_F32 && a.itype == LRNNX_F32 && a.dstate == 1 && !a.var_B &&
          !a.var_C && a.z.ptr == nullptr && a.delta_bias.ptr == nullptr && a.deltaA.ptr == nullptr &&
          !a.delta_softplus && fast_paths_enabled();
 }
@@ -263,7 +285,8 @@ hipError_t rgf_fwd(const lrnnx_selective_scan_args& a, hipStream_t st) {
   const SSGeom g = ss_geom(a);
   const int64_t n_x = (a.seqlen + kXChunk - 1) / kXChunk;
   const dim3 grid((unsigned)((a.batch * a.dim + 3) / 4));
-  hipLaunchKernelGGL(rgf_fwd_kernel, grid, dim3(256), 0, st, a, g.n_ck, n_x);
+  if (a.method == LRNNX_S7) hipLaunchKernelGGL(rgf_fwd_kernel<LRNNX_S7>, grid, dim3(256), 0, st, a, g.n_ck, n_x);
+  else hipLaunchKernelGGL(rgf_fwd_kernel<LRNNX_RGLRU>, grid, dim3(256), 0, st, a, g.n_ck, n_x);
   return hipGetLastError();
 }
 
@@ -271,7 +294,8 @@ hipError_t rgf_bwd(const lrnnx_selective_scan_args& a, float* ws, const float* c
   const SSGeom g = ss_geom(a);
   const SSBwdWs wo = ss_bwd_ws(a, g, a.ckpt == nullptr);
   const dim3 grid((unsigned)((a.batch * a.dim + 3) / 4));
-  hipLaunchKernelGGL(rgf_bwd_kernel, grid, dim3(256), 0, st, a, g.n_ck, ckp, ws, wo);
+  if (a.method == LRNNX_S7) hipLaunchKernelGGL(rgf_bwd_kernel<LRNNX_S7>, grid, dim3(256), 0, st, a, g.n_ck, ckp, ws, wo);
+  else hipLaunchKernelGGL(rgf_bwd_kernel<LRNNX_RGLRU>, grid, dim3(256), 0, st, a, g.n_ck, ckp, ws, wo);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return ss_bwd_reductions<float, false, false>(a, g, ws, wo, st);

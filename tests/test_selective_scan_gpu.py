@@ -119,6 +119,12 @@ def test_rglru_fast_path_lengths(dev, L, has_D):
          softplus=False, A_override=A, seed=L)
 
 
+@pytest.mark.parametrize("L", [513, 2100])
+def test_s7_fast_path_lengths(dev, L):
+    _run(dev, 2, 64, L, 1, method="s7", varB=False, varC=False, has_z=False, has_D=True, has_bias=False,
+         softplus=False, seed=L + 1)
+
+
 def _rglru_leaves(dev, L, seed):
     inp = R.make_selective_inputs(2, 48, L, 1, seed=seed, varB=False, varC=False, has_z=False, has_D=True,
                                   has_bias=False)
@@ -128,11 +134,12 @@ def _rglru_leaves(dev, L, seed):
     return {k: d[k].clone().requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D")}
 
 
+@pytest.mark.parametrize("method", ["rglru", "s7"])
 @pytest.mark.parametrize("fwd_generic,bwd_generic", [("0", "1"), ("1", "0"), ("1", "1")])
-def test_rglru_fast_path_matches_generic(dev, monkeypatch, fwd_generic, bwd_generic):
-    """The rglru fast kernels write and read the general path's checkpoint
-    layout: a forward on one path followed by a backward on the other gives
-    the results of the fast path on both."""
+def test_rglru_fast_path_matches_generic(dev, monkeypatch, method, fwd_generic, bwd_generic):
+    """The one-state rglru / s7 fast kernels write and read the general path's
+    checkpoint layout: a forward on one path followed by a backward on the
+    other gives the results of the fast path on both."""
     L = 1100
     dout = torch.randn(2, 48, L, generator=torch.Generator().manual_seed(3)).to(dev)
     res = []
@@ -140,7 +147,7 @@ def test_rglru_fast_path_matches_generic(dev, monkeypatch, fwd_generic, bwd_gene
         lv = _rglru_leaves(dev, L, 11)
         monkeypatch.setenv("LRNNX_SCAN_GENERIC", fg)
         out, last = selective_scan_fn(lv["u"], lv["delta"], lv["A"], lv["B"], lv["C"], lv["D"], None, None, None,
-                                      False, True, "rglru")
+                                      False, True, method)
         monkeypatch.setenv("LRNNX_SCAN_GENERIC", bg)
         out.backward(dout)
         torch.cuda.synchronize()
