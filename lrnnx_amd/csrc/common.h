@@ -80,6 +80,28 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // otherwise move the chain to that read and keep every step's operands live.
 __device__ __forceinline__ void pin_vgpr(float& v) { asm volatile("" : "+v"(v)); }
 
+// sin and cos of x without branches.  Cody-Waite reduction to r = x - k pi/2,
+// |r| <= pi/4, with pi/2 split into three parts (the leading ones short, so
+// the products k * part are exact for |k| < 2^15); then the minimax
+// polynomials of the Cephes library (S. L. Moshier) for sin and cos on
+// [-pi/4, pi/4] (about 1 ulp), and the quadrant k mod 4 selects and signs them.
+__device__ __forceinline__ void sincos_cw(float x, float& sn, float& cs) {
+  const float k = __builtin_rintf(x * 0.63661977236758134f);  // 2 / pi
+  float r = fmaf(-k, 1.5703125f, x);
+  r = fmaf(-k, 4.837512969970703125e-4f, r);
+  r = fmaf(-k, 7.54978995489188216e-8f, r);
+  const float z = r * r;
+  const float sp = fmaf(z, fmaf(z, -1.9515295891e-4f, 8.3321608736e-3f), -1.6666654611e-1f);
+  const float s = fmaf(r * z, sp, r);
+  const float cp = fmaf(z, fmaf(z, 2.443315711809948e-5f, -1.388731625493765e-3f), 4.166664568298827e-2f);
+  const float c = fmaf(z * z, cp, fmaf(-0.5f, z, 1.f));
+  const int q = (int)k;
+  const float S = (q & 1) ? c : s;
+  const float C = (q & 1) ? s : c;
+  sn = (q & 2) ? -S : S;
+  cs = ((q + 1) & 2) ? -C : C;
+}
+
 // softplus with the reference's threshold: identity above 20
 // (selective_scan.cuh:172-174; F.softplus default threshold).
 __device__ __forceinline__ float softplus20(float x) { return x <= 20.f ? log1pf(expf(x)) : x; }

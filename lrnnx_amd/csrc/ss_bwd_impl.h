@@ -8,8 +8,8 @@
 // Tiles of kTB steps are processed from the end of the sequence to the start;
 // a tile holds kTB / kCk checkpoint intervals ("sub-chunks").  Per sub-chunk a
 // wave takes h at the sub-chunk start from the forward's fp32 checkpoints,
-// recomputes A_bar and h for the kCk steps into VGPRs, then walks the steps
-// backwards:
+// recomputes h (and A_bar where kAbLive) for the kCk steps into VGPRs, then
+// walks the steps backwards:
 //   dh_t = A_bar_{t+1} dh_{t+1} + C_t dy_t
 // accumulating the per-step partials of du / ddelta / ddeltaA (summed over
 // its kS states; crossed over waves in LDS), dA (per lane) and the values of

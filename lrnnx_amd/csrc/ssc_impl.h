@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "ss_common.h"
+#include "tile_io.h"
 
 namespace lrnnx {
 namespace ssc {
@@ -44,21 +45,23 @@ __device__ __forceinline__ cf cfma(cf a, cf b, cf c) {
   return cf{fmaf(a.r, b.r, fmaf(-a.i, b.i, c.r)), fmaf(a.r, b.i, fmaf(a.i, b.r, c.i))};
 }
 __device__ __forceinline__ cf cdiv(cf a, cf b) {
-  const float den = b.r * b.r + b.i * b.i;
-  return cf{(a.r * b.r + a.i * b.i) / den, (a.i * b.r - a.r * b.i) / den};
+  const float inv = __builtin_amdgcn_rcpf(b.r * b.r + b.i * b.i);
+  return cf{(a.r * b.r + a.i * b.i) * inv, (a.i * b.r - a.r * b.i) * inv};
 }
 __device__ __forceinline__ cf cexp_(cf z) {
   float s, c;
-  sincosf(z.i, &s, &c);
-  const float e = expf(z.r);
+  sincos_cw(z.i, s, c);
+  const float e = exp_fast(z.r);
   return cf{e * c, e * s};
 }
-// exp(z) - 1 without cancellation: expm1(x) cos y - 2 sin^2(y/2) + i e^x sin y
+// exp(z) - 1 without cancellation: expm1(x) cos y - 2 sin^2(y/2) + i e^x sin y,
+// with sin y = 2 sin(y/2) cos(y/2) and cos y = 1 - 2 sin^2(y/2)
 __device__ __forceinline__ cf cexpm1_(cf z) {
-  float s, c;
-  sincosf(z.i, &s, &c);
-  const float sh = sinf(0.5f * z.i);
-  return cf{fmaf(expm1f(z.r), c, -2.f * sh * sh), expf(z.r) * s};
+  float sh, ch;
+  sincos_cw(0.5f * z.i, sh, ch);
+  const float e = exp_fast(z.r);
+  const float s2 = 2.f * sh * sh;
+  return cf{fmaf(expm1_from(z.r, e), 1.f - s2, -s2), e * (2.f * sh * ch)};
 }
 // Re(conj(a) * b)
 __device__ __forceinline__ float cdotr(cf a, cf b) { return fmaf(a.r, b.r, a.i * b.i); }
@@ -69,7 +72,9 @@ constexpr int kPad = kWave + 1; // LDS row pitch of [kTc][64] tiles (conflict-fr
 
 __host__ __device__ constexpr int ck_c(int kS) { return 16 / kS; }  // kS * kCk = 16 complex values
 
-inline int pick_kS_c(int64_t N) { return N <= 4 ? 1 : (N <= 16 ? 4 : (N <= 64 ? 8 : 16)); }
+// states per wave: up to 8 waves per workgroup below N = 16, so that a grid
+// of B * D / 64 workgroups still gives the SIMDs more than one wave each
+inline int pick_kS_c(int64_t N) { return N <= 8 ? 1 : (N <= 16 ? 2 : (N <= 32 ? 4 : (N <= 64 ? 8 : 16))); }
 
 struct SSCGeom {
   int CB, n_cb, kS, nW, ck;
@@ -110,8 +115,8 @@ __device__ __forceinline__ void cdisc(float dtA, float dl, cf A, cf& Ab, cf& bet
   }
 }
 
-__device__ __forceinline__ float softplus_ref(float x) { return x <= 20.f ? log1pf(expf(x)) : x; }
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+__device__ __forceinline__ float softplus_ref(float x) { return softplus_fast(x); }
+__device__ __forceinline__ float sigmoidf_(float x) { return sigmoid_fast(x); }
 
 struct SSCPtrs {
   int64_t b, d0;
@@ -144,8 +149,8 @@ __device__ __forceinline__ void load_bc(const float* __restrict__ base, int64_t 
   }
 }
 
-// at most 4 / 8 / 16 waves for kS <= 4 / 8 / 16 (N <= 16 / 64 / 256)
-__host__ __device__ constexpr int ssc_max_threads(int kS) { return kS <= 4 ? 256 : kS * kWave; }
+// at most 8 waves for kS <= 8 (N <= 64), 16 for kS = 16 (N <= 256)
+__host__ __device__ constexpr int ssc_max_threads(int kS) { return kS <= 8 ? 8 * kWave : kS * kWave; }
 
 template <int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
 __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_fwd_kernel(const lrnnx_selective_scan_args a, const int CB,
@@ -564,7 +569,7 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
       else ddl += P2;
       if (a.delta_softplus) {
         float x = s_dl[t * kPad + r];  // softplus'(x) = sigmoid(x) = 1 - exp(-softplus(x))
-        ddl *= -expm1f(-x);
+        ddl *= one_minus_exp_neg(x);
       }
       gdu[r * a.du.s1 + t0 + t] = du;
       gddl[r * a.ddelta.s1 + t0 + t] = ddl;
@@ -727,6 +732,7 @@ hipError_t ssc_dispatch(const lrnnx_selective_scan_args& a, const SSCGeom& g, fl
                         const float* ckp, hipStream_t st) {
   switch (g.kS) {
     case 1: return ssc_dispatch_m<1, kBwd>(a, g, ws, wo, ckp, st);
+    case 2: return ssc_dispatch_m<2, kBwd>(a, g, ws, wo, ckp, st);
     case 4: return ssc_dispatch_m<4, kBwd>(a, g, ws, wo, ckp, st);
     case 8: return ssc_dispatch_m<8, kBwd>(a, g, ws, wo, ckp, st);
     case 16: return ssc_dispatch_m<16, kBwd>(a, g, ws, wo, ckp, st);

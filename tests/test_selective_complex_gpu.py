@@ -53,7 +53,13 @@ def test_complex_methods(dev, method, varB, varC):
     _run(dev, 2, 64, 40, 4, method=method, varB=varB, varC=varC)
 
 
-@pytest.mark.parametrize("N", [1, 3, 16, 40, 100])
+@pytest.mark.parametrize("method", ["mamba", "zoh", "bilinear", "dirac"])
+def test_complex_methods_two_states_per_wave(dev, method):
+    # 9 <= N <= 16 runs two states per wave (here 6 waves, the last one full)
+    _run(dev, 2, 64, 40, 12, method=method)
+
+
+@pytest.mark.parametrize("N", [1, 3, 8, 16, 30, 40, 100])
 def test_complex_dstate(dev, N):
     _run(dev, 1, 70, 33, N)
 

@@ -207,3 +207,26 @@ def test_fast_path_matches_generic(dev, itype, monkeypatch):
     rt = 1e-5 if itype == torch.float32 else 1e-2
     for n, a, b in zip(names, res[0], res[1]):
         close(n, a, b.cpu().double(), rt, rt)
+
+
+def test_binding_bwd_recompute_out_z(dev):
+    """selective_scan_cuda.bwd with recompute_out_z=True appends out_z, equal to
+    the forward's (selective_scan_cpu.cpp:627-631 return order)."""
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    inp = R.make_selective_inputs(2, 64, 96, 16, seed=12)
+    d = to_dev(inp, dev)
+    g = torch.Generator().manual_seed(13)
+    dout = torch.randn(2, 64, 96, generator=g).to(dev)
+    d["B"], d["C"] = d["B"].unsqueeze(1).contiguous(), d["C"].unsqueeze(1).contiguous()  # (b, g, n, l)
+    fwd = ssc.fwd(d["u"], d["delta"], d["A"], d["B"], d["C"], d["D"], d["z"], d["delta_bias"], None, True, "mamba")
+    out, x, out_z = fwd
+    res = ssc.bwd(d["u"], d["delta"], d["A"], d["B"], d["C"], d["D"], d["z"], d["delta_bias"], None, dout, x, out,
+                  None, True, True, "mamba")
+    assert len(res) == 9  # du, ddelta, dA, dB, dC, dD, ddelta_bias, dz, out_z
+    close("out_z", res[-1], out_z.cpu().double(), 1e-6, 1e-6)
+    ref = ssc.bwd(d["u"], d["delta"], d["A"], d["B"], d["C"], d["D"], d["z"], d["delta_bias"], None, dout, x, out,
+                  None, True, False, "mamba")
+    assert len(ref) == 8
+    for n, a_, b_ in zip(("du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz"), res[:8], ref):
+        close(n, a_, b_.cpu().double(), 1e-6, 1e-6)
