@@ -105,9 +105,6 @@ __device__ __forceinline__ void sincos_cw(float x, float& sn, float& cs) {
 // softplus with the reference's threshold: identity above 20
 // (selective_scan.cuh:172-174; F.softplus default threshold).
 __device__ __forceinline__ float softplus20(float x) { return x <= 20.f ? log1pf(expf(x)) : x; }
-// d softplus / dx = sigmoid(x), 1 above the threshold
-// (selective_scan_backward.cuh:797-799).
-__device__ __forceinline__ float softplus20_grad(float x) { return x <= 20.f ? 1.f / (1.f + expf(-x)) : 1.f; }
 
 __device__ __forceinline__ float silu(float z) { return z / (1.f + expf(-z)); }
 

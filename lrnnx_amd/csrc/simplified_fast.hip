@@ -338,6 +338,16 @@ __device__ __forceinline__ cf crcp(cf z) {   // 1 / z
   return cf{z.r * inv, -z.i * inv};
 }
 
+// exp(z) for the per-step discretisation: v_exp_f32 and the branch-free
+// sincos_cw (each step has its own A_bar, so per-step rounding does not compound
+// the way a constant A_bar's does in A_bar^t)
+__device__ __forceinline__ cf cexp_step(cf z) {
+  float s, c;
+  sincos_cw(z.i, s, c);
+  const float e = __builtin_amdgcn_exp2f(z.r * kLog2e);
+  return cf{e * c, e * s};
+}
+
 // A_bar, beta of one step (simplified_scan.cuh:198-224); dt = deltaA (kDA) or delta
 template <int kMethod, bool kDA>
 __device__ __forceinline__ void sdisc_tv(float dt, float dl, cf A, cf invA, cf& Ab, cf& beta) {
@@ -347,8 +357,8 @@ __device__ __forceinline__ void sdisc_tv(float dt, float dl, cf A, cf invA, cf& 
     Ab = cmul(cadd(one, cscale(A, 0.5f * dt)), inv);
     beta = kDA ? cscale(crcp(csub(one, cscale(A, 0.5f * dl))), dl) : cscale(inv, dl);
   } else {
-    Ab = cexp_(cscale(A, dt));
-    if constexpr (kMethod == LRNNX_ZOH) beta = cmul(csub(kDA ? cexp_(cscale(A, dl)) : Ab, one), invA);
+    Ab = cexp_step(cscale(A, dt));
+    if constexpr (kMethod == LRNNX_ZOH) beta = cmul(csub(kDA ? cexp_step(cscale(A, dl)) : Ab, one), invA);
     else beta = one;
   }
 }
@@ -550,7 +560,7 @@ __global__ void __launch_bounds__(256) simpf_bwd_tv_kernel(const lrnnx_simplifie
         dAb_dt = cmul(A, Ab[j]);
         dAb_dA = cscale(Ab[j], dt);
         if constexpr (kMethod == LRNNX_ZOH) {
-          const cf e = kDA ? cexp_(cscale(A, dl[j])) : Ab[j];
+          const cf e = kDA ? cexp_step(cscale(A, dl[j])) : Ab[j];
           db_dl = e;
           db_dA = cmul(csub(cscale(e, dl[j]), be[j]), invA);
         }

@@ -115,8 +115,6 @@ __device__ __forceinline__ void cdisc(float dtA, float dl, cf A, cf& Ab, cf& bet
   }
 }
 
-__device__ __forceinline__ float softplus_ref(float x) { return softplus_fast(x); }
-__device__ __forceinline__ float sigmoidf_(float x) { return sigmoid_fast(x); }
 
 struct SSCPtrs {
   int64_t b, d0;
@@ -219,7 +217,7 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_fwd_kernel(const lrnn
     __syncthreads();
     load_tile<kTc>(gd + t0, a.delta.s1, rows, nt, s_dl, tid, blockDim.x, [&](float x, int r) {
       x += bias ? bias[(d0 + r) * a.delta_bias.s0] : 0.f;
-      return a.delta_softplus ? softplus_ref(x) : x;
+      return a.delta_softplus ? softplus_fast(x) : x;
     });
     load_tile<kTc>(gu + t0, a.u.s1, rows, nt, s_u, tid, blockDim.x, [](float x, int) { return x; });
     if constexpr (kDA) load_tile<kTc>(gdA + t0, a.deltaA.s1, rows, nt, s_dt, tid, blockDim.x, [](float x, int) { return x; });
@@ -282,7 +280,7 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_fwd_kernel(const lrnn
       if (go) go[r * a.out.s1 + t0 + t] = y;
       if (has_z && goz) {
         const float zz = s_z[t * kPad + r];
-        goz[r * a.out_z.s1 + t0 + t] = y * zz * sigmoidf_(zz);
+        goz[r * a.out_z.s1 + t0 + t] = y * zz * sigmoid_fast(zz);
       }
     }
   }
@@ -386,7 +384,7 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
     __syncthreads();
     load_tile<kTc>(gd + t0, a.delta.s1, rows, nt, s_dl, tid, blockDim.x, [&](float x, int r) {
       x += bias ? bias[(d0 + r) * a.delta_bias.s0] : 0.f;
-      return a.delta_softplus ? softplus_ref(x) : x;
+      return a.delta_softplus ? softplus_fast(x) : x;
     });
     load_tile<kTc>(gu + t0, a.u.s1, rows, nt, s_u, tid, blockDim.x, [](float x, int) { return x; });
     if constexpr (kDA) load_tile<kTc>(gdA + t0, a.deltaA.s1, rows, nt, s_dt, tid, blockDim.x, [](float x, int) { return x; });
@@ -398,7 +396,7 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
         dy = gdo[r * a.dout.s1 + t0 + t];
         if (has_z) {
           const float zz = gz[r * a.z.s1 + t0 + t];
-          const float sg = sigmoidf_(zz);
+          const float sg = sigmoid_fast(zz);
           gdz[r * a.dz.s1 + t0 + t] = dy * gos[r * a.out_saved.s1 + t0 + t] * sg * (1.f + zz * (1.f - sg));
           dy *= zz * sg;
         }
