@@ -467,6 +467,58 @@ def cpu_configs(torch, R):
     return res
 
 
+def method_configs(torch, dev):
+    """fwd+bwd through the autograd wrappers for the other discretisations and
+    weight types at B=8, D=1536, L=2048 (fp32, event-timed medians of 10): the
+    general kernels (zoh / bilinear / dirac, N=16, variable B/C), the
+    one-state fast path (rglru N=1; the s7 binding call with 256 S7 states) and
+    the complex-weight kernels (N=16)."""
+    import lrnnx_amd as lx
+    from lrnnx_amd import selective_scan_cuda as ssb
+
+    def med(fn, reps=10):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ms = []
+        for _ in range(reps):
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ms.append(e0.elapsed_time(e1))
+        return round(sorted(ms)[len(ms) // 2], 4)
+
+    g = torch.Generator(device=dev).manual_seed(4)
+    Bt, D, L, N = 8, 1536, 2048, 16
+    rn = lambda *s: torch.randn(*s, device=dev, generator=g)
+    u, dl, dout = rn(Bt, D, L).requires_grad_(), (0.5 * rn(Bt, D, L)).requires_grad_(), rn(Bt, D, L)
+    A = (-torch.rand(D, N, device=dev, generator=g) - 0.5).requires_grad_()
+    B, C = rn(Bt, N, L).requires_grad_(), rn(Bt, N, L).requires_grad_()
+    res = {}
+    for m in ("zoh", "bilinear", "dirac"):
+        def fb(m=m):
+            lx.selective_scan_fn(u, dl, A, B, C, None, None, None, None, True, discretization=m).backward(dout)
+        res[f"{m}_n16_fwd_bwd_ms"] = med(fb)
+    dr = (8 * torch.rand(Bt, D, L, device=dev, generator=g)).requires_grad_()
+    a1 = (0.5 * torch.rand(D, 1, device=dev, generator=g) + 0.45).requires_grad_()
+    res["rglru_n1_fwd_bwd_ms"] = med(lambda: lx.rglru_scan_fn(u, dr, a1).backward(dout))
+    n7 = 256
+    Bu, d7, do7 = rn(Bt, n7, L), rn(Bt, n7, L), rn(Bt, n7, L)
+    Ak, Bk, Ck = (torch.zeros(n7, 1, device=dev), torch.ones(n7, 1, device=dev), torch.ones(n7, 1, device=dev))
+
+    def s7():
+        out_k, x_k = ssb.fwd(Bu, d7, Ak, Bk, Ck, None, None, None, None, False, "s7")[:2]
+        ssb.bwd(Bu, d7, Ak, Bk, Ck, None, None, None, None, do7, x_k, out_k, None, False, False, "s7")
+    res["s7_kernel_call_256_states_fwd_bwd_ms"] = med(s7)
+    Ac = torch.complex(-torch.rand(D, N, device=dev, generator=g) - 0.5, rn(D, N)).requires_grad_()
+    Bc, Cc = rn(Bt, 1, N, 2 * L).requires_grad_(), rn(Bt, 1, N, 2 * L).requires_grad_()
+    res["complex_n16_fwd_bwd_ms"] = med(
+        lambda: lx.selective_scan_fn(u, dl, Ac, Bc, Cc, None, None, None, None, True).backward(dout))
+    return res
+
+
 def other_configs(torch, ss, L_, dev):
     """Config 2 (Mamba-130m layer, fwd+bwd) and config 1 (LRU complex scan,
     fwd+bwd) timings, reported beside the headline line."""
@@ -515,6 +567,11 @@ def other_configs(torch, ss, L_, dev):
     torch.cuda.empty_cache()
     res.update(aux_kernels(torch, L_, dev))
     res["cfg4_decode_state_update"] = decode_cfg4(torch, dev)
+    try:
+        res["other_methods_b8_d1536_l2048_f32"] = method_configs(torch, dev)
+    except Exception as e:  # reported in the line; the measurements above stand
+        res["other_methods_b8_d1536_l2048_f32"] = {"error": repr(e)}
+    torch.cuda.empty_cache()
     return res
 
 
