@@ -672,6 +672,9 @@ def main():
     ap.add_argument("--traffic-from", nargs=2, metavar=("READ_CSV", "WRITE_CSV"),
                     help="write profiles/traffic_cfg3.json from two rocprofv3 --pmc counter_collection.csv "
                          "files (TCC_EA0_RDREQ*, TCC_EA0_WRREQ*) of a --copy-calib run, then exit")
+    ap.add_argument("--methods-only", action="store_true",
+                    help="time only the other discretisations / one-state path / complex weights (for a kernel "
+                         "trace of those kernels), print their JSON, then exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print a markdown summary of a rocprofv3 --kernel-trace CSV of this bench, then exit")
     args = ap.parse_args()
@@ -697,6 +700,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     L_.lib()
+    if args.methods_only:
+        print(json.dumps(method_configs(torch, dev)))
+        return
     if args.copy_calib:
         _log(f"copy calibration: {COPY_CALIB_BYTES} bytes read + written")
         src = torch.ones(COPY_CALIB_BYTES // 4, dtype=torch.float32, device=dev)

@@ -4,7 +4,9 @@
 
 The scan runs through this package's ``selective_scan_cuda`` binding with the
 ``"rglru"`` discretisation (A_bar = a ** delta, B_bar = sqrt(1 - A_bar^2),
-identity B / C), exactly as the reference's wrapper drives its own binding.
+identity B / C), exactly as the reference's wrapper drives its own binding;
+the forward keeps the binding's fine state checkpoints for the backward, so
+the backward does not re-run the forward to rebuild them.
 
 ``rglru_inner_fn`` computes the reference's ``RGLRUInnerFn`` forward (causal
 conv1d, the recurrence and input gates, the scan, the stream-1 gate and the
@@ -36,20 +38,23 @@ class RGLRUScanFn(torch.autograd.Function):
         dim, dstate = A.shape
         B = torch.ones(dim, dstate, dtype=u.dtype, device=u.device)
         C = torch.ones(dim, dstate, dtype=u.dtype, device=u.device)
-        out, x = _ss.fwd(u, delta, A, B, C, None, None, None, None, False, "rglru")[:2]
+        # the binding's fwd, keeping the fine state checkpoints for the backward
+        # (the reference's wrapper saves x, from which its backward restarts)
+        a = _ss.build_args(u, delta, A, B, C, None, None, None, None, False, "rglru")
+        out, x, _, ckpt = _ss.run_fwd(a, u, delta, A, None, want_out=True, want_ckpt=True)
         last_state = x[:, :, -1, 1::2]
-        ctx.save_for_backward(u, delta, A, B, C, out, x)
+        ctx.save_for_backward(u, delta, A, B, C, ckpt)
         if return_last_state:
             return out, last_state
         return out
 
     @staticmethod
     def backward(ctx, dout, *args):
-        u, delta, A, B, C, out, x = ctx.saved_tensors
+        u, delta, A, B, C, ckpt = ctx.saved_tensors
         if not dout.is_contiguous():
             dout = dout.contiguous()
-        du, ddelta, dA = _ss.bwd(u, delta, A, B, C, None, None, None, None, dout, x, out, None, False, False,
-                                 "rglru")[:3]
+        a = _ss.build_args(u, delta, A, B, C, None, None, None, None, False, "rglru")
+        du, ddelta, dA = _ss.run_bwd(a, u, delta, A, B, C, None, None, None, None, dout, None, ckpt)[:3]
         return du, ddelta, dA, None
 
 

@@ -3,7 +3,8 @@
 (:236-509).
 
 The scan runs through this package's ``selective_scan_cuda`` binding with the
-``"s7"`` discretisation, exactly as the reference's wrapper drives its own
+``"s7"`` discretisation (the forward keeping the fine state checkpoints for
+the backward), exactly as the reference's wrapper drives its own
 binding: the time-varying A goes in as delta, the kernel's A is zero and its
 B / C are ones, one state per "channel" (the S7 state index), and the input
 and output projections B u and C h are einsums around the kernel.
@@ -48,10 +49,12 @@ class S7ScanFn(torch.autograd.Function):
         A_k = torch.zeros(dstate, 1, dtype=Bu.dtype, device=Bu.device)
         B_k = torch.ones(dstate, 1, dtype=Bu.dtype, device=Bu.device)
         C_k = torch.ones(dstate, 1, dtype=Bu.dtype, device=Bu.device)
-        out_k, x_k = _ss.fwd(Bu, delta, A_k, B_k, C_k, None, None, None, None, False, "s7")[:2]
+        # the binding's fwd, keeping the fine state checkpoints for the backward
+        a = _ss.build_args(Bu, delta, A_k, B_k, C_k, None, None, None, None, False, "s7")
+        out_k, _, _, ckpt = _ss.run_fwd(a, Bu, delta, A_k, None, want_out=True, want_ckpt=True)
         y = torch.einsum("bhnl,bnl->bhl", C.float(), out_k.float())
         last_state = out_k[:, :, -1]
-        ctx.save_for_backward(u, B, C, bias, Bu, out_k, x_k, delta, A_k, B_k, C_k)
+        ctx.save_for_backward(u, B, C, bias, Bu, out_k, ckpt, delta, A_k, B_k, C_k)
         if return_last_state:
             return y.to(u.dtype), last_state
         return y.to(u.dtype)
@@ -59,14 +62,14 @@ class S7ScanFn(torch.autograd.Function):
     @staticmethod
     @_bwd
     def backward(ctx, dout, *args):
-        u, B, C, bias, Bu, out_k, x_k, delta, A_k, B_k, C_k = ctx.saved_tensors
+        u, B, C, bias, Bu, out_k, ckpt, delta, A_k, B_k, C_k = ctx.saved_tensors
         dout = dout.float()
         if dout.stride(-1) != 1:
             dout = dout.contiguous()
         dC = torch.einsum("bhl,bnl->bhnl", dout, out_k.float())
         dout_k = torch.einsum("bhnl,bhl->bnl", C.float(), dout).contiguous()
-        dBu, ddelta = _ss.bwd(Bu, delta, A_k, B_k, C_k, None, None, None, None, dout_k, x_k, out_k, None, False,
-                              False, "s7")[:2]
+        a = _ss.build_args(Bu, delta, A_k, B_k, C_k, None, None, None, None, False, "s7")
+        dBu, ddelta = _ss.run_bwd(a, Bu, delta, A_k, B_k, C_k, None, None, None, None, dout_k, None, ckpt)[:2]
         dB = torch.einsum("bnl,bhl->bnhl", dBu, u.float())
         du = torch.einsum("bnhl,bnl->bhl", B.float(), dBu)
         return du.to(u.dtype), ddelta, dB, dC, (dBu if bias is not None else None), None
