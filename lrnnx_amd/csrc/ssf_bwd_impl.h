@@ -30,8 +30,11 @@
 //               ddelta_bias terms stay in per-thread registers) and
 //               conversion of raw tile k-1 (delta' = softplus(delta + bias),
 //               u, dy = dout silu(z) to fp32, dz written here, B / C rows).
-// The fp32 operands are double buffered: the epilogue of tile k and the
-// conversion of tile k-1 share the finish phase.
+// The fp32 operands have one buffer: in the finish phase every thread reads
+// its own slots of tile k (epilogue) before it writes the same slots with
+// tile k-1 (conversion), and the compute phases read them only between the
+// barriers.  (Keeping the LDS under 80 KB also for fp32 I/O with z lets two
+// workgroups share a CU.)
 #pragma once
 #include <type_traits>
 
@@ -72,9 +75,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   __shared__ __attribute__((aligned(16))) char s_raw_b[kRawS];
   __shared__ __attribute__((aligned(16))) char s_raw_c[kRawS];
   __shared__ __attribute__((aligned(16))) float s_ck[2][16 * kWave];   // [buf][n][lane] h at the tile start
-  __shared__ __attribute__((aligned(16))) float s_dl[2][kOp];          // [buf][g][lane][4] delta'
-  __shared__ __attribute__((aligned(16))) float s_u[2][kOp];           // u
-  __shared__ __attribute__((aligned(16))) float s_dy[2][kOp];          // dout silu(z)
+  __shared__ __attribute__((aligned(16))) float s_dl[kOp];             // [g][lane][4] delta'
+  __shared__ __attribute__((aligned(16))) float s_u[kOp];              // u
+  __shared__ __attribute__((aligned(16))) float s_dy[kOp];             // dout silu(z)
   __shared__ __attribute__((aligned(16))) float s_B[kT * 16];          // [t][n]
   __shared__ __attribute__((aligned(16))) float s_C[kT * 16];
   __shared__ __attribute__((aligned(16))) float s_P1[kNW * kOp];       // [w][g][lane][4] sum_k dh B
@@ -144,8 +147,8 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
                                                reinterpret_cast<char*>(s_ck[tile & 1]), w, kNW, lane);
   };
 
-  // raw tile -> fp32 operands of buffer p; dz is written here
-  auto convert = [&](int64_t tile, int p) __attribute__((always_inline)) {
+  // raw tile -> fp32 operands; dz is written here
+  auto convert = [&](int64_t tile) __attribute__((always_inline)) {
     float vu[4], vd[4], vdo[4];
     const int ro = er * kRow + eq * kEb;   // byte offset of this thread's 4 raw elements
     raw4_to_f32<IT>(s_raw_u + ro, vu);
@@ -172,9 +175,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       store4<IT>(gdz + tile * kT, dz);
     }
     const int o = op_off<0>(eq, er);
-    *reinterpret_cast<float4*>(&s_dl[p][o]) = make_float4(vd[0], vd[1], vd[2], vd[3]);
-    *reinterpret_cast<float4*>(&s_u[p][o]) = make_float4(vu[0], vu[1], vu[2], vu[3]);
-    *reinterpret_cast<float4*>(&s_dy[p][o]) = make_float4(dy[0], dy[1], dy[2], dy[3]);
+    *reinterpret_cast<float4*>(&s_dl[o]) = make_float4(vd[0], vd[1], vd[2], vd[3]);
+    *reinterpret_cast<float4*>(&s_u[o]) = make_float4(vu[0], vu[1], vu[2], vu[3]);
+    *reinterpret_cast<float4*>(&s_dy[o]) = make_float4(dy[0], dy[1], dy[2], dy[3]);
     // B / C rows, transposed to step-major: threads [0, 64) B, [64, 128) C,
     // 4 steps of one state each; states >= N are zero
     if (tid < 2 * 16 * 4) {
@@ -189,8 +192,8 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     }
   };
 
-  // epilogue of tile (fp32 buffer p): du, ddelta; dD / ddelta_bias terms
-  auto epilogue = [&](int64_t tile, int p) __attribute__((always_inline)) {
+  // epilogue of tile: du, ddelta; dD / ddelta_bias terms
+  auto epilogue = [&](int64_t tile) __attribute__((always_inline)) {
     const int o = op_off<0>(eq, er);
     float4 P1 = *reinterpret_cast<const float4*>(&s_P1[o]);
     float4 P2 = *reinterpret_cast<const float4*>(&s_P2[o]);
@@ -201,9 +204,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       P1.x += q1.x; P1.y += q1.y; P1.z += q1.z; P1.w += q1.w;
       P2.x += q2.x; P2.y += q2.y; P2.z += q2.z; P2.w += q2.w;
     }
-    const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[p][o]);
-    const float4 u4 = *reinterpret_cast<const float4*>(&s_u[p][o]);
-    const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[p][o]);
+    const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[o]);
+    const float4 u4 = *reinterpret_cast<const float4*>(&s_u[o]);
+    const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[o]);
     const float p1[4] = {P1.x, P1.y, P1.z, P1.w}, p2[4] = {P2.x, P2.y, P2.z, P2.w};
     const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, uu[4] = {u4.x, u4.y, u4.z, u4.w};
     const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
@@ -224,7 +227,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   fetch(n_tiles - 1);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
   __syncthreads();
-  convert(n_tiles - 1, (int)((n_tiles - 1) & 1));
+  convert(n_tiles - 1);
   __syncthreads();
 
   for (int64_t tile = n_tiles - 1; tile >= 0; --tile) {
@@ -247,9 +250,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
         // scheduling fence: the LDS operand loads of later groups are not
         // hoisted above this group's arithmetic (that would exceed 256 VGPRs)
         __builtin_amdgcn_sched_barrier(0);
-        const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[p][op_off<0>(g, lane)]);
-        const float4 u4 = *reinterpret_cast<const float4*>(&s_u[p][op_off<0>(g, lane)]);
-        const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[p][op_off<0>(g, lane)]);
+        const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[op_off<0>(g, lane)]);
+        const float4 u4 = *reinterpret_cast<const float4*>(&s_u[op_off<0>(g, lane)]);
+        const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[op_off<0>(g, lane)]);
         const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, uu[4] = {u4.x, u4.y, u4.z, u4.w};
         const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
 #pragma unroll
@@ -302,9 +305,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
 #pragma unroll
     for (int g = kG - 1; g >= 0; --g) {
       __builtin_amdgcn_sched_barrier(0);
-      const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[p][op_off<0>(g, lane)]);
-      const float4 u4 = *reinterpret_cast<const float4*>(&s_u[p][op_off<0>(g, lane)]);
-      const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[p][op_off<0>(g, lane)]);
+      const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[op_off<0>(g, lane)]);
+      const float4 u4 = *reinterpret_cast<const float4*>(&s_u[op_off<0>(g, lane)]);
+      const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[op_off<0>(g, lane)]);
       const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
       const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
       float p1v[4], p2v[4];
@@ -345,8 +348,8 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       wsB[tile * kT] = dB_part;
       wsC[tile * kT] = dC_part;
     }
-    epilogue(tile, p);
-    if (tile > 0) convert(tile - 1, p ^ 1);
+    epilogue(tile);
+    if (tile > 0) convert(tile - 1);
     __syncthreads();
   }
 
