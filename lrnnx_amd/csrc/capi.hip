@@ -30,6 +30,7 @@ bool ssf_bwd_f32(const lrnnx_selective_scan_args&, float*, const float*, hipStre
 bool ssf_bwd_bf16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t, hipError_t*);
 bool ssf_bwd_f16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t, hipError_t*);
 hipError_t ss_fwd_other_f32(const lrnnx_selective_scan_args&, hipStream_t);
+int64_t ssf_fwd_workspace_bytes(const lrnnx_selective_scan_args&);
 hipError_t ss_bwd_mamba_f32(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
 hipError_t ss_bwd_mamba_bf16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
 hipError_t ss_bwd_mamba_f16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
@@ -170,7 +171,10 @@ int64_t lrnnx_selective_scan_ckpt_size(const lrnnx_selective_scan_args* a) {
 
 int64_t lrnnx_selective_scan_workspace_size(const lrnnx_selective_scan_args* a, int bwd) {
   if (!a) return -1;
-  if (!bwd) return 0;
+  if (!bwd) {  // optional: lets the fast path split L for grids too small to fill the chip
+    if (a->wtype == LRNNX_C64 || a->method != LRNNX_MAMBA || !fast_paths_enabled()) return 0;
+    return ssf_fwd_workspace_bytes(*a);
+  }
   if (a->wtype == LRNNX_C64) return ssc_bwd_ws_bytes(*a);
   return ss_bwd_ws_bytes(*a);
 }
@@ -207,6 +211,8 @@ int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args* a, void* stream) {
     f.z.ptr = nullptr;
     f.x = nullptr;
     f.ckpt = reinterpret_cast<char*>(a->workspace) + ss_bwd_ckpt_offset_bytes(*a);
+    f.workspace = nullptr;  // the rebuild runs unsplit: the workspace holds its checkpoints
+    f.workspace_bytes = 0;
     hipError_t e = a->method == LRNNX_MAMBA ? fwd_mamba(f, st) : ss_fwd_other_f32(f, st);
     if (from_hip(e, "selective_scan_bwd (checkpoint rebuild)")) return 1;
     ckp = static_cast<const float*>(f.ckpt);

@@ -7,4 +7,13 @@ bool ssf_fwd_f32(const lrnnx_selective_scan_args& a, hipStream_t st, hipError_t*
   *err = ssf_fwd_launch<float>(a, ss_geom(a).n_ck, st);
   return true;
 }
+
+// Forward workspace bytes of the fast path's L split (0 when it does not split).
+int64_t ssf_fwd_workspace_bytes(const lrnnx_selective_scan_args& a) {
+  switch (a.itype) {
+    case LRNNX_F32: return ssf_fwd_ws_bytes<float>(a);
+    case LRNNX_BF16: return ssf_fwd_ws_bytes<bf16>(a);
+    default: return ssf_fwd_ws_bytes<f16>(a);
+  }
+}
 }  // namespace lrnnx

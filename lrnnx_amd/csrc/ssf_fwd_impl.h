@@ -68,11 +68,26 @@ __device__ __forceinline__ float sigmoidf_fast(float z) {
   return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-z * kLog2e));
 }
 
+// Split of L into segments for grids too small to fill the chip (blockIdx.z =
+// segment).  Segment s covers tiles [s * tiles, min((s + 1) * tiles, n_tiles)).
+// Summary pass: h_end != nullptr; the segment runs from h = 0 and writes its
+// final state and its sum of delta' (no other outputs).  Main pass: h_init !=
+// nullptr; the segment starts from h_init and from dsum_pre, the sum of delta'
+// from its 2048-step chunk's start to the segment start (for the x carries).
+// Buffers: states [seg][b][n][d], sums [seg][b][d].
+struct SsfSeg {
+  int64_t tiles;
+  const float* h_init;
+  const float* dsum_pre;
+  float* h_end;
+  float* dsum_seg;
+};
+
 }  // namespace ssf
 
 template <typename IT, bool kSP, bool kZ>
 __global__ void __launch_bounds__(ssf::kNT)
-ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
+ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf::SsfSeg sg) {
   using namespace ssf;
   constexpr int kT = tile_steps<IT>();   // steps per tile
   constexpr int kE = 16 / sizeof(IT);    // elements per 16-byte block
@@ -128,14 +143,19 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
     const int n = n0 + k;
     const float Av = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + lane) * a.A.s0 + n * a.A.s1] : -1.f;
     a2[k] = Av * kLog2e;
-    h[k] = 0.f;
+    h[k] = (sg.h_init && n < N) ? sg.h_init[((blockIdx.z * a.batch + b) * N + n) * D + d0 + lane] : 0.f;
   }
   // per-thread constants of the per-element phases (channel d0 + er)
   const float e_bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[(d0 + er) * a.delta_bias.s0] : 0.f;
   const float e_D = a.D.ptr ? static_cast<const float*>(a.D.ptr)[(d0 + er) * a.D.s0] : 0.f;
-  float e_dsum = 0.f;  // sum of this thread's delta' over the current 2048-step chunk
+  // sum of this thread's delta' over the current 2048-step chunk (a segment
+  // that starts inside a chunk takes the chunk's earlier sum on one thread)
+  float e_dsum = (sg.dsum_pre && eq == 0) ? sg.dsum_pre[(blockIdx.z * a.batch + b) * D + d0 + er] : 0.f;
+  float e_seg = 0.f;  // sum of this thread's delta' over the segment (summary pass)
 
   const int64_t n_tiles = L / kT;
+  const int64_t tb = (int64_t)blockIdx.z * sg.tiles;                     // this segment's tiles
+  const int64_t te = tb + sg.tiles < n_tiles ? tb + sg.tiles : n_tiles;
   const int64_t n_xc = (L + kXChunk - 1) / kXChunk;
 
   auto fetch = [&](int64_t tile) __attribute__((always_inline)) {
@@ -162,6 +182,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
       vd[i] = dl;
     }
     e_dsum += dsum;
+    e_seg += dsum;
 #pragma unroll
     for (int i = 0; i < kE; i += 4) {
       const int o = op_off<kSh>((eq * kE + i) >> 2, er);
@@ -235,17 +256,17 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
     return ((tile + 1) * kT) % kXChunk == 0 || tile + 1 == n_tiles;
   };
 
-  // ---- prologue: tile 0
-  fetch(0);
+  // ---- prologue: the segment's first tile
+  fetch(tb);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
   __syncthreads();
   convert();
   __syncthreads();
 
   float* sYw = s_Y + w * kG * kWave * 4;
-  for (int64_t tile = 0; tile < n_tiles; ++tile) {
-    if (tile + 1 < n_tiles) fetch(tile + 1);
-    if (tile > 0 && xp && chunk_end(tile - 1)) store_x(tile - 1);
+  for (int64_t tile = tb; tile < te; ++tile) {
+    if (tile + 1 < te) fetch(tile + 1);
+    if (tile > tb && xp && chunk_end(tile - 1)) store_x(tile - 1);
 
     // ---- compute(tile)
     const int64_t t0 = tile * kT;
@@ -290,10 +311,45 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck) {
       s_dsum[tid] = e_dsum;
       e_dsum = 0.f;
     }
-    if (tile + 1 < n_tiles) convert();
+    if (tile + 1 < te) convert();
     __syncthreads();
   }
-  if (xp) store_x(n_tiles - 1);
+  if (xp && chunk_end(te - 1)) store_x(te - 1);
+  if (sg.h_end) {  // summary pass: the segment's final state and sum of delta'
+#pragma unroll
+    for (int k = 0; k < kS; ++k)
+      if (n0 + k < N) sg.h_end[((blockIdx.z * a.batch + b) * N + n0 + k) * D + d0 + lane] = h[k];
+    e_seg += dpp_mov<kDppQuadXor1>(e_seg);  // the kQ = 4 threads of a channel are consecutive lanes
+    e_seg += dpp_mov<kDppQuadXor2>(e_seg);
+    if (eq == 0) sg.dsum_seg[(blockIdx.z * a.batch + b) * D + d0 + er] = e_seg;
+  }
+}
+
+// Chains the segments' carries, in segment order, per (b, n, d):
+// h_init[0] = 0, h_init[s + 1] = exp(A dsum_seg[s]) h_init[s] + h_end[s];
+// and per (b, d) the sum of delta' from each segment's chunk start.
+template <typename IT>  // one instantiation per unit that launches it
+__global__ void __launch_bounds__(256)
+ssf_seg_chain_kernel(const lrnnx_selective_scan_args a, const ssf::SsfSeg sg, const int n_seg, const int seg_steps,
+                     float* __restrict__ h_init, float* __restrict__ dsum_pre) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (b, n, d)
+  const int64_t B = a.batch, D = a.dim, N = a.dstate;
+  if (i >= B * N * D) return;
+  const int64_t d = i % D, n = (i / D) % N, b = i / (D * N);
+  const float a2 = static_cast<const float*>(a.A.ptr)[d * a.A.s0 + n * a.A.s1] * kLog2e;
+  float carry = 0.f, pre = 0.f;
+  for (int s = 0; s < n_seg; ++s) {
+    const int64_t o = ((s * B + b) * N + n) * D + d;
+    h_init[o] = carry;
+    const int64_t t_start = (int64_t)s * seg_steps;
+    if (t_start % kXChunk == 0) pre = 0.f;
+    if (n == 0) dsum_pre[(s * B + b) * D + d] = pre;
+    if (s + 1 < n_seg) {
+      const float ds = sg.dsum_seg[(s * B + b) * D + d];
+      carry = fmaf(__builtin_amdgcn_exp2f(a2 * ds), carry, sg.h_end[o]);
+      pre += ds;
+    }
+  }
 }
 
 namespace ssf {
@@ -326,18 +382,86 @@ inline bool ssf_fwd_eligible(const lrnnx_selective_scan_args& a) {
   return ssf::rows_aligned<IT>(a.out, false) && ssf::rows_aligned<IT>(a.out_z, false);
 }
 
+namespace ssf {
+// Steps per segment of the L split: 0 (no split) for grids of more than 128
+// workgroups (B * D / 64; half the CUs), where the summary pass costs more than
+// the added parallelism gains (measured: 192 workgroups ran 16 % slower
+// split), else the shortest power of two >= 128 steps that keeps the grid at
+// most 512 workgroups.  Powers of two keep every 2048-step chunk boundary on a
+// segment boundary and are multiples of every tile length.
+inline int64_t seg_steps(const lrnnx_selective_scan_args& a) {
+  const int64_t wgs = (a.dim / kWave) * a.batch;
+  if (wgs > 128) return 0;
+  int64_t steps = 128;
+  while (steps < a.seqlen && wgs * ((a.seqlen + steps - 1) / steps) > 512) steps *= 2;
+  return steps < a.seqlen ? steps : 0;
+}
+inline int64_t n_segs(const lrnnx_selective_scan_args& a, int64_t steps) { return (a.seqlen + steps - 1) / steps; }
+// workspace of the split: h_end and h_init [seg][b][n][d], dsum_seg and dsum_pre [seg][b][d]
+inline int64_t split_ws_floats(const lrnnx_selective_scan_args& a, int64_t S) {
+  return 2 * S * a.batch * a.dstate * a.dim + 2 * S * a.batch * a.dim;
+}
+}  // namespace ssf
+
+// Bytes of forward workspace the fast path uses for this call (0: no split).
+template <typename IT>
+inline int64_t ssf_fwd_ws_bytes(const lrnnx_selective_scan_args& a) {
+  if (!ssf_fwd_eligible<IT>(a)) return 0;
+  const int64_t steps = ssf::seg_steps(a);
+  return steps ? ssf::split_ws_floats(a, ssf::n_segs(a, steps)) * (int64_t)sizeof(float) : 0;
+}
+
+template <typename IT, bool kSP>
+inline void ssf_fwd_launch_t(const lrnnx_selective_scan_args& a, int64_t n_ck, const ssf::SsfSeg& sg, unsigned nz,
+                             bool z, hipStream_t st) {
+  const dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch, nz);
+  if (z) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true>), grid, dim3(ssf::kNT), 0, st, a, n_ck, sg);
+  else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false>), grid, dim3(ssf::kNT), 0, st, a, n_ck, sg);
+}
+
+// One launch over the whole of L, or, for small grids and with a workspace of
+// ssf_fwd_ws_bytes, the three-pass split: segment summaries (every segment
+// but the last), the carry chain, then every segment from its initial state.
 template <typename IT>
 inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_ck, hipStream_t st) {
-  dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch);
-  dim3 block(ssf::kNT);
+  constexpr int kT = ssf::tile_steps<IT>();
+  const int64_t n_tiles = a.seqlen / kT;
   const bool z = a.z.ptr != nullptr;
-  if (a.delta_softplus) {
-    if (z) hipLaunchKernelGGL((ssf_fwd_kernel<IT, true, true>), grid, block, 0, st, a, n_ck);
-    else hipLaunchKernelGGL((ssf_fwd_kernel<IT, true, false>), grid, block, 0, st, a, n_ck);
-  } else {
-    if (z) hipLaunchKernelGGL((ssf_fwd_kernel<IT, false, true>), grid, block, 0, st, a, n_ck);
-    else hipLaunchKernelGGL((ssf_fwd_kernel<IT, false, false>), grid, block, 0, st, a, n_ck);
+  auto launch = [&](const lrnnx_selective_scan_args& x, const ssf::SsfSeg& sg, unsigned nz, bool zz) {
+    if (x.delta_softplus) ssf_fwd_launch_t<IT, true>(x, n_ck, sg, nz, zz, st);
+    else ssf_fwd_launch_t<IT, false>(x, n_ck, sg, nz, zz, st);
+  };
+  const int64_t steps = ssf::seg_steps(a);
+  const int64_t need = ssf_fwd_ws_bytes<IT>(a);
+  if (steps == 0 || need == 0 || a.workspace == nullptr || a.workspace_bytes < need ||
+      (reinterpret_cast<uintptr_t>(a.workspace) & 15u) != 0) {
+    launch(a, ssf::SsfSeg{n_tiles, nullptr, nullptr, nullptr, nullptr}, 1, z);
+    return hipGetLastError();
   }
+  const int64_t S = ssf::n_segs(a, steps), tiles = steps / kT;
+  float* ws = static_cast<float*>(a.workspace);
+  const int64_t ns = S * a.batch * a.dstate * a.dim, nd = S * a.batch * a.dim;
+  float* h_end = ws;
+  float* h_init = ws + ns;
+  float* dsum_seg = ws + 2 * ns;
+  float* dsum_pre = ws + 2 * ns + nd;
+  // summaries: no outputs, no z
+  lrnnx_selective_scan_args s = a;
+  s.out.ptr = nullptr;
+  s.out_z.ptr = nullptr;
+  s.z.ptr = nullptr;
+  s.x = nullptr;
+  s.ckpt = nullptr;
+  launch(s, ssf::SsfSeg{tiles, nullptr, nullptr, h_end, dsum_seg}, (unsigned)(S - 1), false);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const ssf::SsfSeg chain{tiles, nullptr, nullptr, h_end, dsum_seg};
+  const int64_t nt = a.batch * a.dstate * a.dim;
+  hipLaunchKernelGGL(ssf_seg_chain_kernel<IT>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st, a, chain, (int)S,
+                     (int)steps, h_init, dsum_pre);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  launch(a, ssf::SsfSeg{tiles, h_init, dsum_pre, nullptr, nullptr}, (unsigned)S, z);
   return hipGetLastError();
 }
 

@@ -122,6 +122,11 @@ def run_fwd(a, u, delta, A, z, want_out=True, want_ckpt=False):
         n = _lib.lib().lrnnx_selective_scan_ckpt_size(a)
         ckpt = torch.empty(max(n, 4) // 4, dtype=torch.float32, device=u.device)
         a.ckpt = ckpt.data_ptr()
+    nws = _lib.lib().lrnnx_selective_scan_workspace_size(a, 0)
+    ws = None
+    if nws > 0:  # small grids: the forward splits L into segments
+        ws = torch.empty(nws, dtype=torch.uint8, device=u.device)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), nws
     with _lib.on_device(u):
         _lib.check(_lib.lib().lrnnx_selective_scan_fwd(a, _lib.stream_of(u)), "selective_scan_fwd")
     return out, x, out_z, ckpt

@@ -194,5 +194,11 @@ def test_workspace_queries_are_host_only():
     a.itype, a.wtype, a.method, a.var_B, a.var_C = _lib.BF16, _lib.F32, 3, 1, 1
     ck = L.lrnnx_selective_scan_ckpt_size(a)
     assert ck == 8 * (4096 // 16) * 16 * 4096 * 4
-    assert L.lrnnx_selective_scan_workspace_size(a, 0) == 0
+    assert L.lrnnx_selective_scan_workspace_size(a, 0) == 0   # 512 workgroups: no split of L
     assert L.lrnnx_selective_scan_workspace_size(a, 1) > 0
+    # one workgroup (B=1, D=64): L = 2048 in 16 segments of 128 steps; h_end and h_init
+    # (seg, b, n, d) plus two (seg, b, d) sums of delta', fp32
+    a.batch, a.dim, a.seqlen = 1, 64, 2048
+    assert L.lrnnx_selective_scan_workspace_size(a, 0) == (2 * 16 * 16 * 64 + 2 * 16 * 64) * 4
+    a.method = 0  # zoh: the general kernels, never split
+    assert L.lrnnx_selective_scan_workspace_size(a, 0) == 0
