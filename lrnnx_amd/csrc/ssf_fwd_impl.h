@@ -404,9 +404,10 @@ inline int64_t split_ws_floats(const lrnnx_selective_scan_args& a, int64_t S) {
 }  // namespace ssf
 
 // Bytes of forward workspace the fast path uses for this call (0: no split).
+// Depends on shapes and options only (the output pointers need not be set).
 template <typename IT>
 inline int64_t ssf_fwd_ws_bytes(const lrnnx_selective_scan_args& a) {
-  if (!ssf_fwd_eligible<IT>(a)) return 0;
+  if (!ssf::shape_ok<IT>(a, ssf::tile_steps<IT>())) return 0;
   const int64_t steps = ssf::seg_steps(a);
   return steps ? ssf::split_ws_floats(a, ssf::n_segs(a, steps)) * (int64_t)sizeof(float) : 0;
 }

@@ -230,3 +230,39 @@ def test_binding_bwd_recompute_out_z(dev):
     assert len(ref) == 8
     for n, a_, b_ in zip(("du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz"), res[:8], ref):
         close(n, a_, b_.cpu().double(), 1e-6, 1e-6)
+
+
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+def test_fast_forward_split_matches_unsplit(dev, itype):
+    """A small grid (B=1, D=64: one workgroup) splits L into segments when the
+    forward gets a workspace; without one it runs unsplit.  Both give the same
+    out, x carries (chunk products and states) and checkpoints, up to the
+    rounding of the carry chain."""
+    from lrnnx_amd import _lib
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    L = 4160  # 2048-step chunk ends inside the run, a ragged last chunk
+    inp = R.make_selective_inputs(1, 64, L, 16, seed=21, itype=itype)
+    d = to_dev(inp, dev)
+    d["B"], d["C"] = d["B"].unsqueeze(1).contiguous(), d["C"].unsqueeze(1).contiguous()
+    res = []
+    for split in (True, False):
+        a = ssc.build_args(d["u"], d["delta"], d["A"], d["B"], d["C"], d["D"], d["z"], d["delta_bias"], None, True,
+                           "mamba")
+        if split:
+            assert _lib.lib().lrnnx_selective_scan_workspace_size(a, 0) > 0
+            out, x, out_z, ckpt = ssc.run_fwd(a, d["u"], d["delta"], d["A"], d["z"], want_ckpt=True)
+        else:
+            out = torch.empty_like(d["u"])
+            out_z = torch.empty_like(d["z"])
+            x = torch.empty((1, 64, 3, 32), dtype=torch.float32, device=dev)
+            ckpt = torch.empty(_lib.lib().lrnnx_selective_scan_ckpt_size(a) // 4, dtype=torch.float32, device=dev)
+            a.out, a.out_z = _lib.view(out, 2), _lib.view(out_z, 2)
+            a.x, a.ckpt = x.data_ptr(), ckpt.data_ptr()
+            a.workspace, a.workspace_bytes = None, 0
+            _lib.check(_lib.lib().lrnnx_selective_scan_fwd(a, _lib.stream_of(d["u"])), "fwd")
+        torch.cuda.synchronize()
+        res.append((out.float(), out_z.float(), x, ckpt))
+    tol = 1e-5 if itype == torch.float32 else 2e-2
+    for name, s_, u_ in zip(("out", "out_z", "x", "ckpt"), res[0], res[1]):
+        close(name, s_, u_.cpu().double(), tol if name in ("out", "out_z") else 1e-5, tol if name in ("out", "out_z") else 1e-5)
