@@ -47,21 +47,30 @@ __host__ __device__ constexpr bool needs_p3() {
 
 struct SSBwdWs {  // fp32 workspace sections (element offsets)
   int64_t dBv, dCv, dA, dBc, dCc, dD, dbias, ckpt, total;
+  // split of L (fast path, small grids): S segments; the per-(b, ...) partials
+  // dA / dD / ddelta_bias are per (segment, b); the adjoint buffers
+  // g_loc, g_init [seg][b][n][d] and dsum [seg][b][d]
+  int64_t S, g_loc, g_init, dsum;
 };
 
 inline int64_t align64(int64_t x) { return (x + 63) / 64 * 64; }
 
-inline SSBwdWs ss_bwd_ws(const lrnnx_selective_scan_args& a, const SSGeom& g, bool need_ckpt) {
+inline SSBwdWs ss_bwd_ws(const lrnnx_selective_scan_args& a, const SSGeom& g, bool need_ckpt, int64_t S = 1) {
   SSBwdWs w;
   int64_t o = 0;
   const int64_t B = a.batch, D = a.dim, N = a.dstate, L = a.seqlen;
+  const int64_t Bp = B * S;  // rows of the per-(segment, b) partials
+  w.S = S;
   w.dBv = o; if (a.var_B) o += align64((int64_t)g.n_cb * B * N * L);
   w.dCv = o; if (a.var_C) o += align64((int64_t)g.n_cb * B * N * L);
-  w.dA = o; o += align64(B * D * N);
-  w.dBc = o; if (!a.var_B) o += align64(B * D * N);
-  w.dCc = o; if (!a.var_C) o += align64(B * D * N);
-  w.dD = o; o += align64(B * D);
-  w.dbias = o; o += align64(B * D);
+  w.dA = o; o += align64(Bp * D * N);
+  w.dBc = o; if (!a.var_B) o += align64(Bp * D * N);
+  w.dCc = o; if (!a.var_C) o += align64(Bp * D * N);
+  w.dD = o; o += align64(Bp * D);
+  w.dbias = o; o += align64(Bp * D);
+  w.g_loc = o; if (S > 1) o += align64(S * B * N * D);
+  w.g_init = o; if (S > 1) o += align64(S * B * N * D);
+  w.dsum = o; if (S > 1) o += align64(S * B * D);
   w.ckpt = o; if (need_ckpt) o += align64(B * g.n_ck * N * D);
   w.total = o;
   return w;
@@ -847,20 +856,20 @@ static hipError_t ss_bwd_reductions(const lrnnx_selective_scan_args& a, const SS
       hipLaunchKernelGGL(ss_reduce_bc_kernel<IT>, rg, dim3(256), 0, st, ws + wo.dCv, a.dC, B, G, N, L, ncpg);
   }
   const unsigned gdn = (unsigned)((D * N + 255) / 256), gd = (unsigned)((D + 255) / 256);
-  hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dA, a.dA, B, D, N);
+  hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dA, a.dA, B * wo.S, D, N);
   if (!kVarB && !batch_only)
-    hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dBc, a.dB, B, D, N);
+    hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dBc, a.dB, B * wo.S, D, N);
   if (!kVarC && !batch_only)
-    hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dCc, a.dC, B, D, N);
+    hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gdn), dim3(256), 0, st, ws + wo.dCc, a.dC, B * wo.S, D, N);
   if (a.dD.ptr) {
     lrnnx_view v = a.dD;
     v.s1 = 0;
-    hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gd), dim3(256), 0, st, ws + wo.dD, v, B, D, (int64_t)1);
+    hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gd), dim3(256), 0, st, ws + wo.dD, v, B * wo.S, D, (int64_t)1);
   }
   if (a.ddelta_bias.ptr) {
     lrnnx_view v = a.ddelta_bias;
     v.s1 = 0;
-    hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gd), dim3(256), 0, st, ws + wo.dbias, v, B, D, (int64_t)1);
+    hipLaunchKernelGGL(ss_reduce_batch_kernel<float>, dim3(gd), dim3(256), 0, st, ws + wo.dbias, v, B * wo.S, D, (int64_t)1);
   }
   return hipGetLastError();
 }

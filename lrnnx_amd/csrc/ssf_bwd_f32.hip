@@ -8,4 +8,15 @@ bool ssf_bwd_f32(const lrnnx_selective_scan_args& a, float* ws, const float* ckp
   *err = ssf_bwd_launch<float>(a, ws, ckp, st);
   return true;
 }
+
+// Segments of the fast backward's split of L for this call (1: no split),
+// for the workspace layout queries.
+int64_t ssf_bwd_segments(const lrnnx_selective_scan_args& a) {
+  if (a.method != LRNNX_MAMBA || a.wtype != LRNNX_F32) return 1;
+  switch (a.itype) {
+    case LRNNX_F32: return ssf_bwd_segs<float>(a);
+    case LRNNX_BF16: return ssf_bwd_segs<bf16>(a);
+    default: return ssf_bwd_segs<f16>(a);
+  }
+}
 }  // namespace lrnnx

@@ -56,7 +56,7 @@ __device__ __forceinline__ float sigmoid_from_softplus(float d) {
 template <typename IT, bool kSP, bool kZ>
 __global__ void __launch_bounds__(ssf::kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __restrict__ ws, const SSBwdWs wo,
-               const float* __restrict__ ckp) {
+               const float* __restrict__ ckp, const int64_t seg_tiles) {
   using namespace ssf;
   constexpr int kT = 16;                  // steps per tile = checkpoint interval
   static_assert(kT == kCk, "one checkpoint interval per tile");
@@ -121,7 +121,8 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     const int n = n0 + k;
     const float A_ = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + lane) * a.A.s0 + n * a.A.s1] : -1.f;
     a2[k] = A_ * kLog2e;
-    gn[k] = 0.f;
+    // split of L: the adjoint entering this segment from the right
+    gn[k] = (wo.S > 1 && n < N) ? ws[wo.g_init + ((blockIdx.z * a.batch + b) * N + n) * D + d0 + lane] : 0.f;
     dA_acc[k] = 0.f;
   }
   const float e_bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[(d0 + er) * a.delta_bias.s0] : 0.f;
@@ -129,6 +130,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   float e_dD = 0.f, e_dbias = 0.f;  // this thread's share of dD and ddelta_bias (channel d0 + er)
 
   const int64_t n_tiles = L / kT;
+  const int64_t tb = (int64_t)blockIdx.z * seg_tiles;   // this segment's tiles [tb, te)
+  const int64_t te = tb + seg_tiles < n_tiles ? tb + seg_tiles : n_tiles;
+  const int64_t prow = (int64_t)blockIdx.z * a.batch + b;  // row of the (segment, b) partials
 
   auto fetch = [&](int64_t tile) __attribute__((always_inline)) {
     const int64_t t0 = tile * kT;
@@ -223,16 +227,16 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     store4<IT>(gddl + tile * kT, dd);
   };
 
-  // ---- prologue: last tile
-  fetch(n_tiles - 1);
+  // ---- prologue: the segment's last tile
+  fetch(te - 1);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
   __syncthreads();
-  convert(n_tiles - 1);
+  convert(te - 1);
   __syncthreads();
 
-  for (int64_t tile = n_tiles - 1; tile >= 0; --tile) {
+  for (int64_t tile = te - 1; tile >= tb; --tile) {
     const int p = (int)(tile & 1);
-    if (tile > 0) fetch(tile - 1);
+    if (tile > tb) fetch(tile - 1);
 
     // ---- compute(tile)
     float h0[kS];
@@ -349,22 +353,99 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       wsC[tile * kT] = dC_part;
     }
     epilogue(tile);
-    if (tile > 0) convert(tile - 1);
+    if (tile > tb) convert(tile - 1);
     __syncthreads();
   }
 
-  // per-(b, d, n) and per-(b, d) partials, summed over b by ss_reduce_batch_kernel
+  // per-((segment, b), d, n) and per-((segment, b), d) partials, summed over
+  // the rows by ss_reduce_batch_kernel
 #pragma unroll
   for (int k = 0; k < kS; ++k)
-    if (n0 + k < N) ws[wo.dA + (b * D + d0 + lane) * N + n0 + k] = dA_acc[k];
+    if (n0 + k < N) ws[wo.dA + (prow * D + d0 + lane) * N + n0 + k] = dA_acc[k];
   // dD / ddelta_bias: the 4 threads of a channel are consecutive lanes
   e_dD += dpp_mov<kDppQuadXor1>(e_dD);
   e_dD += dpp_mov<kDppQuadXor2>(e_dD);
   e_dbias += dpp_mov<kDppQuadXor1>(e_dbias);
   e_dbias += dpp_mov<kDppQuadXor2>(e_dbias);
   if (eq == 0) {
-    ws[wo.dD + b * D + d0 + er] = e_dD;
-    ws[wo.dbias + b * D + d0 + er] = e_dbias;
+    ws[wo.dD + prow * D + d0 + er] = e_dD;
+    ws[wo.dbias + prow * D + d0 + er] = e_dbias;
+  }
+}
+
+// Split of L, adjoint summaries: for each segment s >= 1 and state n, the
+// adjoint it carries out of its first step when it starts from zero at its
+// last step, g <- A_bar_t (C_t dy_t + g) with dy = dout silu(z) (the recurrence
+// of the kernel above without the states), and the segment's sum of delta'.
+// One thread per (segment, b, d, n), 16 consecutive lanes per channel (lanes
+// past d_state idle); 8 steps per 16-byte (bf16) or 32-byte (fp32) load.
+template <typename IT>
+__device__ __forceinline__ void ld8_f32(const IT* p, float* o) {
+  if constexpr (sizeof(IT) == 4) {
+    raw_to_f32<IT>(*reinterpret_cast<const uint4*>(p), o);
+    raw_to_f32<IT>(*reinterpret_cast<const uint4*>(p + 4), o + 4);
+  } else {
+    raw_to_f32<IT>(*reinterpret_cast<const uint4*>(p), o);
+  }
+}
+
+template <typename IT, bool kSP, bool kZ>
+__global__ void __launch_bounds__(256)
+ssf_bwd_adj_summary_kernel(const lrnnx_selective_scan_args a, const int64_t seg_steps, const int n_seg, float* ws,
+                           const SSBwdWs wo) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t B = a.batch, D = a.dim, L = a.seqlen;
+  const int N = (int)a.dstate;
+  if (i >= (int64_t)(n_seg - 1) * B * D * 16) return;
+  const int n = (int)(i & 15);
+  const int64_t d = (i >> 4) % D, b = ((i >> 4) / D) % B, s = (i >> 4) / (B * D) + 1;
+  const bool on = n < N;
+  const int64_t grp = d / (D / a.n_groups);
+  const int64_t t0 = s * seg_steps, t1 = t0 + seg_steps < L ? t0 + seg_steps : L;  // multiples of 8
+  const float a2 = on ? static_cast<const float*>(a.A.ptr)[d * a.A.s0 + n * a.A.s1] * kLog2e : 0.f;
+  const float bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[d * a.delta_bias.s0] : 0.f;
+  const IT* pd = static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d * a.delta.s1;
+  const IT* pdo = static_cast<const IT*>(a.dout.ptr) + b * a.dout.s0 + d * a.dout.s1;
+  const IT* pz = kZ ? static_cast<const IT*>(a.z.ptr) + b * a.z.s0 + d * a.z.s1 : nullptr;
+  const IT* pc = static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1 + (on ? n : 0) * a.C.s2;
+  float g = 0.f, ssum = 0.f;
+  for (int64_t tb = t1 - 8; tb >= t0; tb -= 8) {
+    float vd[8], vdo[8], vz[8], vc[8];
+    ld8_f32<IT>(pd + tb, vd);
+    ld8_f32<IT>(pdo + tb, vdo);
+    if constexpr (kZ) ld8_f32<IT>(pz + tb, vz);
+    ld8_f32<IT>(pc + tb, vc);
+#pragma unroll
+    for (int j = 7; j >= 0; --j) {
+      float dl = vd[j] + bias;
+      if constexpr (kSP) dl = ssf::softplus20_fast(dl);
+      float dy = vdo[j];
+      if constexpr (kZ) dy *= vz[j] * ssf::sigmoidf_fast(vz[j]);
+      ssum += dl;
+      g = __builtin_amdgcn_exp2f(dl * a2) * fmaf(dy, vc[j], g);
+    }
+  }
+  if (on) ws[wo.g_loc + ((s * B + b) * N + n) * D + d] = g;
+  if (n == 0) ws[wo.dsum + (s * B + b) * D + d] = ssum;
+}
+
+// Split of L, adjoint chain (right to left) per (b, n, d): the adjoint entering
+// segment S-1 is 0; entering segment s it is
+// exp(A sum delta'(s + 1)) g_in(s + 1) + g_loc(s + 1).
+template <typename IT>  // one instantiation per unit that launches it
+__global__ void __launch_bounds__(256)
+ssf_bwd_adj_chain_kernel(const lrnnx_selective_scan_args a, const int n_seg, float* ws, const SSBwdWs wo) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (b, n, d)
+  const int64_t B = a.batch, D = a.dim, N = a.dstate;
+  if (i >= B * N * D) return;
+  const int64_t d = i % D, n = (i / D) % N, b = i / (D * N);
+  const float a2 = static_cast<const float*>(a.A.ptr)[d * a.A.s0 + n * a.A.s1] * kLog2e;
+  float gi = 0.f;
+  ws[wo.g_init + (((int64_t)(n_seg - 1) * B + b) * N + n) * D + d] = 0.f;
+  for (int s = n_seg - 2; s >= 0; --s) {
+    const int64_t r = (int64_t)(s + 1) * B + b;
+    gi = fmaf(__builtin_amdgcn_exp2f(a2 * ws[wo.dsum + r * D + d]), gi, ws[wo.g_loc + (r * N + n) * D + d]);
+    ws[wo.g_init + (((int64_t)s * B + b) * N + n) * D + d] = gi;
   }
 }
 
@@ -378,19 +459,44 @@ inline bool ssf_bwd_eligible(const lrnnx_selective_scan_args& a) {
          rows_aligned<IT>(a.ddelta, false) && rows_aligned<IT>(a.dz, false);
 }
 
+// Segments of the backward's split of L (1: no split): the forward's rule,
+// from shapes and options only, so that the workspace size and the launch agree.
+template <typename IT>
+inline int64_t ssf_bwd_segs(const lrnnx_selective_scan_args& a) {
+  if (!ssf::shape_ok<IT>(a, ssf::kCk)) return 1;
+  const int64_t steps = ssf::seg_steps(a);
+  return steps ? ssf::n_segs(a, steps) : 1;
+}
+
+template <typename IT, bool kSP, bool kZ>
+inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
+                             const float* ckp, int64_t seg_steps, hipStream_t st) {
+  const int64_t S = wo.S, B = a.batch, D = a.dim, N = a.dstate;
+  const int64_t seg_tiles = S > 1 ? seg_steps / ssf::kCk : a.seqlen / ssf::kCk;
+  if (S > 1) {
+    const int64_t nsum = (S - 1) * B * D * 16, nch = B * N * D;
+    hipLaunchKernelGGL((ssf_bwd_adj_summary_kernel<IT, kSP, kZ>), dim3((unsigned)((nsum + 255) / 256)), dim3(256), 0,
+                       st, a, seg_steps, (int)S, ws, wo);
+    hipLaunchKernelGGL(ssf_bwd_adj_chain_kernel<IT>, dim3((unsigned)((nch + 255) / 256)), dim3(256), 0, st, a, (int)S,
+                       ws, wo);
+  }
+  const dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch, (unsigned)S);
+  hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ>), grid, dim3(ssf::kNT), 0, st, a, g.n_ck, ws, wo, ckp, seg_tiles);
+}
+
 template <typename IT>
 inline hipError_t ssf_bwd_launch(const lrnnx_selective_scan_args& a, float* ws, const float* ckp, hipStream_t st) {
   const SSGeom g = ss_geom(a);
-  const SSBwdWs wo = ss_bwd_ws(a, g, a.ckpt == nullptr);
-  dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch);
-  dim3 block(ssf::kNT);
+  const int64_t S = ssf_bwd_segs<IT>(a);
+  const SSBwdWs wo = ss_bwd_ws(a, g, a.ckpt == nullptr, S);
+  const int64_t steps = S > 1 ? ssf::seg_steps(a) : 0;
   const bool z = a.z.ptr != nullptr;
   if (a.delta_softplus) {
-    if (z) hipLaunchKernelGGL((ssf_bwd_kernel<IT, true, true>), grid, block, 0, st, a, g.n_ck, ws, wo, ckp);
-    else hipLaunchKernelGGL((ssf_bwd_kernel<IT, true, false>), grid, block, 0, st, a, g.n_ck, ws, wo, ckp);
+    if (z) ssf_bwd_launch_t<IT, true, true>(a, g, ws, wo, ckp, steps, st);
+    else ssf_bwd_launch_t<IT, true, false>(a, g, ws, wo, ckp, steps, st);
   } else {
-    if (z) hipLaunchKernelGGL((ssf_bwd_kernel<IT, false, true>), grid, block, 0, st, a, g.n_ck, ws, wo, ckp);
-    else hipLaunchKernelGGL((ssf_bwd_kernel<IT, false, false>), grid, block, 0, st, a, g.n_ck, ws, wo, ckp);
+    if (z) ssf_bwd_launch_t<IT, false, true>(a, g, ws, wo, ckp, steps, st);
+    else ssf_bwd_launch_t<IT, false, false>(a, g, ws, wo, ckp, steps, st);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
