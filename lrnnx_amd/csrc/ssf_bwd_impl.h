@@ -44,12 +44,17 @@
 namespace lrnnx {
 
 namespace ssf {
-// 1 - exp(-d) for d = softplus(x) >= 0, i.e. sigmoid(x); 4-term series below
-// 1/32 so that small d keeps its relative precision
-__device__ __forceinline__ float sigmoid_from_softplus(float d) {
-  const float small = d * fmaf(d, fmaf(d, fmaf(d, -0.041666668f, 0.16666667f), -0.5f), 1.f);
-  const float big = 1.f - __builtin_amdgcn_exp2f(-d * kLog2e);
-  return d < 0.03125f ? small : big;
+// softplus20_fast(x) and its derivative from the same exp: sigmoid(x) =
+// e / (1 + e), e = exp(x) (relative precision kept for small e), and 1 past
+// the threshold 20, where softplus is the identity
+__device__ __forceinline__ float softplus20_sig(float x, float& sg) {
+  const float e = __builtin_amdgcn_exp2f(x * kLog2e);
+  const float t = 1.f + e;
+  const float small = e * fmaf(e, fmaf(e, fmaf(e, -0.25f, 0.33333334f), -0.5f), 1.f);
+  const float big = __builtin_amdgcn_logf(t) * kLn2;
+  const float r = e < 0.03125f ? small : big;
+  sg = x > 20.f ? 1.f : e * __builtin_amdgcn_rcpf(t);
+  return x > 20.f ? x : r;
 }
 }  // namespace ssf
 
@@ -78,6 +83,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   __shared__ __attribute__((aligned(16))) float s_dl[kOp];             // [g][lane][4] delta'
   __shared__ __attribute__((aligned(16))) float s_u[kOp];              // u
   __shared__ __attribute__((aligned(16))) float s_dy[kOp];             // dout silu(z)
+  __shared__ __attribute__((aligned(16))) float s_sg[kSP ? kOp : 4];   // sigmoid(delta + bias)
   __shared__ __attribute__((aligned(16))) float s_B[kT * 16];          // [t][n]
   __shared__ __attribute__((aligned(16))) float s_C[kT * 16];
   __shared__ __attribute__((aligned(16))) float s_P1[kNW * kOp];       // [w][g][lane][4] sum_k dh B
@@ -158,11 +164,11 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     raw4_to_f32<IT>(s_raw_u + ro, vu);
     raw4_to_f32<IT>(s_raw_d + ro, vd);
     raw4_to_f32<IT>(s_raw_do + ro, vdo);
-    float dy[4];
+    float dy[4], sg[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float x = vd[i] + e_bias;
-      vd[i] = kSP ? softplus20_fast(x) : x;
+      vd[i] = kSP ? softplus20_sig(x, sg[i]) : x;
       dy[i] = vdo[i];
     }
     if constexpr (kZ) {
@@ -182,6 +188,8 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     *reinterpret_cast<float4*>(&s_dl[o]) = make_float4(vd[0], vd[1], vd[2], vd[3]);
     *reinterpret_cast<float4*>(&s_u[o]) = make_float4(vu[0], vu[1], vu[2], vu[3]);
     *reinterpret_cast<float4*>(&s_dy[o]) = make_float4(dy[0], dy[1], dy[2], dy[3]);
+    // read back by this thread only, in the epilogue
+    if constexpr (kSP) *reinterpret_cast<float4*>(&s_sg[o]) = make_float4(sg[0], sg[1], sg[2], sg[3]);
     // B / C rows, transposed to step-major: threads [0, 64) B, [64, 128) C,
     // 4 steps of one state each; states >= N are zero
     if (tid < 2 * 16 * 4) {
@@ -214,12 +222,17 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     const float p1[4] = {P1.x, P1.y, P1.z, P1.w}, p2[4] = {P2.x, P2.y, P2.z, P2.w};
     const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, uu[4] = {u4.x, u4.y, u4.z, u4.w};
     const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+    float sg[4] = {1.f, 1.f, 1.f, 1.f};
+    if constexpr (kSP) {
+      const float4 sg4 = *reinterpret_cast<const float4*>(&s_sg[o]);
+      sg[0] = sg4.x; sg[1] = sg4.y; sg[2] = sg4.z; sg[3] = sg4.w;
+    }
     float du[4], dd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       du[i] = fmaf(dl[i], p1[i], e_D * dy[i]);
       const float ddl = fmaf(uu[i], p1[i], kLn2 * p2[i]);
-      dd[i] = kSP ? ddl * sigmoid_from_softplus(dl[i]) : ddl;
+      dd[i] = kSP ? ddl * sg[i] : ddl;
       e_dD = fmaf(dy[i], uu[i], e_dD);
       e_dbias += dd[i];
     }
