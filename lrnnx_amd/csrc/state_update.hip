@@ -68,7 +68,7 @@ __global__ void __launch_bounds__(256) state_update_rows(const lrnnx_state_updat
   // the kSplit lanes of a row sit in one quad and share d, so they leave together
   if (d >= a.dim) return;
   const int64_t b = blockIdx.y, hd = blockIdx.z;
-  const int64_t g = hd / (a.nheads / a.ngroups);
+  const int64_t g = (int)hd / ((int)a.nheads / (int)a.ngroups);
   const int64_t sb = a.state_batch_indices ? (int64_t)a.state_batch_indices[b] : b;
   ST* __restrict__ state = static_cast<ST*>(a.state) + sb * a.state_s0 + hd * a.state_s1 + d * a.state_s2 + part * kV;
   const float* __restrict__ A = static_cast<const float*>(a.A) + hd * a.A_s0 + d * a.A_s1 + part * kV;
@@ -91,12 +91,20 @@ __global__ void __launch_bounds__(256) state_update_rows(const lrnnx_state_updat
     Bv[v] = to_f32(Bp[v]);
     Cv[v] = to_f32(Cp[v]);
   }
-  const float x = to_f32(static_cast<const XT*>(a.x)[b * a.x_s0 + hd * a.x_s1 + d * a.x_s2]);
+  // The optional operands are loaded with the others, unconditionally: an
+  // absent one reads this row's x (or A) entry instead and is dropped, so the
+  // row's loads all issue before the first wait.
+  const XT* xp = static_cast<const XT*>(a.x) + b * a.x_s0 + hd * a.x_s1 + d * a.x_s2;
+  const float* dtbp = a.dt_bias ? static_cast<const float*>(a.dt_bias) + hd * a.dtb_s0 + d * a.dtb_s1 : A;
+  const float* Dp = a.D ? static_cast<const float*>(a.D) + hd * a.D_s0 + d * a.D_s1 : A;
+  const XT* zp = a.z ? static_cast<const XT*>(a.z) + b * a.z_s0 + hd * a.z_s1 + d * a.z_s2 : xp;
+  const XT* dAp = a.deltaA ? static_cast<const XT*>(a.deltaA) + b * a.dA_s0 + hd * a.dA_s1 + d * a.dA_s2 : xp;
+  const float x = to_f32(*xp);
   float dt = to_f32(static_cast<const XT*>(a.dt)[b * a.dt_s0 + hd * a.dt_s1 + d * a.dt_s2]);
-  if (a.dt_bias) dt += static_cast<const float*>(a.dt_bias)[hd * a.dtb_s0 + d * a.dtb_s1];
+  const float dtb = *dtbp, Dv = *Dp, zv = to_f32(*zp), dAraw = to_f32(*dAp);
+  if (a.dt_bias) dt += dtb;
   if (a.dt_softplus) dt = softplus20(dt);
-  const float dAv =
-      a.deltaA ? to_f32(static_cast<const XT*>(a.deltaA)[b * a.dA_s0 + hd * a.dA_s1 + d * a.dA_s2]) : dt;
+  const float dAv = a.deltaA ? dAraw : dt;
   float acc = 0.f;
   {
     uint4 raw;
@@ -113,8 +121,8 @@ __global__ void __launch_bounds__(256) state_update_rows(const lrnnx_state_updat
   acc += dpp_mov<kDppQuadXor1>(acc);
   if constexpr (kSplit == 4) acc += dpp_mov<kDppQuadXor2>(acc);
   if (part != 0) return;
-  if (a.D) acc += x * static_cast<const float*>(a.D)[hd * a.D_s0 + d * a.D_s1];
-  if (a.z) acc *= silu(to_f32(static_cast<const XT*>(a.z)[b * a.z_s0 + hd * a.z_s1 + d * a.z_s2]));
+  if (a.D) acc += x * Dv;
+  if (a.z) acc *= silu(zv);
   static_cast<XT*>(a.out)[b * a.out_s0 + hd * a.out_s1 + d * a.out_s2] = from_f32<XT>(acc);
 }
 
