@@ -10,9 +10,9 @@
 //   state <- state * A_bar + B_bar * x   (stored in the state dtype, in place)
 //   out = sum_n state_n C_n (+ D x), times silu(z).
 // General kernel: one thread owns one (batch, head, channel) row of `state`;
-// consecutive threads own consecutive channels.  At d_state 16 with unit-stride
-// aligned rows a row is split over 2 (16-bit state) or 4 (fp32) lanes of one
-// quad, each reading and writing 16 bytes after all its operands are loaded.
+// consecutive threads own consecutive channels.  At d_state 16, 32 or 64 with
+// unit-stride aligned rows a row is split over 2 to 16 adjacent lanes, each
+// reading and writing 16 bytes after all its operands are loaded.
 #include "common.h"
 
 namespace lrnnx {
@@ -52,20 +52,21 @@ __device__ __forceinline__ void discretize1(float An, float Bn, float dt, float 
 
 // Row-at-once update for d_state == kN with unit-stride, 16-byte aligned state
 // / A rows and unit-stride B / C (checked on the host).  A row is split over
-// kSplit = kN / kV adjacent lanes, each owning kV entries = 16 bytes of state,
-// so every state access of a wave is one contiguous 1 KiB; the lanes' partial
-// outputs are summed with quad DPP.  All types are compile-time (ST: state;
+// kSplit = kN / kV adjacent lanes (2 to 16, an aligned group inside one 16-lane
+// DPP row), each owning kV entries = 16 bytes of state, so every state access
+// of a wave is one contiguous 1 KiB; the lanes' partial outputs are summed with
+// DPP (quad xor 1, xor 2, then half-row and row mirrors).  All types are compile-time (ST: state;
 // XT: x, dt, z, deltaA, B, C and out), and a lane loads all its operands
 // before it computes and stores, so a row costs one round trip to memory.
 template <typename ST, typename XT, int kMethod, int kN>
 __global__ void __launch_bounds__(256) state_update_rows(const lrnnx_state_update_args a) {
   constexpr int kV = 16 / sizeof(ST);   // state entries per lane (one 16-byte access)
   constexpr int kSplit = kN / kV;       // lanes per row: 2 (16-bit state) or 4 (fp32)
-  static_assert(kSplit == 2 || kSplit == 4, "a row spans 2 or 4 lanes of one quad");
+  static_assert(kSplit == 2 || kSplit == 4 || kSplit == 8 || kSplit == 16, "a row spans 2 to 16 lanes");
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t d = t / kSplit;
   const int part = (int)(t % kSplit);
-  // the kSplit lanes of a row sit in one quad and share d, so they leave together
+  // the kSplit lanes of a row are one aligned group and share d, so they leave together
   if (d >= a.dim) return;
   const int64_t b = blockIdx.y, hd = blockIdx.z;
   const int64_t g = (int)hd / ((int)a.nheads / (int)a.ngroups);
@@ -118,8 +119,12 @@ __global__ void __launch_bounds__(256) state_update_rows(const lrnnx_state_updat
     }
     *reinterpret_cast<uint4*>(state) = raw;
   }
+  // every lane of the group ends with the group's sum: xor 1 and xor 2 sum a
+  // quad, the half-row mirror pairs quads 0 / 1, the row mirror halves 0 / 1
   acc += dpp_mov<kDppQuadXor1>(acc);
-  if constexpr (kSplit == 4) acc += dpp_mov<kDppQuadXor2>(acc);
+  if constexpr (kSplit >= 4) acc += dpp_mov<kDppQuadXor2>(acc);
+  if constexpr (kSplit >= 8) acc += dpp_mov<kDppRowHalfMirror>(acc);
+  if constexpr (kSplit >= 16) acc += dpp_mov<kDppRowMirror>(acc);
   if (part != 0) return;
   if (a.D) acc += x * Dv;
   if (a.z) acc *= silu(zv);
@@ -165,37 +170,47 @@ __global__ void __launch_bounds__(256) state_update_kernel(const lrnnx_state_upd
   }
 }
 
-// the d_state == 16 fast path's layout requirements
+// the row-at-once kernel's layout requirements (d_state 16, 32 or 64)
 template <typename ST>
 static bool su_rows_ok(const lrnnx_state_update_args& a) {
   const int64_t es = sizeof(ST);
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  return a.dstate == 16 && a.state_s3 == 1 && a.A_s2 == 1 && a.B_s2 == 1 && a.C_s2 == 1 && al16(a.state) &&
+  return (a.dstate == 16 || a.dstate == 32 || a.dstate == 64) && a.state_s3 == 1 && a.A_s2 == 1 && a.B_s2 == 1 && a.C_s2 == 1 && al16(a.state) &&
          al16(a.A) && (a.state_s0 * es) % 16 == 0 && (a.state_s1 * es) % 16 == 0 && (a.state_s2 * es) % 16 == 0 &&
          (a.A_s0 * 4) % 16 == 0 && (a.A_s1 * 4) % 16 == 0;
+}
+
+// Row-at-once launch at d_state kN; false when the x / B / C type has no
+// instantiation (x / B / C of the state's own type, or 16-bit with an fp32 state).
+template <typename ST, int kMethod, int kN>
+static bool su_rows_launch(const lrnnx_state_update_args& a, dim3 grid, hipStream_t st) {
+  // kSplit lanes per row (kN entries, 16 / sizeof(ST) per lane)
+  constexpr int64_t kSplit = kN / (16 / sizeof(ST));
+  const dim3 rg((unsigned)((a.dim * kSplit + 255) / 256), grid.y, grid.z);
+  if (a.x_type == a.state_type) {
+    hipLaunchKernelGGL((state_update_rows<ST, ST, kMethod, kN>), rg, dim3(256), 0, st, a);
+    return true;
+  }
+  if constexpr (sizeof(ST) == 4) {
+    if (a.x_type == LRNNX_BF16) {
+      hipLaunchKernelGGL((state_update_rows<ST, bf16, kMethod, kN>), rg, dim3(256), 0, st, a);
+      return true;
+    }
+    if (a.x_type == LRNNX_F16) {
+      hipLaunchKernelGGL((state_update_rows<ST, f16, kMethod, kN>), rg, dim3(256), 0, st, a);
+      return true;
+    }
+  }
+  return false;
 }
 
 template <typename ST, int kMethod>
 static void su_launch(const lrnnx_state_update_args& a, dim3 grid, hipStream_t st) {
   if (su_rows_ok<ST>(a) && a.bc_type == a.x_type) {
-    // kSplit lanes per row (16 entries of 16 / sizeof(ST) per lane)
-    constexpr int64_t kSplit = 16 / (16 / sizeof(ST));
-    const dim3 rg((unsigned)((a.dim * kSplit + 255) / 256), grid.y, grid.z);
-    // x / B / C types of the row-at-once kernel: the state's own, or 16-bit with an fp32 state
-    if (a.x_type == a.state_type) {
-      hipLaunchKernelGGL((state_update_rows<ST, ST, kMethod, 16>), rg, dim3(256), 0, st, a);
-      return;
-    }
-    if constexpr (sizeof(ST) == 4) {
-      if (a.x_type == LRNNX_BF16) {
-        hipLaunchKernelGGL((state_update_rows<ST, bf16, kMethod, 16>), rg, dim3(256), 0, st, a);
-        return;
-      }
-      if (a.x_type == LRNNX_F16) {
-        hipLaunchKernelGGL((state_update_rows<ST, f16, kMethod, 16>), rg, dim3(256), 0, st, a);
-        return;
-      }
-    }
+    const bool done = a.dstate == 16   ? su_rows_launch<ST, kMethod, 16>(a, grid, st)
+                      : a.dstate == 32 ? su_rows_launch<ST, kMethod, 32>(a, grid, st)
+                                       : su_rows_launch<ST, kMethod, 64>(a, grid, st);
+    if (done) return;
   }
   hipLaunchKernelGGL((state_update_kernel<ST, kMethod>), grid, dim3(256), 0, st, a);
 }
