@@ -140,13 +140,22 @@ __global__ void __launch_bounds__(256) state_update_kernel(const lrnnx_state_upd
   const int64_t g = hd / (a.nheads / a.ngroups);
   const int64_t sb = a.state_batch_indices ? (int64_t)a.state_batch_indices[b] : b;
   ST* __restrict__ state = static_cast<ST*>(a.state) + sb * a.state_s0 + hd * a.state_s1 + d * a.state_s2;
-  const float x = ld_any(a.x, b * a.x_s0 + hd * a.x_s1 + d * a.x_s2, a.x_type);
-  float dt = ld_any(a.dt, b * a.dt_s0 + hd * a.dt_s1 + d * a.dt_s2, a.x_type);
-  if (a.dt_bias) dt += static_cast<const float*>(a.dt_bias)[hd * a.dtb_s0 + d * a.dtb_s1];
-  if (a.dt_softplus) dt = softplus20(dt);
-  const bool has_dA = a.deltaA != nullptr;
-  const float dAv = has_dA ? ld_any(a.deltaA, b * a.dA_s0 + hd * a.dA_s1 + d * a.dA_s2, a.x_type) : dt;
   const float* __restrict__ A = static_cast<const float*>(a.A) + hd * a.A_s0 + d * a.A_s1;
+  // optional operands load with x and dt (an absent one reads x's entry or A[0]
+  // and is dropped), so none of them waits behind a branch or the state loop
+  const int64_t xi = b * a.x_s0 + hd * a.x_s1 + d * a.x_s2;
+  const float* dtbp = a.dt_bias ? static_cast<const float*>(a.dt_bias) + hd * a.dtb_s0 + d * a.dtb_s1 : A;
+  const float* Dp = a.D ? static_cast<const float*>(a.D) + hd * a.D_s0 + d * a.D_s1 : A;
+  const void* zb = a.z ? a.z : a.x;
+  const int64_t zi = a.z ? b * a.z_s0 + hd * a.z_s1 + d * a.z_s2 : xi;
+  const void* dAb = a.deltaA ? a.deltaA : a.x;
+  const int64_t dAi = a.deltaA ? b * a.dA_s0 + hd * a.dA_s1 + d * a.dA_s2 : xi;
+  const float x = ld_any(a.x, xi, a.x_type);
+  float dt = ld_any(a.dt, b * a.dt_s0 + hd * a.dt_s1 + d * a.dt_s2, a.x_type);
+  const float dtb = *dtbp, Dv = *Dp, zv = ld_any(zb, zi, a.x_type), dAraw = ld_any(dAb, dAi, a.x_type);
+  if (a.dt_bias) dt += dtb;
+  if (a.dt_softplus) dt = softplus20(dt);
+  const float dAv = a.deltaA ? dAraw : dt;
   float acc = 0.f;
 #pragma unroll 4
   for (int64_t n = 0; n < a.dstate; ++n) {
@@ -160,8 +169,8 @@ __global__ void __launch_bounds__(256) state_update_kernel(const lrnnx_state_upd
     state[si] = stored;
     acc = fmaf(to_f32(stored), Cn, acc);
   }
-  if (a.D) acc += x * static_cast<const float*>(a.D)[hd * a.D_s0 + d * a.D_s1];
-  if (a.z) acc *= silu(ld_any(a.z, b * a.z_s0 + hd * a.z_s1 + d * a.z_s2, a.x_type));
+  if (a.D) acc += x * Dv;
+  if (a.z) acc *= silu(zv);
   const int64_t oi = b * a.out_s0 + hd * a.out_s1 + d * a.out_s2;
   switch (a.x_type) {
     case LRNNX_BF16: static_cast<bf16*>(a.out)[oi] = from_f32<bf16>(acc); break;
