@@ -19,6 +19,13 @@ bool fast_paths_enabled() {
   const char* v = getenv("LRNNX_SCAN_GENERIC");
   return !(v && v[0] && v[0] != '0');
 }
+// LRNNX_SCAN_NO_SPLIT=1 keeps the fast paths from splitting L on small grids,
+// so that tests can run the unsplit schedule at shapes the oracle finishes
+// quickly.
+bool l_split_enabled() {
+  const char* v = getenv("LRNNX_SCAN_NO_SPLIT");
+  return !(v && v[0] && v[0] != '0');
+}
 
 hipError_t ss_fwd_mamba_f32(const lrnnx_selective_scan_args&, hipStream_t);
 hipError_t ss_fwd_mamba_bf16(const lrnnx_selective_scan_args&, hipStream_t);

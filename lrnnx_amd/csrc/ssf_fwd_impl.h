@@ -382,8 +382,11 @@ inline bool ssf_fwd_eligible(const lrnnx_selective_scan_args& a) {
   return ssf::rows_aligned<IT>(a.out, false) && ssf::rows_aligned<IT>(a.out_z, false);
 }
 
+bool l_split_enabled();  // capi.hip: LRNNX_SCAN_NO_SPLIT
+
 namespace ssf {
-// Steps per segment of the L split: 0 (no split) for grids of more than 128
+// Steps per segment of the L split: 0 (no split) when the split is switched
+// off (l_split_enabled) or for grids of more than 128
 // workgroups (B * D / 64; half the CUs), where the summary pass costs more than
 // the added parallelism gains (measured: 192 workgroups ran 16 % slower
 // split), else the shortest power of two >= 128 steps that keeps the grid at
@@ -391,7 +394,7 @@ namespace ssf {
 // segment boundary and are multiples of every tile length.
 inline int64_t seg_steps(const lrnnx_selective_scan_args& a) {
   const int64_t wgs = (a.dim / kWave) * a.batch;
-  if (wgs > 128) return 0;
+  if (wgs > 128 || !l_split_enabled()) return 0;
   int64_t steps = 128;
   while (steps < a.seqlen && wgs * ((a.seqlen + steps - 1) / steps) > 512) steps *= 2;
   return steps < a.seqlen ? steps : 0;

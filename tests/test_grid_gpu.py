@@ -1,0 +1,162 @@
+"""GPU parity at the grids the bench times, against the float64 C oracle
+(oracle/selective_scan_ref.c, pinned in tests/test_oracle.py against fp64
+autograd of the restated selective_scan_ref, lrnnx/ops/selective_scan.py:
+200-360).
+
+* Config 3 (B=8, D=4096, L=4096, N=16, G=1, bf16; 512 workgroups) and
+  config 2 (B=8, D=1536, L=2048; 192 workgroups) in full: every output and
+  gradient of ``selective_scan_fn`` on every element.
+* Grids just above the 128-workgroup split limit (unsplit fast kernels at
+  moderate L): bf16 B=3 D=2816 L=1024 and fp32 B=2 D=4160 L=512.
+* The small-grid split of L against the unsplit schedule
+  (LRNNX_SCAN_NO_SPLIT=1) at B=1 D=64 L=4160, both against the oracle.
+* The binding's own call sequence ``selective_scan_cuda.fwd`` -> ``bwd(x)``
+  (the backward rebuilds its checkpoints: no checkpoint buffer is passed).
+
+Tolerance, elementwise |got - ref| <= atol + rtol |ref|:
+  fp32 I/O: north_star's bound as stated, rtol 1e-4 and an absolute atol of
+  1e-5, on every output and every gradient (sums over batch and length
+  included);
+  bf16 I/O (fp32 state): rtol 2e-2, atol 1e-2 max|ref| of the tensor (the
+  outputs are rounded to bf16, a relative step of 2^-8).
+Each comparison also prints (and with $LRNNX_PARITY_REPORT set, records) the
+max abs / rel error and the count of elements outside the fp32 bound.
+"""
+
+import pytest
+import torch
+
+import bench
+from lrnnx_amd import selective_scan_cuda as ssc
+from lrnnx_amd import selective_scan_fn
+from oracle import fast as OF
+from oracle import scan_ref as R
+from tests.parity import close, close_dev, oracle_selective, to_dev
+
+pytestmark = pytest.mark.gpu
+
+_REDUCED = ("dA", "dD", "ddelta_bias", "dB", "dC")
+
+
+def _tol(itype):
+    """(rtol, atol relative to max|ref|, absolute atol)"""
+    return (1e-4, 0.0, 1e-5) if itype == torch.float32 else (2e-2, 1e-2, 0.0)
+
+
+def _gpu_inputs(dev, Bt, D, L, N, seed, itype):
+    inp = bench.make_cfg3(dev, torch, None, Bt, D, L, N, seed=seed, io=itype)
+    return inp
+
+
+def _oracle(inp):
+    return OF.selective_scan_mamba(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                                   inp["delta_bias"], True, inp["dout"])
+
+
+def _run_fn(inp):
+    """selective_scan_fn fwd + bwd (the autograd drop-in path)."""
+    lv = {k: inp[k].clone().requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")}
+    out, last = selective_scan_fn(lv["u"], lv["delta"], lv["A"], lv["B"], lv["C"], lv["D"], lv["z"],
+                                  lv["delta_bias"], None, True, True, "mamba")
+    out.backward(inp["dout"])
+    torch.cuda.synchronize()
+    res = {"out": out.detach(), "last_state": last.detach()}
+    for k, gk in (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC"), ("D", "dD"),
+                  ("z", "dz"), ("delta_bias", "ddelta_bias")):
+        res[gk] = lv[k].grad
+    return res
+
+
+def _compare(got, ref, itype):
+    rt, at, aa = _tol(itype)
+    for name in ("out", "last_state", "du", "ddelta", "dz", "dA", "dB", "dC", "dD", "ddelta_bias"):
+        close_dev(name, got[name], ref[name], rt, at, aa)
+
+
+@pytest.mark.parametrize("case", [
+    # (name, B, D, L, seed, itype): configs 2 and 3 of the benchmark, then grids just above 128 workgroups
+    ("cfg3", 8, 4096, 4096, 3, torch.bfloat16),
+    ("cfg2", 8, 1536, 2048, 2, torch.bfloat16),
+    ("grid132", 3, 2816, 1024, 7, torch.bfloat16),
+    ("grid130_f32", 2, 4160, 512, 8, torch.float32),
+], ids=lambda c: c[0])
+def test_full_grid_vs_oracle(dev, case):
+    name, Bt, D, L, seed, itype = case
+    print(f"[{name}] B={Bt} D={D} L={L} N=16 {itype} seed={seed}: GPU fwd+bwd", flush=True)
+    inp = _gpu_inputs(dev, Bt, D, L, 16, seed, itype)
+    got = _run_fn(inp)
+    print(f"[{name}] oracle (C, fp64, {OF.lib().lrnnx_oracle_ss_threads()} threads)", flush=True)
+    ref = _oracle(inp)
+    _compare(got, ref, itype)
+
+
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+def test_small_grid_split_and_unsplit_vs_oracle(dev, monkeypatch, itype):
+    """B=1, D=64 is one workgroup: by default both directions split L into
+    segments; LRNNX_SCAN_NO_SPLIT=1 runs the unsplit kernels.  Both schedules
+    match the oracle, and each other."""
+    inp = _gpu_inputs(dev, 1, 64, 4160, 16, 21, itype)
+    ref = _oracle(inp)
+    res = {}
+    for mode in ("split", "unsplit"):
+        monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", "1" if mode == "unsplit" else "0")
+        print(f"[{mode}] {itype}", flush=True)
+        res[mode] = _run_fn(inp)
+        _compare(res[mode], ref, itype)
+    for name in res["split"]:
+        rt, at, aa = _tol(itype)
+        close_dev(f"{name} split/unsplit", res["split"][name], res["unsplit"][name].double(), rt, at, aa)
+
+
+def _binding_fwd_bwd(inp, method="mamba", softplus=True):
+    """selective_scan_cuda.fwd then bwd with the forward's x and out, as the
+    reference's SelectiveScanFn calls them (selective_scan.py:70-82, :116-135)."""
+    u, dl, A, B, C, D, z, db = (inp.get(k) for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias"))
+    r = ssc.fwd(u, dl, A, B, C, D, z, db, None, softplus, method)
+    out, x = r[0], r[1]
+    g = ssc.bwd(u, dl, A, B, C, D, z, db, None, inp["dout"], x, out, None, softplus, False, method)
+    torch.cuda.synchronize()
+    res = {"out": r[2] if z is not None else out, "last_state": x[:, :, -1, 1::2],
+           "du": g[0], "ddelta": g[1], "dA": g[2], "dB": g[3], "dC": g[4], "dD": g[5], "ddelta_bias": g[6]}
+    if z is not None:
+        res["dz"] = g[7]
+    return res
+
+
+@pytest.mark.parametrize("case", [
+    ("small_f32", 2, 64, 512, torch.float32),
+    ("small_bf16", 2, 64, 512, torch.bfloat16),
+    ("grid132_bf16", 3, 2816, 1024, torch.bfloat16),
+    ("grid130_f32", 2, 4160, 256, torch.float32),
+], ids=lambda c: c[0])
+def test_binding_fwd_then_bwd_x_vs_oracle(dev, case):
+    """The boundary's own sequence: bwd gets x and out but no checkpoints, so
+    it rebuilds them (the path the reference's SelectiveScanFn, S7ScanFn and
+    RGLRUScanFn take after the import swap)."""
+    name, Bt, D, L, itype = case
+    inp = _gpu_inputs(dev, Bt, D, L, 16, 31, itype)
+    print(f"[{name}] fwd -> bwd(x)", flush=True)
+    got = _binding_fwd_bwd(inp)
+    ref = _oracle(inp)
+    _compare(got, ref, itype)
+
+
+@pytest.mark.parametrize("method", ["rglru", "s7"])
+def test_binding_fwd_then_bwd_x_one_state_methods(dev, method):
+    """The S7 / RG-LRU wrappers' binding calls (N = 1, constant B / C, fp32)
+    through fwd -> bwd(x), against fp64 autograd of the restated oracle."""
+    g = torch.Generator().manual_seed(41)
+    Bt, D, L = 2, 96, 700
+    inp = R.make_selective_inputs(Bt, D, L, 1, seed=41, varB=False, varC=False, has_z=False, has_D=True,
+                                  has_bias=False)
+    inp["delta"] = inp["delta"].abs() * 0.2 + 1e-3
+    if method == "rglru":
+        inp["A"] = torch.rand(D, 1, generator=g) * 0.5 + 0.45
+    dout = torch.randn(Bt, D, L, generator=g)
+    ro, rl, rg = oracle_selective(inp, method, False, None, True, dout)
+    d = to_dev(inp, dev)
+    d["dout"] = dout.to(dev)
+    got = _binding_fwd_bwd(d, method, softplus=False)
+    close("out", got["out"], ro, 1e-4, 1e-5)
+    for k, gk in (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC"), ("D", "dD")):
+        close(gk, got[gk], rg[k], 1e-4, 1e-4 if gk in _REDUCED else 1e-5)

@@ -559,3 +559,69 @@ def test_rglru_inner_ref_vs_scalar_loop():
             for o in range(dm):
                 ref = sum(float(Wo[o, k]) * y[k] for k in range(d)) + float(bo[o])
                 assert abs(ref - float(out[bb, t, o])) < 1e-10
+
+
+# ----------------------------------------------------------------------------
+# The float64 C restatement (oracle/selective_scan_ref.c via oracle/fast.py),
+# pinned against fp64 autograd of selective_scan_ref (pinned above by brute
+# force, closed forms and gradcheck) before the GPU tests use it at full shapes.
+# ----------------------------------------------------------------------------
+
+_FAST_CASES = [
+    dict(),
+    dict(groups=2),
+    dict(varB=False),
+    dict(varC=False),
+    dict(varB=False, varC=False),
+    dict(has_z=False),
+    dict(has_D=False, has_bias=False),
+]
+
+
+@pytest.mark.parametrize("kw", _FAST_CASES)
+@pytest.mark.parametrize("softplus", [True, False])
+def test_fast_oracle_vs_autograd(kw, softplus):
+    from oracle import fast
+    from tests.parity import oracle_selective
+
+    b, d, L, n = 2, 8, 37, 5
+    inp = R.make_selective_inputs(b, d, L, n, seed=11, **kw)
+    if not softplus:  # the time step must be positive without softplus, as the callers guarantee
+        inp["delta"] = inp["delta"].abs() * 0.3 + 1e-3
+        if inp.get("delta_bias") is not None:
+            inp["delta_bias"] = inp["delta_bias"].abs() * 0.01
+    # a few pre-activations above softplus' threshold (identity there, derivative 1)
+    inp["delta"][0, 0, :3] = 25.0
+    dout = torch.randn(b, d, L, generator=torch.Generator().manual_seed(12))
+    o, last, g = oracle_selective(inp, "mamba", softplus, None, True, dout)
+    r = fast.selective_scan_mamba(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                                  inp["delta_bias"], softplus, dout)
+    assert torch.allclose(r["out"], o, rtol=1e-12, atol=1e-12)
+    assert torch.allclose(r["last_state"], last, rtol=1e-12, atol=1e-12)
+    names = {"u": "du", "delta": "ddelta", "A": "dA", "B": "dB", "C": "dC", "D": "dD", "z": "dz",
+             "delta_bias": "ddelta_bias"}
+    for k, gk in names.items():
+        if k in g:
+            assert r[gk].shape == g[k].shape, gk
+            assert torch.allclose(r[gk], g[k], rtol=1e-10, atol=1e-11), gk
+
+
+def test_fast_oracle_forward_only_and_threads():
+    """dout=None runs the forward only; the result does not depend on the
+    number of threads beyond the order of the final fp64 sums."""
+    from oracle import fast
+
+    inp = R.make_selective_inputs(3, 16, 64, 4, seed=13, groups=4)
+    dout = torch.randn(3, 16, 64, generator=torch.Generator().manual_seed(14))
+    f = fast.selective_scan_mamba(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                                  inp["delta_bias"], True, None, want_out_pre=True)
+    assert set(f) == {"out", "last_state", "out_pre"}
+    assert torch.allclose(f["out"], f["out_pre"] * F.silu(inp["z"].double()), rtol=1e-14, atol=1e-14)
+    r1 = fast.selective_scan_mamba(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                                   inp["delta_bias"], True, dout, threads=1)
+    r4 = fast.selective_scan_mamba(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                                   inp["delta_bias"], True, dout, threads=4)
+    assert torch.equal(r1["out"], f["out"])
+    for k in r1:
+        assert torch.allclose(r1[k], r4[k], rtol=1e-13, atol=1e-13), k
+

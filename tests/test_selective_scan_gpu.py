@@ -70,9 +70,16 @@ def test_mamba_fp32_var_const(dev, varB, varC):
     _run(dev, 2, 70, 96, 16, varB=varB, varC=varC)
 
 
-@pytest.mark.parametrize("N", [1, 3, 8, 16, 33, 64])
+@pytest.mark.parametrize("N", [1, 3, 8, 16, 33, 64, 100, 128, 256])
 def test_mamba_fp32_dstate(dev, N):
+    # N > 64 runs the 32-states-per-wave instantiation (the reference accepts
+    # N <= 256; its LM tests use d_state 128)
     _run(dev, 1, 64, 80, N)
+
+
+@pytest.mark.parametrize("N", [128, 256])
+def test_mamba_bf16_large_dstate(dev, N):
+    _run(dev, 2, 64, 96, N, itype=torch.bfloat16, seed=N)
 
 
 @pytest.mark.parametrize("flags", [dict(has_z=False), dict(has_D=False), dict(has_bias=False), dict(softplus=False)])
