@@ -101,6 +101,19 @@ int64_t lrnnx_selective_scan_workspace_size(const lrnnx_selective_scan_args *a, 
  * Replaces selective_scan_fwd (selective_scan_cpu.cpp:263-421). */
 int lrnnx_selective_scan_fwd(const lrnnx_selective_scan_args *a, void *stream);
 
+/* Forward that allocates nothing and takes no workspace.  No counterpart in
+ * the reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, serving loops, harnesses that forbid allocation) and still want the
+ * small-grid split of L.  Same arguments and results as
+ * lrnnx_selective_scan_fwd; `workspace` / `workspace_bytes` are ignored and
+ * the split's segment summaries go to a scratch array in device memory that
+ * the library holds per GPU (LRNNX_FWD_NOALLOC_SCRATCH_BYTES: enough for
+ * every call the split covers; a larger need is rejected).  Calls on one GPU
+ * share that array, so calls that overlap on one GPU (concurrent streams)
+ * race; nothing in it needs to start at zero. */
+int lrnnx_selective_scan_fwd_noalloc(const lrnnx_selective_scan_args *a, void *stream);
+#define LRNNX_FWD_NOALLOC_SCRATCH_BYTES 4456448
+
 /* Backward.  Needs `ckpt` from a forward over the same inputs; when
  * ckpt == NULL the checkpoints are rebuilt into the workspace first (the
  * reference re-runs its chunk scan from `x`, selective_scan_backward.cuh:330).

@@ -106,6 +106,7 @@ EXPORTS = (
     "lrnnx_selective_scan_ckpt_size",
     "lrnnx_selective_scan_workspace_size",
     "lrnnx_selective_scan_fwd",
+    "lrnnx_selective_scan_fwd_noalloc",
     "lrnnx_selective_scan_bwd",
     "lrnnx_simplified_scan_ckpt_size",
     "lrnnx_simplified_scan_workspace_size",
@@ -146,6 +147,7 @@ def lib():
         L.lrnnx_selective_scan_workspace_size.argtypes = [P(SelectiveScanArgs), ctypes.c_int]
         L.lrnnx_selective_scan_workspace_size.restype = c_i64
         L.lrnnx_selective_scan_fwd.argtypes = [P(SelectiveScanArgs), c_vp]
+        L.lrnnx_selective_scan_fwd_noalloc.argtypes = [P(SelectiveScanArgs), c_vp]
         L.lrnnx_selective_scan_bwd.argtypes = [P(SelectiveScanArgs), c_vp]
         L.lrnnx_simplified_scan_ckpt_size.argtypes = [P(SimplifiedScanArgs)]
         L.lrnnx_simplified_scan_ckpt_size.restype = c_i64
@@ -166,7 +168,8 @@ def lib():
         L.lrnnx_layer_norm_workspace_size.argtypes = [P(LayerNormArgs)]
         L.lrnnx_layer_norm_workspace_size.restype = c_i64
         L.lrnnx_last_error.restype = ctypes.c_char_p
-        for fn in ("lrnnx_selective_scan_fwd", "lrnnx_selective_scan_bwd", "lrnnx_simplified_scan_fwd",
+        for fn in ("lrnnx_selective_scan_fwd", "lrnnx_selective_scan_fwd_noalloc", "lrnnx_selective_scan_bwd",
+                   "lrnnx_simplified_scan_fwd",
                    "lrnnx_simplified_scan_bwd", "lrnnx_selective_state_update",
                    "lrnnx_simplified_state_update", "lrnnx_abi_version"):
             getattr(L, fn).restype = ctypes.c_int

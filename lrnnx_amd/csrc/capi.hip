@@ -5,9 +5,11 @@
 // csrc/selective_scan/selective_scan_cpu.cpp:263-632 and
 // csrc/simplified_scan/simplified_scan_cpu.cpp:160-331); a failed check
 // returns 1 and leaves the message in lrnnx_last_error().
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include "ss_common.h"
@@ -163,6 +165,42 @@ int check_ss(const lrnnx_selective_scan_args* a, bool bwd) {
 }
 }  // namespace
 
+// Device scratch of lrnnx_selective_scan_fwd_noalloc: the segment summaries
+// and carries of the forward's split of L (h_end, h_init [seg][b][n][d],
+// dsum_seg, dsum_pre [seg][b][d], fp32).  The split keeps segments x
+// batch x dim / 64 <= 512 and the fast path has d_state <= 16, so any call
+// needs at most 2 * 32768 * 16 + 2 * 32768 floats = 4 456 448 bytes.  Each GPU
+// holds its own copy from the library's load until the process ends.
+constexpr int64_t kFwdScratchBytes = LRNNX_FWD_NOALLOC_SCRATCH_BYTES;
+static_assert(kFwdScratchBytes == 2 * 32768 * 16 * 4 + 2 * 32768 * 4, "bound of the split's summaries");
+static __device__ __align__(256) char scratch[kFwdScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of this device's `scratch`, looked up once per device with
+// that device current (the array's host-side name is not a device address).
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  if (from_hip(hipGetDevice(&dev), "hipGetDevice")) return 1;
+  if (dev < 0 || dev >= kMaxDevices) return fail("device index %d out of range (at most %d devices)", dev, kMaxDevices);
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      if (from_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return 1;
+      if (!p) return fail("hipGetSymbolAddress(scratch) returned a null address");
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return 0;
+}
+}  // namespace
+
 extern "C" {
 
 const char* lrnnx_last_error(void) { return g_err.c_str(); }
@@ -197,6 +235,24 @@ int lrnnx_selective_scan_fwd(const lrnnx_selective_scan_args* a, void* stream) {
     e = ss_fwd_other_f32(*a, st);
   }
   return from_hip(e, "selective_scan_fwd");
+}
+
+int lrnnx_selective_scan_fwd_noalloc(const lrnnx_selective_scan_args* a, void* stream) {
+  if (check_ss(a, false)) return 1;
+  lrnnx_selective_scan_args f = *a;  // the caller's workspace fields are ignored
+  f.workspace = nullptr;
+  f.workspace_bytes = 0;
+  const int64_t need = lrnnx_selective_scan_workspace_size(&f, 0);
+  if (need > kFwdScratchBytes)
+    return fail("selective_scan_fwd_noalloc: the call needs %lld bytes of scratch, more than the %lld it holds",
+                (long long)need, (long long)kFwdScratchBytes);
+  if (need > 0) {
+    void* p = nullptr;
+    if (scratch_of_current_device(&p)) return 1;
+    f.workspace = p;
+    f.workspace_bytes = kFwdScratchBytes;
+  }
+  return lrnnx_selective_scan_fwd(&f, stream);
 }
 
 int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args* a, void* stream) {
