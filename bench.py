@@ -519,6 +519,42 @@ def method_configs(torch, dev):
     return res
 
 
+def module_path(torch, ss, inp, steps=10, warmup=2):
+    """fwd + bwd at the headline shape through the drop-in module
+    (``selective_scan_cuda.fwd`` then ``bwd(x)``, as the reference's
+    SelectiveScanFn calls them, outputs allocated per call by torch's caching
+    allocator), in both save modes: "checkpoints" (fwd attaches them to x)
+    and "x" (the backward first rebuilds them from the x carries).  Event-timed
+    medians in ms."""
+    i = inp
+    res = {}
+    prev = ss.save_mode()
+    try:
+        for mode in ("checkpoints", "x"):
+            ss.set_save_mode(mode)
+
+            def run():
+                out, x, out_z = ss.fwd(i["u"], i["delta"], i["A"], i["B"], i["C"], i["D"], i["z"],
+                                       i["delta_bias"], None, True, "mamba")
+                ss.bwd(i["u"], i["delta"], i["A"], i["B"], i["C"], i["D"], i["z"], i["delta_bias"], None,
+                       i["dout"], x, out, None, True, False, "mamba")
+            for _ in range(warmup):
+                run()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ms = []
+            for _ in range(steps):
+                e0.record()
+                run()
+                e1.record()
+                torch.cuda.synchronize()
+                ms.append(e0.elapsed_time(e1))
+            res[f"save_{mode}_fwd_bwd_ms"] = round(sorted(ms)[len(ms) // 2], 4)
+    finally:
+        ss.set_save_mode(prev)
+    return res
+
+
 def other_configs(torch, ss, L_, dev):
     """Config 2 (Mamba-130m layer, fwd+bwd) and config 1 (LRU complex scan,
     fwd+bwd) timings, reported beside the headline line."""
@@ -761,7 +797,12 @@ def main():
                      "frac": round(bwd_achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "fwd_achieved": round(fb / (f_avg * 1e-3) / 1e9, 2)},
     }
-    del step, inp
+    del step
+    torch.cuda.empty_cache()
+    if not args.no_extra:
+        _log("module path (selective_scan_cuda.fwd -> bwd(x)) at the headline shape")
+        result["module_path_cfg3"] = module_path(torch, ss, inp)
+    del inp
     torch.cuda.empty_cache()
     if not args.no_extra:
         try:

@@ -117,6 +117,8 @@ int lrnnx_selective_scan_fwd_noalloc(const lrnnx_selective_scan_args *a, void *s
 /* Backward.  Needs `ckpt` from a forward over the same inputs; when
  * ckpt == NULL the checkpoints are rebuilt into the workspace first (the
  * reference re-runs its chunk scan from `x`, selective_scan_backward.cuh:330).
+ * `x` is optional here; when given (the forward's chunk carries of the same
+ * inputs) the rebuild starts every 2048-step chunk from them, in parallel.
  * Writes du, ddelta, dA, dB, dC, dD, ddelta_bias, ddeltaA (if deltaA), dz
  * (if z).  Variable dB/dC are written in the input dtype (the reference
  * accumulates them in fp32 and casts, selective_scan_cpu.cpp:627); constant

@@ -38,6 +38,12 @@ bool ssf_fwd_f16(const lrnnx_selective_scan_args&, hipStream_t, hipError_t*);
 bool ssf_bwd_f32(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t, hipError_t*);
 bool ssf_bwd_bf16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t, hipError_t*);
 bool ssf_bwd_f16(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t, hipError_t*);
+bool ssf_ckpt_rebuild_f32(const lrnnx_selective_scan_args&, float*, float*, int64_t, const float*, hipStream_t,
+                          hipError_t*);
+bool ssf_ckpt_rebuild_bf16(const lrnnx_selective_scan_args&, float*, float*, int64_t, const float*, hipStream_t,
+                           hipError_t*);
+bool ssf_ckpt_rebuild_f16(const lrnnx_selective_scan_args&, float*, float*, int64_t, const float*, hipStream_t,
+                          hipError_t*);
 hipError_t ss_fwd_other_f32(const lrnnx_selective_scan_args&, hipStream_t);
 int64_t ssf_fwd_workspace_bytes(const lrnnx_selective_scan_args&);
 hipError_t ss_bwd_mamba_f32(const lrnnx_selective_scan_args&, float*, const float*, hipStream_t);
@@ -61,6 +67,7 @@ int64_t ln_workspace_bytes(const lrnnx_layer_norm_args&);
 // defined in ss_bwd_layout.hip (shares ss_bwd_ws with the backward units)
 int64_t ss_bwd_ws_bytes(const lrnnx_selective_scan_args&);
 int64_t ss_bwd_ckpt_offset_bytes(const lrnnx_selective_scan_args&);
+int64_t ss_bwd_fws_offset_bytes(const lrnnx_selective_scan_args&, int64_t*);
 }  // namespace lrnnx
 
 using namespace lrnnx;
@@ -267,18 +274,36 @@ int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args* a, void* stream) {
                                              "selective_scan_bwd (complex)");
   const float* ckp = static_cast<const float*>(a->ckpt);
   if (!ckp) {
-    // rebuild the fine checkpoints with a forward pass that writes nothing else
-    lrnnx_selective_scan_args f = *a;
-    f.out.ptr = nullptr;
-    f.out_z.ptr = nullptr;
-    f.z.ptr = nullptr;
-    f.x = nullptr;
-    f.ckpt = reinterpret_cast<char*>(a->workspace) + ss_bwd_ckpt_offset_bytes(*a);
-    f.workspace = nullptr;  // the rebuild runs unsplit: the workspace holds its checkpoints
-    f.workspace_bytes = 0;
-    hipError_t e = a->method == LRNNX_MAMBA ? fwd_mamba(f, st) : ss_fwd_other_f32(f, st);
+    // rebuild the fine checkpoints into the workspace.  The mamba fast path
+    // has a states-only forward: split like the forward on small grids, or
+    // with the caller's x carries (the reference's seeds,
+    // selective_scan_backward.cuh:330) one 2048-step chunk per grid slice.
+    char* wsb = reinterpret_cast<char*>(a->workspace);
+    float* ck = reinterpret_cast<float*>(wsb + ss_bwd_ckpt_offset_bytes(*a));
+    hipError_t e = hipSuccess;
+    bool done = false;
+    if (a->method == LRNNX_MAMBA && fast_paths_enabled()) {
+      int64_t fws_bytes = 0;
+      float* fws = reinterpret_cast<float*>(wsb + ss_bwd_fws_offset_bytes(*a, &fws_bytes));
+      if (fws_bytes == 0) fws = nullptr;
+      const float* xs = static_cast<const float*>(a->x);
+      done = a->itype == LRNNX_F32    ? ssf_ckpt_rebuild_f32(*a, ck, fws, fws_bytes, xs, st, &e)
+             : a->itype == LRNNX_BF16 ? ssf_ckpt_rebuild_bf16(*a, ck, fws, fws_bytes, xs, st, &e)
+                                      : ssf_ckpt_rebuild_f16(*a, ck, fws, fws_bytes, xs, st, &e);
+    }
+    if (!done) {  // a forward pass that writes nothing else
+      lrnnx_selective_scan_args f = *a;
+      f.out.ptr = nullptr;
+      f.out_z.ptr = nullptr;
+      f.z.ptr = nullptr;
+      f.x = nullptr;
+      f.ckpt = ck;
+      f.workspace = nullptr;  // unsplit
+      f.workspace_bytes = 0;
+      e = a->method == LRNNX_MAMBA ? fwd_mamba(f, st) : ss_fwd_other_f32(f, st);
+    }
     if (from_hip(e, "selective_scan_bwd (checkpoint rebuild)")) return 1;
-    ckp = static_cast<const float*>(f.ckpt);
+    ckp = ck;
   }
   hipError_t e;
   if (a->method == LRNNX_MAMBA) {

@@ -51,6 +51,9 @@ struct SSBwdWs {  // fp32 workspace sections (element offsets)
   // dA / dD / ddelta_bias are per (segment, b); the adjoint buffers
   // g_loc, g_init [seg][b][n][d] and dsum [seg][b][d]
   int64_t S, g_loc, g_init, dsum;
+  // checkpoint rebuild on a split grid: the forward split's summaries and
+  // carries (h_end, h_init [seg][b][n][d], dsum_seg, dsum_pre [seg][b][d])
+  int64_t fws, fws_floats;
 };
 
 inline int64_t align64(int64_t x) { return (x + 63) / 64 * 64; }
@@ -72,6 +75,9 @@ inline SSBwdWs ss_bwd_ws(const lrnnx_selective_scan_args& a, const SSGeom& g, bo
   w.g_init = o; if (S > 1) o += align64(S * B * N * D);
   w.dsum = o; if (S > 1) o += align64(S * B * D);
   w.ckpt = o; if (need_ckpt) o += align64(B * g.n_ck * N * D);
+  w.fws = o;
+  w.fws_floats = (need_ckpt && S > 1) ? 2 * S * B * N * D + 2 * S * B * D : 0;
+  o += align64(w.fws_floats);
   w.total = o;
   return w;
 }

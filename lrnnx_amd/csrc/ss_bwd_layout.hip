@@ -11,4 +11,10 @@ int64_t ss_bwd_ws_bytes(const lrnnx_selective_scan_args& a) {
 int64_t ss_bwd_ckpt_offset_bytes(const lrnnx_selective_scan_args& a) {
   return ss_bwd_ws(a, ss_geom(a), true, ssf_bwd_segments(a)).ckpt * (int64_t)sizeof(float);
 }
+// Section of the checkpoint rebuild's forward split (offset; its size in *bytes, 0 if none).
+int64_t ss_bwd_fws_offset_bytes(const lrnnx_selective_scan_args& a, int64_t* bytes) {
+  const SSBwdWs w = ss_bwd_ws(a, ss_geom(a), true, ssf_bwd_segments(a));
+  *bytes = w.fws_floats * (int64_t)sizeof(float);
+  return w.fws * (int64_t)sizeof(float);
+}
 }  // namespace lrnnx

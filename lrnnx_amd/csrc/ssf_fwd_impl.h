@@ -74,21 +74,30 @@ __device__ __forceinline__ float sigmoidf_fast(float z) {
 // final state and its sum of delta' (no other outputs).  Main pass: h_init !=
 // nullptr; the segment starts from h_init and from dsum_pre, the sum of delta'
 // from its 2048-step chunk's start to the segment start (for the x carries).
-// Buffers: states [seg][b][n][d], sums [seg][b][d].
+// Buffers: states [seg][b][n][d], sums [seg][b][d].  Checkpoint rebuild
+// (kOut = false, below): x_seed != nullptr; segments are the 2048-step chunks
+// of the x carries and segment s > 0 starts from the state x holds at the end
+// of chunk s - 1.
 struct SsfSeg {
   int64_t tiles;
   const float* h_init;
   const float* dsum_pre;
   float* h_end;
   float* dsum_seg;
+  const float* x_seed;
 };
 
 }  // namespace ssf
 
-template <typename IT, bool kSP, bool kZ>
+// kOut = false: checkpoint rebuild for a backward that was given no
+// checkpoints.  Only the states run (no C, no y, no z, no out / x writes):
+// the per-step work drops to exp, two multiplies and the state FMA, and the
+// per-element work to softplus and delta' u.
+template <typename IT, bool kSP, bool kZ, bool kOut = true>
 __global__ void __launch_bounds__(ssf::kNT)
 ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf::SsfSeg sg) {
   using namespace ssf;
+  static_assert(kOut || !kZ, "the checkpoint rebuild reads no z");
   constexpr int kT = tile_steps<IT>();   // steps per tile
   constexpr int kE = 16 / sizeof(IT);    // elements per 16-byte block
   constexpr int kQ = kT / kE;            // blocks per row (= 4)
@@ -103,12 +112,12 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   __shared__ __attribute__((aligned(16))) char s_raw_d[kRaw];
   __shared__ __attribute__((aligned(16))) char s_raw_z[kZ ? 2 * kRaw : 16];
   __shared__ __attribute__((aligned(16))) char s_raw_b[kRawS];
-  __shared__ __attribute__((aligned(16))) char s_raw_c[kRawS];
+  __shared__ __attribute__((aligned(16))) char s_raw_c[kOut ? kRawS : 16];
   __shared__ __attribute__((aligned(16))) float s_dl[kG * kWave * 4];       // [g][lane][4] delta'
   __shared__ __attribute__((aligned(16))) float s_x[kG * kWave * 4];        // [g][lane][4] delta' u
   __shared__ __attribute__((aligned(16))) float s_B[16 * kT];               // [n][t]
-  __shared__ __attribute__((aligned(16))) float s_C[16 * kT];
-  __shared__ __attribute__((aligned(16))) float s_Y[(kNW + 1) * kG * kWave * 4];  // [w][g][lane][4]; w = 4: D u
+  __shared__ __attribute__((aligned(16))) float s_C[kOut ? 16 * kT : 4];
+  __shared__ __attribute__((aligned(16))) float s_Y[kOut ? (kNW + 1) * kG * kWave * 4 : 4];  // [w][g][lane][4]; w = 4: D u
   __shared__ __attribute__((aligned(16))) float s_dsum[kNT];                // [lane][q] chunk sums of delta'
 
   const int tid = threadIdx.x;
@@ -134,7 +143,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   const uint32_t su = (uint32_t)a.u.s1, sd = (uint32_t)a.delta.s1, sz = (uint32_t)a.z.s1;
   const uint32_t sBn = (uint32_t)a.B.s2, sCn = (uint32_t)a.C.s2;
   float* ckp = static_cast<float*>(a.ckpt);
-  float* xp = static_cast<float*>(a.x);
+  float* xp = kOut ? static_cast<float*>(a.x) : nullptr;
 
   // per-lane constants of the recurrence (channel d0 + lane, states n0..n0+3)
   float a2[kS], h[kS];
@@ -144,6 +153,8 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
     const float Av = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + lane) * a.A.s0 + n * a.A.s1] : -1.f;
     a2[k] = Av * kLog2e;
     h[k] = (sg.h_init && n < N) ? sg.h_init[((blockIdx.z * a.batch + b) * N + n) * D + d0 + lane] : 0.f;
+    if (!kOut && sg.x_seed && blockIdx.z > 0 && n < N)   // the state at the end of chunk z - 1
+      h[k] = sg.x_seed[((b * D + d0 + lane) * ((L + kXChunk - 1) / kXChunk) + blockIdx.z - 1) * 2 * N + 2 * n + 1];
   }
   // per-thread constants of the per-element phases (channel d0 + er)
   const float e_bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[(d0 + er) * a.delta_bias.s0] : 0.f;
@@ -165,7 +176,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
     if constexpr (kZ) tile_fetch_async<IT, kQ>(gz + t0, sz, kWave, s_raw_z + (tile & 1) * kRaw, w, kNW, lane);
     // B on wave 0, C on wave 1 (N * kQ <= 64 blocks each: one instruction)
     if (w == 0) tile_fetch_async<IT, kQ>(gB + t0, sBn, N, s_raw_b, 0, 1, lane);
-    if (w == 1) tile_fetch_async<IT, kQ>(gC + t0, sCn, N, s_raw_c, 0, 1, lane);
+    if (kOut && w == 1) tile_fetch_async<IT, kQ>(gC + t0, sCn, N, s_raw_c, 0, 1, lane);
   };
 
   // raw tile -> fp32 operands; thread tid owns row er, steps eq*kE .. +kE
@@ -189,11 +200,12 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
       *reinterpret_cast<float4*>(s_dl + o) = make_float4(vd[i], vd[i + 1], vd[i + 2], vd[i + 3]);
       *reinterpret_cast<float4*>(s_x + o) =
           make_float4(vd[i] * vu[i], vd[i + 1] * vu[i + 1], vd[i + 2] * vu[i + 2], vd[i + 3] * vu[i + 3]);
-      *reinterpret_cast<float4*>(s_Y + kNW * kG * kWave * 4 + o) =
-          make_float4(e_D * vu[i], e_D * vu[i + 1], e_D * vu[i + 2], e_D * vu[i + 3]);
+      if constexpr (kOut)
+        *reinterpret_cast<float4*>(s_Y + kNW * kG * kWave * 4 + o) =
+            make_float4(e_D * vu[i], e_D * vu[i + 1], e_D * vu[i + 2], e_D * vu[i + 3]);
     }
     // B / C rows: threads [0, 64) convert B, [64, 128) C; rows >= N are zero
-    if (tid < 2 * 16 * kQ) {
+    if (tid < (kOut ? 2 : 1) * 16 * kQ) {
       const bool isC = tid >= 16 * kQ;
       const int j = isC ? tid - 16 * kQ : tid;
       const int n = j / kQ;
@@ -279,7 +291,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
 #pragma unroll
       for (int k = 0; k < kS; ++k) {
         b4[k] = *reinterpret_cast<const float4*>(s_B + (n0 + k) * kT + 4 * g);
-        c4[k] = *reinterpret_cast<const float4*>(s_C + (n0 + k) * kT + 4 * g);
+        if constexpr (kOut) c4[k] = *reinterpret_cast<const float4*>(s_C + (n0 + k) * kT + 4 * g);
       }
       const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
       const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
@@ -291,11 +303,11 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
         for (int k = 0; k < kS; ++k) {
           const float ab = __builtin_amdgcn_exp2f(dlv[i] * a2[k]);
           h[k] = fmaf(ab, h[k], xv[i] * (&b4[k].x)[i]);
-          acc = fmaf((&c4[k].x)[i], h[k], acc);
+          if constexpr (kOut) acc = fmaf((&c4[k].x)[i], h[k], acc);
         }
         y[i] = acc;
       }
-      *reinterpret_cast<float4*>(sYw + og) = make_float4(y[0], y[1], y[2], y[3]);
+      if constexpr (kOut) *reinterpret_cast<float4*>(sYw + og) = make_float4(y[0], y[1], y[2], y[3]);
       // checkpoints inside the tile; the one at the tile end is stored after
       // the barrier below, so that the wait before it does not wait for it
       if (ckp != nullptr && ((4 * g + 4) % kCk) == 0 && 4 * g + 4 < kT) store_ckpt(t0 + 4 * g + 4);
@@ -306,7 +318,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
     if (ckp != nullptr) store_ckpt(t0 + kT);
-    epilogue(tile);
+    if constexpr (kOut) epilogue(tile);
     if (chunk_end(tile)) {
       s_dsum[tid] = e_dsum;
       e_dsum = 0.f;
@@ -415,31 +427,55 @@ inline int64_t ssf_fwd_ws_bytes(const lrnnx_selective_scan_args& a) {
   return steps ? ssf::split_ws_floats(a, ssf::n_segs(a, steps)) * (int64_t)sizeof(float) : 0;
 }
 
+namespace ssf {
+enum class FwdKind { kOutZ, kOut, kStates };  // with z gate / without / states and checkpoints only
+}
+
 template <typename IT, bool kSP>
 inline void ssf_fwd_launch_t(const lrnnx_selective_scan_args& a, int64_t n_ck, const ssf::SsfSeg& sg, unsigned nz,
-                             bool z, hipStream_t st) {
+                             ssf::FwdKind kind, hipStream_t st) {
   const dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch, nz);
-  if (z) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true>), grid, dim3(ssf::kNT), 0, st, a, n_ck, sg);
-  else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false>), grid, dim3(ssf::kNT), 0, st, a, n_ck, sg);
+  switch (kind) {
+    case ssf::FwdKind::kOutZ:
+      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true>), grid, dim3(ssf::kNT), 0, st, a, n_ck, sg);
+      break;
+    case ssf::FwdKind::kOut:
+      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true>), grid, dim3(ssf::kNT), 0, st, a, n_ck, sg);
+      break;
+    case ssf::FwdKind::kStates:
+      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false>), grid, dim3(ssf::kNT), 0, st, a, n_ck, sg);
+      break;
+  }
 }
 
 // One launch over the whole of L, or, for small grids and with a workspace of
 // ssf_fwd_ws_bytes, the three-pass split: segment summaries (every segment
-// but the last), the carry chain, then every segment from its initial state.
+// but the last; states only), the carry chain, then every segment from its
+// initial state.  states_only: the checkpoint rebuild of a backward (writes
+// a.ckpt and nothing else); then, when the grid does not split, the x carries
+// `x_seed` (if given) let the 2048-step chunks run in parallel.
 template <typename IT>
-inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_ck, hipStream_t st) {
+inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_ck, hipStream_t st,
+                                 bool states_only = false, const float* x_seed = nullptr) {
   constexpr int kT = ssf::tile_steps<IT>();
   const int64_t n_tiles = a.seqlen / kT;
-  const bool z = a.z.ptr != nullptr;
-  auto launch = [&](const lrnnx_selective_scan_args& x, const ssf::SsfSeg& sg, unsigned nz, bool zz) {
-    if (x.delta_softplus) ssf_fwd_launch_t<IT, true>(x, n_ck, sg, nz, zz, st);
-    else ssf_fwd_launch_t<IT, false>(x, n_ck, sg, nz, zz, st);
+  const ssf::FwdKind kind = states_only             ? ssf::FwdKind::kStates
+                            : a.z.ptr != nullptr    ? ssf::FwdKind::kOutZ
+                                                    : ssf::FwdKind::kOut;
+  auto launch = [&](const lrnnx_selective_scan_args& x, const ssf::SsfSeg& sg, unsigned nz, ssf::FwdKind k) {
+    if (x.delta_softplus) ssf_fwd_launch_t<IT, true>(x, n_ck, sg, nz, k, st);
+    else ssf_fwd_launch_t<IT, false>(x, n_ck, sg, nz, k, st);
   };
   const int64_t steps = ssf::seg_steps(a);
   const int64_t need = ssf_fwd_ws_bytes<IT>(a);
   if (steps == 0 || need == 0 || a.workspace == nullptr || a.workspace_bytes < need ||
       (reinterpret_cast<uintptr_t>(a.workspace) & 15u) != 0) {
-    launch(a, ssf::SsfSeg{n_tiles, nullptr, nullptr, nullptr, nullptr}, 1, z);
+    const int64_t n_xc = (a.seqlen + kXChunk - 1) / kXChunk;
+    if (states_only && x_seed != nullptr && n_xc > 1) {
+      launch(a, ssf::SsfSeg{kXChunk / kT, nullptr, nullptr, nullptr, nullptr, x_seed}, (unsigned)n_xc, kind);
+    } else {
+      launch(a, ssf::SsfSeg{n_tiles, nullptr, nullptr, nullptr, nullptr, nullptr}, 1, kind);
+    }
     return hipGetLastError();
   }
   const int64_t S = ssf::n_segs(a, steps), tiles = steps / kT;
@@ -449,23 +485,23 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
   float* h_init = ws + ns;
   float* dsum_seg = ws + 2 * ns;
   float* dsum_pre = ws + 2 * ns + nd;
-  // summaries: no outputs, no z
+  // summaries: the states only
   lrnnx_selective_scan_args s = a;
   s.out.ptr = nullptr;
   s.out_z.ptr = nullptr;
   s.z.ptr = nullptr;
   s.x = nullptr;
   s.ckpt = nullptr;
-  launch(s, ssf::SsfSeg{tiles, nullptr, nullptr, h_end, dsum_seg}, (unsigned)(S - 1), false);
+  launch(s, ssf::SsfSeg{tiles, nullptr, nullptr, h_end, dsum_seg, nullptr}, (unsigned)(S - 1), ssf::FwdKind::kStates);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const ssf::SsfSeg chain{tiles, nullptr, nullptr, h_end, dsum_seg};
+  const ssf::SsfSeg chain{tiles, nullptr, nullptr, h_end, dsum_seg, nullptr};
   const int64_t nt = a.batch * a.dstate * a.dim;
   hipLaunchKernelGGL(ssf_seg_chain_kernel<IT>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st, a, chain, (int)S,
                      (int)steps, h_init, dsum_pre);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  launch(a, ssf::SsfSeg{tiles, h_init, dsum_pre, nullptr, nullptr}, (unsigned)S, z);
+  launch(a, ssf::SsfSeg{tiles, h_init, dsum_pre, nullptr, nullptr, nullptr}, (unsigned)S, kind);
   return hipGetLastError();
 }
 

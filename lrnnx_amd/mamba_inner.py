@@ -146,7 +146,9 @@ class MambaInnerFn(torch.autograd.Function):
         if D is not None:
             D = D.contiguous()
         a = _ss.build_args(conv1d_out, delta, A, B, C, D, z, delta_bias, None, delta_softplus, "mamba")
-        out, _, out_z, ckpt = _ss.run_fwd(a, conv1d_out, delta, A, z, want_out=True, want_ckpt=True)
+        out, x, out_z, ckpt = _ss.run_fwd(a, conv1d_out, delta, A, z, want_out=True,
+                                          want_ckpt=_ss.keeps_checkpoints())
+        ckpt = _ss.for_backward(x, ckpt)
         ctx.delta_softplus = delta_softplus
         ctx.out_proj_bias_is_None = out_proj_bias is None
         ctx.checkpoint_lvl = checkpoint_lvl

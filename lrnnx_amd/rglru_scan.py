@@ -39,11 +39,12 @@ class RGLRUScanFn(torch.autograd.Function):
         B = torch.ones(dim, dstate, dtype=u.dtype, device=u.device)
         C = torch.ones(dim, dstate, dtype=u.dtype, device=u.device)
         # the binding's fwd, keeping the fine state checkpoints for the backward
-        # (the reference's wrapper saves x, from which its backward restarts)
+        # (the reference's wrapper saves x, from which its backward restarts;
+        # so does the "x" save mode)
         a = _ss.build_args(u, delta, A, B, C, None, None, None, None, False, "rglru")
-        out, x, _, ckpt = _ss.run_fwd(a, u, delta, A, None, want_out=True, want_ckpt=True)
+        out, x, _, ckpt = _ss.run_fwd(a, u, delta, A, None, want_out=True, want_ckpt=_ss.keeps_checkpoints())
         last_state = x[:, :, -1, 1::2]
-        ctx.save_for_backward(u, delta, A, B, C, ckpt)
+        ctx.save_for_backward(u, delta, A, B, C, _ss.for_backward(x, ckpt))
         if return_last_state:
             return out, last_state
         return out

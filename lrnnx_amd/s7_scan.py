@@ -51,10 +51,11 @@ class S7ScanFn(torch.autograd.Function):
         C_k = torch.ones(dstate, 1, dtype=Bu.dtype, device=Bu.device)
         # the binding's fwd, keeping the fine state checkpoints for the backward
         a = _ss.build_args(Bu, delta, A_k, B_k, C_k, None, None, None, None, False, "s7")
-        out_k, _, _, ckpt = _ss.run_fwd(a, Bu, delta, A_k, None, want_out=True, want_ckpt=True)
+        out_k, x_k, _, ckpt = _ss.run_fwd(a, Bu, delta, A_k, None, want_out=True,
+                                          want_ckpt=_ss.keeps_checkpoints())
         y = torch.einsum("bhnl,bnl->bhl", C.float(), out_k.float())
         last_state = out_k[:, :, -1]
-        ctx.save_for_backward(u, B, C, bias, Bu, out_k, ckpt, delta, A_k, B_k, C_k)
+        ctx.save_for_backward(u, B, C, bias, Bu, out_k, _ss.for_backward(x_k, ckpt), delta, A_k, B_k, C_k)
         if return_last_state:
             return y.to(u.dtype), last_state
         return y.to(u.dtype)

@@ -6,8 +6,10 @@ return conventions (``out`` or ``(out, last_state)``, last_state multiplied by
 a constant B, the z-gated output when z is given), same gradient order.
 
 Implementation differences (same results):
-* the forward also writes fp32 state checkpoints every few steps, which the
-  backward reuses instead of re-scanning 2048-step chunks from ``x``;
+* by default the forward also writes fp32 state checkpoints every 16 steps,
+  which the backward reuses instead of re-scanning 2048-step chunks from
+  ``x``; ``selective_scan_cuda.set_save_mode("x")`` (or LRNNX_SCAN_SAVE=x)
+  keeps only ``x``, as the reference does, and the backward rebuilds them;
 * tensors are copied only when their last stride is not 1 (the kernels take
   batch / channel strides), so Mamba's strided x / z halves of ``xz`` are
   not copied;
@@ -43,7 +45,7 @@ class SelectiveScanFn(torch.autograd.Function):
         if C.dim() == 3:
             C = C.unsqueeze(1)
         a = _ss.build_args(u, delta, A, B, C, D, z, delta_bias, deltaA, delta_softplus, discretization)
-        out, x, out_z, ckpt = _ss.run_fwd(a, u, delta, A, z, want_out=True, want_ckpt=True)
+        out, x, out_z, ckpt = _ss.run_fwd(a, u, delta, A, z, want_out=True, want_ckpt=_ss.keeps_checkpoints())
         ctx.delta_softplus = delta_softplus
         ctx.discretization = discretization
         ctx.has_z = z is not None
@@ -51,16 +53,17 @@ class SelectiveScanFn(torch.autograd.Function):
         last_state = x[:, :, -1, 1::2]
         if B.dim() < 3 and return_last_state:
             last_state = last_state * B
-        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, deltaA, ckpt, out if z is not None else None)
+        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, deltaA, _ss.for_backward(x, ckpt),
+                              out if z is not None else None)
         res = out_z if z is not None else out
         return (res, last_state) if return_last_state else res
 
     @staticmethod
     def backward(ctx, dout, *args):
-        u, delta, A, B, C, D, z, delta_bias, deltaA, ckpt, out = ctx.saved_tensors
+        u, delta, A, B, C, D, z, delta_bias, deltaA, saved, out = ctx.saved_tensors
         dout = _lastdim_contig(dout)
         a = _ss.build_args(u, delta, A, B, C, D, z, delta_bias, deltaA, ctx.delta_softplus, ctx.discretization)
-        res = _ss.run_bwd(a, u, delta, A, B, C, D, z, delta_bias, deltaA, dout, out, ckpt)
+        res = _ss.run_bwd(a, u, delta, A, B, C, D, z, delta_bias, deltaA, dout, out, saved)
         du, ddelta, dA, dB, dC, dD, ddelta_bias = res[:7]
         rest = res[7:]
         ddeltaA = rest.pop(0) if ctx.has_deltaA else None

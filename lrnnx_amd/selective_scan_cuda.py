@@ -13,7 +13,20 @@ Differences from the reference, all supersets:
   kernels are fp32-only, selective_scan_cpu.cpp:404, :612);
 * inputs need unit stride along L only (the reference additionally copies
   non-contiguous tensors in its Python wrapper);
-* ``bwd`` does not need ``x``: it rebuilds its fine checkpoints itself.
+* ``bwd`` does not need ``x``: it rebuilds its fine checkpoints itself
+  (from the x carries when given, chunk-parallel).
+
+What the backward keeps from the forward (``set_save_mode``, or
+``LRNNX_SCAN_SAVE`` in the environment):
+* "checkpoints" (default): the forward also writes fp32 states every 16
+  steps (B x L/16 x N x D x 4 bytes) and the backward reuses them.  ``fwd``
+  attaches them to the returned ``x`` (attribute ``_lrnnx_ckpt``), so that a
+  caller that saves ``x`` and hands it to ``bwd``, as the reference's
+  wrappers do, gets the fast backward without a rebuild; they live as long
+  as ``x`` does.
+* "x": only the reference's chunk carries ``x`` (B x D x L/2048 x 2N x 4
+  bytes) are kept, as in the reference; the backward first rebuilds the
+  checkpoints in its workspace (a states-only forward pass).
 """
 
 from __future__ import annotations
@@ -23,7 +36,37 @@ import torch.nn.functional as F
 
 from . import _lib
 
+import os
+
 CHUNK = 2048
+
+_SAVE_MODES = ("checkpoints", "x")
+_save_mode = os.environ.get("LRNNX_SCAN_SAVE", "checkpoints")
+if _save_mode not in _SAVE_MODES:
+    raise RuntimeError(f"LRNNX_SCAN_SAVE must be one of {_SAVE_MODES}, got {_save_mode!r}")
+
+
+def set_save_mode(mode: str) -> None:
+    """"checkpoints" (fast backward, B L N D / 16 fp32 values kept per call) or
+    "x" (the reference's chunk carries only; the backward rebuilds)."""
+    global _save_mode
+    if mode not in _SAVE_MODES:
+        raise ValueError(f"save mode must be one of {_SAVE_MODES}, got {mode!r}")
+    _save_mode = mode
+
+
+def save_mode() -> str:
+    return _save_mode
+
+
+def keeps_checkpoints() -> bool:
+    return _save_mode == "checkpoints"
+
+
+def for_backward(x, ckpt):
+    """The tensor a wrapper saves for ``run_bwd``: the checkpoints, or x in
+    the "x" mode."""
+    return ckpt if (ckpt is not None and keeps_checkpoints()) else x
 
 
 def _n_chunks(L: int) -> int:
@@ -132,9 +175,14 @@ def run_fwd(a, u, delta, A, z, want_out=True, want_ckpt=False):
     return out, x, out_z, ckpt
 
 
-def run_bwd(a, u, delta, A, B, C, D, z, delta_bias, deltaA, dout, out, ckpt, dz=None):
-    """Allocate the gradients and launch the backward.  Returns the reference's
-    list [du, ddelta, dA, dB, dC, dD, ddelta_bias, (ddeltaA), (dz)]."""
+def run_bwd(a, u, delta, A, B, C, D, z, delta_bias, deltaA, dout, out, saved, dz=None):
+    """Allocate the gradients and launch the backward.  ``saved`` is what
+    ``for_backward`` chose: the forward's checkpoints (flat fp32), its x
+    carries (4-D; the backward rebuilds the checkpoints from them) or None.
+    Returns the reference's list [du, ddelta, dA, dB, dC, dD, ddelta_bias,
+    (ddeltaA), (dz)]."""
+    ckpt = saved if (saved is not None and saved.dim() == 1) else None
+    x = saved if (saved is not None and saved.dim() == 4) else None
     _lib.require_gpu(dout)
     _check_last_stride(dout, "dout")
     if dout.dtype != u.dtype:
@@ -163,6 +211,11 @@ def run_bwd(a, u, delta, A, B, C, D, z, delta_bias, deltaA, dout, out, ckpt, dz=
     a.dC = _lib.view(dC, 3) if var_C else _lib.view(dC, 2)
     a.dD, a.ddelta_bias = _lib.view(dD, 1), _lib.view(ddb, 1)
     a.ckpt = ckpt.data_ptr() if ckpt is not None else None
+    if ckpt is None and x is not None and x.dtype == torch.float32:
+        _shape(x, u.shape[0], u.shape[1], _n_chunks(u.shape[2]), 2 * A.shape[1], name="x")
+        if not x.is_contiguous():
+            raise RuntimeError("x must be contiguous")
+        a.x = x.data_ptr()   # seeds of the checkpoint rebuild
     L = _lib.lib()
     nws = L.lrnnx_selective_scan_workspace_size(a, 1)
     ws = torch.empty(max(nws, 256), dtype=torch.uint8, device=u.device)
@@ -180,7 +233,9 @@ def run_bwd(a, u, delta, A, B, C, D, z, delta_bias, deltaA, dout, out, ckpt, dz=
 def fwd(u, delta, A, B, C, D, z, delta_bias, deltaA, delta_softplus, discretization):
     """selective_scan_cuda.fwd: returns [out, x] (+ [out_z] if z is given)."""
     a = build_args(u, delta, A, B, C, D, z, delta_bias, deltaA, delta_softplus, discretization)
-    out, x, out_z, _ = run_fwd(a, u, delta, A, z)
+    out, x, out_z, ckpt = run_fwd(a, u, delta, A, z, want_ckpt=keeps_checkpoints())
+    if ckpt is not None:
+        x._lrnnx_ckpt = ckpt   # picked up by bwd when it is handed this x
     res = [out, x]
     if z is not None:
         res.append(out_z)
@@ -192,7 +247,11 @@ def bwd(u, delta, A, B, C, D, z, delta_bias, deltaA, dout, x, out, dz, delta_sof
     """selective_scan_cuda.bwd: returns [du, ddelta, dA, dB, dC, dD, ddelta_bias]
     (+ [ddeltaA] if deltaA, + [dz] if z, + [out_z] if recompute_out_z)."""
     a = build_args(u, delta, A, B, C, D, z, delta_bias, deltaA, delta_softplus, discretization)
-    res = run_bwd(a, u, delta, A, B, C, D, z, delta_bias, deltaA, dout, out, None, dz)
+    saved = x
+    ck = getattr(x, "_lrnnx_ckpt", None) if x is not None else None
+    if ck is not None and ck.device == u.device and ck.numel() * 4 == _lib.lib().lrnnx_selective_scan_ckpt_size(a):
+        saved = ck   # the checkpoints fwd wrote with this x
+    res = run_bwd(a, u, delta, A, B, C, D, z, delta_bias, deltaA, dout, out, saved, dz)
     if recompute_out_z and z is not None:
         res.append((out.float() * F.silu(z.float())).to(out.dtype))
     return res

@@ -11,7 +11,10 @@ autograd of the restated selective_scan_ref, lrnnx/ops/selective_scan.py:
 * The small-grid split of L against the unsplit schedule
   (LRNNX_SCAN_NO_SPLIT=1) at B=1 D=64 L=4160, both against the oracle.
 * The binding's own call sequence ``selective_scan_cuda.fwd`` -> ``bwd(x)``
-  (the backward rebuilds its checkpoints: no checkpoint buffer is passed).
+  in both save modes: "checkpoints" (fwd attaches them to x) and "x" (the
+  backward rebuilds them: split on small grids, one 2048-step chunk per grid
+  slice from the x carries on long sequences, one pass otherwise); the
+  autograd path in the "x" mode at config 2.
 
 Tolerance, elementwise |got - ref| <= atol + rtol |ref|:
   fp32 I/O: north_star's bound as stated, rtol 1e-4 and an absolute atol of
@@ -36,6 +39,14 @@ from tests.parity import close, close_dev, oracle_selective, to_dev
 pytestmark = pytest.mark.gpu
 
 _REDUCED = ("dA", "dD", "ddelta_bias", "dB", "dC")
+
+
+@pytest.fixture(params=["checkpoints", "x"])
+def save_mode(request):
+    prev = ssc.save_mode()
+    ssc.set_save_mode(request.param)
+    yield request.param
+    ssc.set_save_mode(prev)
 
 
 def _tol(itype):
@@ -81,6 +92,21 @@ def _compare(got, ref, itype):
     ("grid130_f32", 2, 4160, 512, 8, torch.float32),
 ], ids=lambda c: c[0])
 def test_full_grid_vs_oracle(dev, case):
+    _full_grid(dev, case)
+
+
+def test_cfg2_autograd_save_x_vs_oracle(dev):
+    """SelectiveScanFn keeping only x (the reference's saved state): the
+    backward rebuilds the checkpoints."""
+    prev = ssc.save_mode()
+    ssc.set_save_mode("x")
+    try:
+        _full_grid(dev, ("cfg2_save_x", 8, 1536, 2048, 2, torch.bfloat16))
+    finally:
+        ssc.set_save_mode(prev)
+
+
+def _full_grid(dev, case):
     name, Bt, D, L, seed, itype = case
     print(f"[{name}] B={Bt} D={D} L={L} N=16 {itype} seed={seed}: GPU fwd+bwd", flush=True)
     inp = _gpu_inputs(dev, Bt, D, L, 16, seed, itype)
@@ -126,23 +152,24 @@ def _binding_fwd_bwd(inp, method="mamba", softplus=True):
 @pytest.mark.parametrize("case", [
     ("small_f32", 2, 64, 512, torch.float32),
     ("small_bf16", 2, 64, 512, torch.bfloat16),
+    ("small_long_bf16", 1, 64, 4160, torch.bfloat16),
     ("grid132_bf16", 3, 2816, 1024, torch.bfloat16),
+    ("grid132_long_bf16", 3, 2816, 4160, torch.bfloat16),
     ("grid130_f32", 2, 4160, 256, torch.float32),
 ], ids=lambda c: c[0])
-def test_binding_fwd_then_bwd_x_vs_oracle(dev, case):
-    """The boundary's own sequence: bwd gets x and out but no checkpoints, so
-    it rebuilds them (the path the reference's SelectiveScanFn, S7ScanFn and
-    RGLRUScanFn take after the import swap)."""
+def test_binding_fwd_then_bwd_x_vs_oracle(dev, case, save_mode):
+    """The boundary's own sequence, the path the reference's SelectiveScanFn,
+    S7ScanFn and RGLRUScanFn take after the import swap: bwd gets x and out."""
     name, Bt, D, L, itype = case
     inp = _gpu_inputs(dev, Bt, D, L, 16, 31, itype)
-    print(f"[{name}] fwd -> bwd(x)", flush=True)
+    print(f"[{name}] fwd -> bwd(x), save mode {save_mode}", flush=True)
     got = _binding_fwd_bwd(inp)
     ref = _oracle(inp)
     _compare(got, ref, itype)
 
 
 @pytest.mark.parametrize("method", ["rglru", "s7"])
-def test_binding_fwd_then_bwd_x_one_state_methods(dev, method):
+def test_binding_fwd_then_bwd_x_one_state_methods(dev, method, save_mode):
     """The S7 / RG-LRU wrappers' binding calls (N = 1, constant B / C, fp32)
     through fwd -> bwd(x), against fp64 autograd of the restated oracle."""
     g = torch.Generator().manual_seed(41)
