@@ -519,6 +519,53 @@ def method_configs(torch, dev):
     return res
 
 
+def lm_cfg4(torch, dev, decode_steps=256):
+    """Config 4: the 24-layer Mamba LM (d_model 768, d_state 16, vocab 50280,
+    bf16, random init; tests/lm_harness.py on this package's kernels + torch
+    GEMMs).  Prefill: forward of input_ids ~ U[0, vocab) at (8, 2048) without
+    autograd, median of 5 after 2 warm-ups.  Decode: 256 greedy steps at
+    batch 64 from zero caches, one captured HIP graph replayed per token (the
+    step feeds its argmax back), event-timed over the 256 replays."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from tests import lm_harness as H
+
+    model = H.build(torch.bfloat16, dev, seed=0)
+    g = torch.Generator(device=dev).manual_seed(5)
+    ids = torch.randint(0, 50280, (8, 2048), generator=g, device=dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.no_grad():
+        for _ in range(2):
+            model(ids)
+        ms = []
+        for _ in range(5):
+            e0.record()
+            model(ids)
+            e1.record()
+            torch.cuda.synchronize()
+            ms.append(e0.elapsed_time(e1))
+    pre_ms = sorted(ms)[len(ms) // 2]
+    del ids
+    torch.cuda.empty_cache()
+    dg = H.DecodeGraph(model, 64)
+    first = torch.randint(0, 50280, (64, 1), generator=g, device=dev)
+    dg.reset(first)
+    for _ in range(8):
+        dg.replay()
+    dg.reset(first)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(decode_steps):
+        dg.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    dec_ms = e0.elapsed_time(e1) / decode_steps
+    return {"model": "Mamba LM, 24 layers, d_model 768, d_state 16, vocab 50280, bf16, random init",
+            "prefill_batch": 8, "prefill_seqlen": 2048, "prefill_ms": round(pre_ms, 3),
+            "prefill_tokens_per_s": round(8 * 2048 / (pre_ms * 1e-3), 1),
+            "decode_batch": 64, "decode_steps": decode_steps, "decode_ms_per_step": round(dec_ms, 4),
+            "decode_tokens_per_s": round(64 / (dec_ms * 1e-3), 1)}
+
+
 def module_path(torch, ss, inp, steps=10, warmup=2):
     """fwd + bwd at the headline shape through the drop-in module
     (``selective_scan_cuda.fwd`` then ``bwd(x)``, as the reference's
@@ -603,6 +650,11 @@ def other_configs(torch, ss, L_, dev):
     torch.cuda.empty_cache()
     res.update(aux_kernels(torch, L_, dev))
     res["cfg4_decode_state_update"] = decode_cfg4(torch, dev)
+    try:
+        res["cfg4_lm"] = lm_cfg4(torch, dev)
+    except Exception as e:  # reported in the line; the measurements above stand
+        res["cfg4_lm"] = {"error": repr(e)}
+    torch.cuda.empty_cache()
     try:
         res["other_methods_b8_d1536_l2048_f32"] = method_configs(torch, dev)
     except Exception as e:  # reported in the line; the measurements above stand

@@ -45,7 +45,10 @@ class SelectiveScanFn(torch.autograd.Function):
         if C.dim() == 3:
             C = C.unsqueeze(1)
         a = _ss.build_args(u, delta, A, B, C, D, z, delta_bias, deltaA, delta_softplus, discretization)
-        out, x, out_z, ckpt = _ss.run_fwd(a, u, delta, A, z, want_out=True, want_ckpt=_ss.keeps_checkpoints())
+        # no backward will run (inference, no_grad): no checkpoints
+        need_bwd = any(ctx.needs_input_grad[:9])
+        out, x, out_z, ckpt = _ss.run_fwd(a, u, delta, A, z, want_out=True,
+                                          want_ckpt=need_bwd and _ss.keeps_checkpoints())
         ctx.delta_softplus = delta_softplus
         ctx.discretization = discretization
         ctx.has_z = z is not None
