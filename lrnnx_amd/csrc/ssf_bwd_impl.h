@@ -140,21 +140,34 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   const int64_t te = tb + seg_tiles < n_tiles ? tb + seg_tiles : n_tiles;
   const int64_t prow = (int64_t)blockIdx.z * a.batch + b;  // row of the (segment, b) partials
 
+  // Tile fetches: at most one LDS-DMA instruction per wave and tensor (64
+  // rows x kQ blocks; the checkpoint row: N rows x 16 blocks), with per-lane
+  // byte offsets fixed along L; per tile only the scalar base moves.  B on
+  // wave 2, C on wave 3 (N * kQ <= 64 blocks each).
+  constexpr int kQck = kWave * 4 / 16;  // 16-byte blocks of one checkpoint row (64 fp32)
+  static_assert(kQ <= kNW, "a channel tile is at most one fetch instruction per wave");
+  const uint32_t off_u = dma_lane_offset<IT, kQ>(su, w, lane);
+  const uint32_t off_d = dma_lane_offset<IT, kQ>(sd, w, lane);
+  const uint32_t off_do = dma_lane_offset<IT, kQ>(sdo, w, lane);
+  const uint32_t off_z = kZ ? dma_lane_offset<IT, kQ>(sz, w, lane) : 0u;
+  const uint32_t off_os = kZ ? dma_lane_offset<IT, kQ>(sos, w, lane) : 0u;
+  const uint32_t off_bc = dma_lane_offset<IT, kQ>(w == 2 ? sBn : sCn, 0, lane);
+  const uint32_t off_ck = dma_lane_offset<float, kQck>((uint32_t)D, w, lane);
   auto fetch = [&](int64_t tile) __attribute__((always_inline)) {
     const int64_t t0 = tile * kT;
-    tile_fetch_async<IT, kQ>(gu + t0, su, kWave, s_raw_u, w, kNW, lane);
-    tile_fetch_async<IT, kQ>(gd + t0, sd, kWave, s_raw_d, w, kNW, lane);
-    tile_fetch_async<IT, kQ>(gdo + t0, sdo, kWave, s_raw_do, w, kNW, lane);
+    tile_fetch_async_s<kQ>(gu + t0, off_u, kWave, s_raw_u, w, lane);
+    tile_fetch_async_s<kQ>(gd + t0, off_d, kWave, s_raw_d, w, lane);
+    tile_fetch_async_s<kQ>(gdo + t0, off_do, kWave, s_raw_do, w, lane);
     if constexpr (kZ) {
-      tile_fetch_async<IT, kQ>(gz + t0, sz, kWave, s_raw_z, w, kNW, lane);
-      tile_fetch_async<IT, kQ>(gos + t0, sos, kWave, s_raw_o, w, kNW, lane);
+      tile_fetch_async_s<kQ>(gz + t0, off_z, kWave, s_raw_z, w, lane);
+      tile_fetch_async_s<kQ>(gos + t0, off_os, kWave, s_raw_o, w, lane);
     }
-    if (w == 2) tile_fetch_async<IT, kQ>(gB + t0, sBn, N, s_raw_b, 0, 1, lane);
-    if (w == 3) tile_fetch_async<IT, kQ>(gC + t0, sCn, N, s_raw_c, 0, 1, lane);
+    if (w == 2) tile_fetch_async_s<kQ>(gB + t0, off_bc, N, s_raw_b, 0, lane);
+    if (w == 3) tile_fetch_async_s<kQ>(gC + t0, off_bc, N, s_raw_c, 0, lane);
     // h at the start of `tile` = checkpoint tile - 1 (none for tile 0)
     if (tile > 0)
-      tile_fetch_async<float, kWave * 4 / 16>(gck + (tile - 1) * N * D, (uint32_t)D, N,
-                                               reinterpret_cast<char*>(s_ck[tile & 1]), w, kNW, lane);
+      tile_fetch_async_s<kQck>(gck + (tile - 1) * N * D, off_ck, N, reinterpret_cast<char*>(s_ck[tile & 1]), w,
+                               lane);
   };
 
   // raw tile -> fp32 operands; dz is written here

@@ -169,14 +169,21 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   const int64_t te = tb + sg.tiles < n_tiles ? tb + sg.tiles : n_tiles;
   const int64_t n_xc = (L + kXChunk - 1) / kXChunk;
 
+  // Tile fetches: one LDS-DMA instruction per wave and tensor (64 rows x kQ
+  // blocks), with per-lane byte offsets fixed along L; per tile only the
+  // scalar base moves.  B on wave 0, C on wave 1 (N * kQ <= 64 blocks each).
+  static_assert(kQ <= kNW, "a channel tile is one fetch instruction per wave");
+  const uint32_t off_u = dma_lane_offset<IT, kQ>(su, w, lane);
+  const uint32_t off_d = dma_lane_offset<IT, kQ>(sd, w, lane);
+  const uint32_t off_z = kZ ? dma_lane_offset<IT, kQ>(sz, w, lane) : 0u;
+  const uint32_t off_bc = dma_lane_offset<IT, kQ>(w == 0 ? sBn : sCn, 0, lane);
   auto fetch = [&](int64_t tile) __attribute__((always_inline)) {
     const int64_t t0 = tile * kT;
-    tile_fetch_async<IT, kQ>(gu + t0, su, kWave, s_raw_u, w, kNW, lane);
-    tile_fetch_async<IT, kQ>(gd + t0, sd, kWave, s_raw_d, w, kNW, lane);
-    if constexpr (kZ) tile_fetch_async<IT, kQ>(gz + t0, sz, kWave, s_raw_z + (tile & 1) * kRaw, w, kNW, lane);
-    // B on wave 0, C on wave 1 (N * kQ <= 64 blocks each: one instruction)
-    if (w == 0) tile_fetch_async<IT, kQ>(gB + t0, sBn, N, s_raw_b, 0, 1, lane);
-    if (kOut && w == 1) tile_fetch_async<IT, kQ>(gC + t0, sCn, N, s_raw_c, 0, 1, lane);
+    tile_fetch_async_s<kQ>(gu + t0, off_u, kWave, s_raw_u, w, lane);
+    tile_fetch_async_s<kQ>(gd + t0, off_d, kWave, s_raw_d, w, lane);
+    if constexpr (kZ) tile_fetch_async_s<kQ>(gz + t0, off_z, kWave, s_raw_z + (tile & 1) * kRaw, w, lane);
+    if (w == 0) tile_fetch_async_s<kQ>(gB + t0, off_bc, N, s_raw_b, 0, lane);
+    if (kOut && w == 1) tile_fetch_async_s<kQ>(gC + t0, off_bc, N, s_raw_c, 0, lane);
   };
 
   // raw tile -> fp32 operands; thread tid owns row er, steps eq*kE .. +kE
@@ -375,12 +382,27 @@ inline bool rows_aligned(const lrnnx_view& v, bool four_d) {
          (!four_d || (v.s2 * s) % 16 == 0);
 }
 
+// The tile fetches' 32-bit lane offsets reach a tile of this view: 64 channel
+// rows (s1 apart; 16 state rows s2 apart for B / C) of `row_bytes` bytes.
+template <typename IT>
+inline bool fetch_fits(const lrnnx_view& v, bool states, int64_t row_bytes) {
+  if (v.ptr == nullptr) return true;
+  return dma_offsets_fit(states ? v.s2 : v.s1, states ? 16 : kWave, row_bytes, sizeof(IT));
+}
+
 // Shape / option part of the fast-path coverage (both directions).
 template <typename IT>
 inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile) {
   if (a.method != LRNNX_MAMBA || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C || a.deltaA.ptr) return false;
   if (a.dstate <= 8 || a.dstate > 16 || a.seqlen <= 0 || a.seqlen % tile != 0) return false;
   if (a.n_groups <= 0 || a.dim % a.n_groups != 0 || (a.dim / a.n_groups) % kWave != 0) return false;
+  // the checkpoint rows (d_state rows of 64 fp32, D apart) of the backward's fetch
+  if (!dma_offsets_fit(a.dim, a.dstate, kWave * 4, 4)) return false;
+  const int64_t rb = 64;  // bytes of one row of the largest tile (64-byte rows)
+  if (!fetch_fits<IT>(a.u, false, rb) || !fetch_fits<IT>(a.delta, false, rb) || !fetch_fits<IT>(a.z, false, rb) ||
+      !fetch_fits<IT>(a.dout, false, rb) || !fetch_fits<IT>(a.out_saved, false, rb) ||
+      !fetch_fits<IT>(a.B, true, rb) || !fetch_fits<IT>(a.C, true, rb))
+    return false;
   return rows_aligned<IT>(a.u, false) && rows_aligned<IT>(a.delta, false) && rows_aligned<IT>(a.z, false) &&
          rows_aligned<IT>(a.B, true) && rows_aligned<IT>(a.C, true);
 }

@@ -57,6 +57,59 @@ __device__ __forceinline__ void lds_dma_16(const void* g, char* lds_wave_base) {
 }
 #pragma clang diagnostic pop
 
+// The same copy in the scalar-base form: lane l copies the 16 bytes at
+// base + voff (base uniform, held in SGPRs; voff a per-lane 32-bit byte
+// offset).  A kernel that moves a tile window along L keeps voff fixed and
+// moves only the scalar base, so a fetch costs no VALU address arithmetic.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma_16_s(const void* base, uint32_t voff, char* lds_wave_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(to_lds(lds_wave_base)));
+  // readfirstlane returns int: both halves go through uint32_t so that the
+  // low half is zero-extended (a sign extension would set the high 32 bits)
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(b))));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(b >> 32))));
+  const uint64_t sb = (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo);
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2"
+      :
+      : "s"(m0), "v"(voff), "s"(sb)
+      : "memory", "m0");
+#endif
+}
+#pragma clang diagnostic pop
+
+// Byte offset of the block that lane `lane` moves in instruction `instr` of
+// a [rows][kQ] raw-tile fetch (block j = 64 instr + lane: row j / kQ, 16-byte
+// piece j % kQ), for rows `g_stride` elements apart.
+template <typename IT, int kQ>
+__device__ __forceinline__ uint32_t dma_lane_offset(uint32_t g_stride, int instr, int lane) {
+  const uint32_t j = static_cast<uint32_t>(instr * kWave + lane);
+  return ((j / kQ) * g_stride + (j % kQ) * (16 / sizeof(IT))) * static_cast<uint32_t>(sizeof(IT));
+}
+
+// Instruction `instr` of the asynchronous fetch of a [rows][kQ] raw tile whose
+// row 0 starts at `base`, with the lane offsets of dma_lane_offset: lanes past
+// the tile's rows * kQ blocks stay idle.  Tiles of at most 64 * (number of
+// waves) blocks are fetched with one instruction per wave (instr = wave).
+template <int kQ>
+__device__ __forceinline__ void tile_fetch_async_s(const void* base, uint32_t voff, int rows, char* lds, int instr,
+                                                   int lane) {
+  const int nblk = rows * kQ;
+  if (instr * kWave < nblk && instr * kWave + lane < nblk) lds_dma_16_s(base, voff, lds + instr * 1024);
+}
+
+// Whether a tile fetch with the scalar-base form reaches every block: the
+// largest lane offset of a [rows][kQ] tile of row stride `stride` elements
+// fits the 32-bit offset.
+inline bool dma_offsets_fit(int64_t stride, int64_t rows, int64_t row_bytes, int64_t elem_bytes) {
+  return (rows - 1) * stride * elem_bytes + row_bytes <= 0xffffffffll;
+}
+
 // Asynchronous full-tile fetch.  `rows` valid rows (rows * kQ blocks), row r
 // at g_base + r * g_stride (elements).  Instructions are dealt round-robin
 // to the nW waves of the workgroup.
