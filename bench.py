@@ -379,32 +379,56 @@ def _cpu_model():
     return platform.processor() or platform.machine()
 
 
+def _median_runs(fn, warmup=2, runs=5):
+    """Median wall time (s) of `runs` calls after `warmup` untimed ones."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
 def cpu_baseline(torch, R, D_slice=8, Bt=8, L=4096, N=16, D_full=4096):
-    """fp32 restated reference (oracle) fwd + autograd bwd on a channel slice of
-    config 3; extrapolated linearly in D (channels are independent)."""
+    """The restated reference's CPU path (the oracle's selective_scan_ref,
+    fp32: vectorised discretisation + Python loop over L, autograd backward)
+    on a channel slice of config 3, median of 5 runs after 2 warm-ups,
+    extrapolated linearly in D (channels are independent).  `value` uses the
+    GPU line's byte accounting (config 3's bf16 algorithmic bytes over the
+    extrapolated time)."""
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
     inp = R.make_selective_inputs(Bt, D_slice, L, N, seed=3, itype=torch.float32, groups=1)
-    leaves = {k: v.clone().requires_grad_(True) for k, v in inp.items() if isinstance(v, torch.Tensor)}
     g = torch.Generator().manual_seed(4)
     dout = torch.randn(Bt, D_slice, L, generator=g)
-    t0 = time.perf_counter()
-    out = R.selective_scan_ref(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"],
-                               leaves["z"], leaves["delta_bias"], None, True, False, "mamba")
-    t1 = time.perf_counter()
-    out.backward(dout)
-    t2 = time.perf_counter()
-    fwd_b, bwd_b = alg_bytes(Bt, D_slice, L, N, 1, 4)
-    sec = t2 - t0
+    split = {}
+
+    def run():
+        leaves = {k: v.clone().requires_grad_(True) for k, v in inp.items() if isinstance(v, torch.Tensor)}
+        t0 = time.perf_counter()
+        out = R.selective_scan_ref(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"],
+                                   leaves["D"], leaves["z"], leaves["delta_bias"], None, True, False, "mamba")
+        t1 = time.perf_counter()
+        out.backward(dout)
+        split.setdefault("fwd", []).append(t1 - t0)
+        split.setdefault("bwd", []).append(time.perf_counter() - t1)
+
+    sec = _median_runs(run)
+    full = sec * D_full / D_slice
+    fwd_b, bwd_b = alg_bytes(Bt, D_full, L, N, 1, 2)
+    med = lambda v: sorted(v[2:])[len(v[2:]) // 2]
     return {
-        "value": round((fwd_b + bwd_b) / sec / 1e9, 4),
+        "value": round((fwd_b + bwd_b) / full / 1e9, 4),
         "unit": "GB/s",
-        "elem_per_s": round(Bt * D_slice * L / sec, 1),
+        "elem_per_s": round(Bt * D_full * L / full, 1),
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle selective_scan_ref (fp32, restated reference) fwd+autograd bwd on a D-slice: "
-                   f"B={Bt}, D={D_slice} of {D_full}, L={L}, N={N}; fwd {t1 - t0:.2f}s bwd {t2 - t1:.2f}s; "
-                   f"full-D time extrapolated {sec * D_full / D_slice:.1f}s"),
+        "sample": (f"oracle selective_scan_ref (fp32 restatement of the reference's CPU path) fwd + autograd bwd "
+                   f"on a channel slice B={Bt}, D={D_slice} of {D_full}, L={L}, N={N}: median of 5 runs after 2 "
+                   f"warm-ups {sec:.2f} s (fwd {med(split['fwd']):.2f} s, bwd {med(split['bwd']):.2f} s); "
+                   f"full config 3 extrapolated to {full:.1f} s; GB/s with the GPU line's bf16 byte accounting"),
         "host_cpu": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
         "torch_threads": torch.get_num_threads(),
@@ -412,11 +436,42 @@ def cpu_baseline(torch, R, D_slice=8, Bt=8, L=4096, N=16, D_full=4096):
     }
 
 
+def parity_vs_oracle(torch, step, inp):
+    """Per-output and per-gradient error of the timed step's results (config
+    3, all elements) against the float64 C restatement of the selective scan
+    (oracle/selective_scan_ref.c, run on this host's cores): max |err|, max
+    |ref|, and the largest relative error over elements with |ref| >= 1 % of
+    the tensor's max."""
+    from oracle import fast as OF
+
+    ref = OF.selective_scan_mamba(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                                  inp["delta_bias"], True, inp["dout"])
+    g = step.grads
+    got = {"out_z": step.out_z, "du": g["du"], "ddelta": g["ddelta"], "dz": g["dz"], "dA": g["dA"], "dB": g["dB"],
+           "dC": g["dC"], "dD": g["dD"], "ddelta_bias": g["ddb"]}
+    names = {"out_z": "out", "du": "du", "ddelta": "ddelta", "dz": "dz", "dA": "dA", "dB": "dB", "dC": "dC",
+             "dD": "dD", "ddelta_bias": "ddelta_bias"}
+    res = {}
+    for k, t in got.items():
+        r = ref[names[k]].to(t.device)
+        err = (t.double() - r).abs()
+        ar = r.abs()
+        mx = ar.max().item()
+        big = ar >= 1e-2 * mx
+        res[k] = {"max_abs": float(f"{err.max().item():.3e}"), "max_ref": float(f"{mx:.4g}"),
+                  "max_rel": float(f"{(err[big] / ar[big]).max().item():.3e}")}
+        del r, err, ar, big
+    res["oracle"] = "float64 C restatement (oracle/selective_scan_ref.c), all elements of config 3"
+    res["outputs"] = "bf16 (out, du, ddelta, dz, dB, dC: rounded to bf16, a relative step of 2^-8); fp32 (dA, dD, ddelta_bias)"
+    return res
+
+
 def cpu_configs(torch, R):
     """The oracle (fp32 restatement of the reference's CPU path) at the other
-    named shapes, timed on this host: config 0 at full shape (forward only,
-    median of 5 after 2 warm-ups), config 1 and config 2 fwd + autograd bwd on
-    a channel slice, extrapolated linearly (channels are independent)."""
+    named shapes, timed on this host, each the median of 5 runs after 2
+    warm-ups: config 0 at full shape (forward only), configs 1 and 2 fwd +
+    autograd bwd on a channel slice, extrapolated linearly (channels are
+    independent)."""
     res = {}
     inp = R.make_selective_inputs(2, 256, 512, 16, seed=0)
     args = (inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"], inp["delta_bias"], None, True,
@@ -440,30 +495,36 @@ def cpu_configs(torch, R):
     Bu = d["Bu"].clone().requires_grad_(True)
     g = torch.Generator().manual_seed(2)
     dh = torch.complex(torch.randn(Bt, Ps, L, generator=g), torch.randn(Bt, Ps, L, generator=g)) / math.sqrt(2.0)
-    t0 = time.perf_counter()
-    out, _ = R.simplified_scan_kernel_ref(Bu, torch.ones(Bt, Ps, L), A, ones, ones, None, "dirac")
-    out.backward(dh)
-    t = time.perf_counter() - t0
+    def run1():
+        b = Bu.detach().clone().requires_grad_(True)
+        out, _ = R.simplified_scan_kernel_ref(b, torch.ones(Bt, Ps, L), A, ones, ones, None, "dirac")
+        out.backward(dh)
+
+    t = _median_runs(run1)
     tf = t * P / Ps
     alg1 = Bt * P * L * 8 * 5
     res["cfg1_lru_fwd_bwd"] = {"slice_s": round(t, 3), "extrapolated_s": round(tf, 3),
                                "elem_per_s": round(Bt * P * L / tf, 1), "GB_s": round(alg1 / tf / 1e9, 4),
-                               "sample": f"B={Bt} P={Ps} of {P} L={L} complex64, fwd + autograd bwd"}
+                               "sample": f"B={Bt} P={Ps} of {P} L={L} complex64, fwd + autograd bwd, median of 5 "
+                                         f"after 2 warm-ups"}
     # config 2: D-slice
     Bt, D, L, N, Ds = 8, 1536, 2048, 16, 16
     inp = R.make_selective_inputs(Bt, Ds, L, N, seed=2, itype=torch.float32)
-    leaves = {k: v.clone().requires_grad_(True) for k, v in inp.items() if isinstance(v, torch.Tensor)}
     dout = torch.randn(Bt, Ds, L, generator=g)
-    t0 = time.perf_counter()
-    o = R.selective_scan_ref(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"],
-                             leaves["z"], leaves["delta_bias"], None, True, False, "mamba")
-    o.backward(dout)
-    t = time.perf_counter() - t0
+
+    def run2():
+        leaves = {k: v.clone().requires_grad_(True) for k, v in inp.items() if isinstance(v, torch.Tensor)}
+        o = R.selective_scan_ref(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"],
+                                 leaves["z"], leaves["delta_bias"], None, True, False, "mamba")
+        o.backward(dout)
+
+    t = _median_runs(run2)
     tf = t * D / Ds
     fb, bb = alg_bytes(Bt, D, L, N, 1, 2)
     res["cfg2_selective_fwd_bwd"] = {"slice_s": round(t, 3), "extrapolated_s": round(tf, 2),
                                      "elem_per_s": round(Bt * D * L / tf, 1), "GB_s": round((fb + bb) / tf / 1e9, 4),
-                                     "sample": f"B={Bt} D={Ds} of {D} L={L} N={N} fp32 (bf16-byte accounting)"}
+                                     "sample": f"B={Bt} D={Ds} of {D} L={L} N={N} fp32, median of 5 after 2 "
+                                               f"warm-ups (bf16-byte accounting)"}
     return res
 
 
@@ -663,6 +724,10 @@ def other_configs(torch, ss, L_, dev):
     return res
 
 
+# What the SQ counters of the headline kernels show (profiles/selective_scan_cfg3_sq_counters.md):
+# the roofline above is HBM bandwidth (the metric), but VALU issue, not HBM, limits these kernels.
+LIMITER = "valu issue (see profiles/selective_scan_cfg3_sq_counters.md)"
+
 COPY_CALIB_BYTES = 1 << 30
 TRAFFIC_TAGS = ("ssf_bwd_kernel", "ssf_fwd_kernel", "ss_reduce_bc4_kernel", "ss_reduce_batch_kernel")
 
@@ -748,6 +813,26 @@ def summarize_trace(trace_csv):
         print(f"| `{k}` | {g} | {len(v)} | {sum(v) / len(v):.1f} | {m:.1f} | {min(v):.1f} | {max(v):.1f} |")
 
 
+def summarize_counters(csv_paths, tags=("ssf_fwd_kernel", "ssf_bwd_kernel", "ss_reduce_bc4_kernel",
+                                         "ss_reduce_batch_kernel")):
+    """Markdown table of rocprofv3 --pmc counter_collection.csv files of this
+    bench: per kernel (by name tag) and counter, the mean per dispatch."""
+    import csv
+
+    agg = {}
+    for path in csv_paths:
+        with open(path) as fh:
+            for row in csv.DictReader(fh):
+                for t in tags:
+                    if t in row["Kernel_Name"]:
+                        agg.setdefault(t, {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+    print("| kernel | counter | dispatches | mean per dispatch |")
+    print("|---|---|---|---|")
+    for t in tags:
+        for c, v in sorted(agg.get(t, {}).items()):
+            print(f"| `{t}` | {c} | {len(v)} | {sum(v) / len(v):.4g} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -763,9 +848,14 @@ def main():
     ap.add_argument("--methods-only", action="store_true",
                     help="time only the other discretisations / one-state path / complex weights (for a kernel "
                          "trace of those kernels), print their JSON, then exit")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="COUNTER_CSV",
+                    help="print a markdown table of rocprofv3 --pmc counter_collection.csv files, then exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print a markdown summary of a rocprofv3 --kernel-trace CSV of this bench, then exit")
     args = ap.parse_args()
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
+        return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
         return
@@ -844,11 +934,15 @@ def main():
         "fwd_ms_median": round(f_med, 4),
         "bwd_ms_median": round(b_med, 4),
         "alg_bytes": {"fwd": fb, "bwd": bb},
-        "roofline": {"bound": "hbm", "kernel": "lrnnx_selective_scan_bwd (ssf_bwd_kernel + dB/dC, dA/dD/ddelta_bias reductions)",
+        "roofline": {"bound": "hbm", "limiter": LIMITER,
+                     "kernel": "lrnnx_selective_scan_bwd (ssf_bwd_kernel + dB/dC, dA/dD/ddelta_bias reductions)",
                      "achieved": round(bwd_achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(bwd_achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "fwd_achieved": round(fb / (f_avg * 1e-3) / 1e9, 2)},
     }
+    if not args.no_cpu:
+        _log("errors of the timed step against the float64 C oracle (all of config 3)")
+        result["parity"] = parity_vs_oracle(torch, step, inp)
     del step
     torch.cuda.empty_cache()
     if not args.no_extra:

@@ -65,7 +65,8 @@ __device__ __forceinline__ void lds_dma_16(const void* g, char* lds_wave_base) {
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma_16_s(const void* base, uint32_t voff, char* lds_wave_base) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(to_lds(lds_wave_base)));
+  const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+      static_cast<int>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(to_lds(lds_wave_base))))));
   // readfirstlane returns int: both halves go through uint32_t so that the
   // low half is zero-extended (a sign extension would set the high 32 bits)
   const uint64_t b = reinterpret_cast<uint64_t>(base);
