@@ -734,14 +734,11 @@ TRAFFIC_TAGS = ("ssf_bwd_kernel", "ssf_fwd_kernel", "ss_reduce_bc4_kernel", "ss_
 
 def traffic_from_counters(read_csv, write_csv):
     """HBM-side bytes per launch of the headline kernels from two rocprofv3
-    --pmc runs of ``bench.py --copy-calib``:
-      read pass : TCC_EA0_RDREQ TCC_EA0_RDREQ_32B TCC_EA0_RDREQ_64B TCC_EA0_RDREQ_128B
-      write pass: TCC_EA0_WRREQ TCC_EA0_WRREQ_64B
-    (requests from the L2 to the memory fabric, per dispatch, summed over
-    the L2 instances).  Bytes = 32 n32 + 64 n64 + 128 n128 for reads and
-    64 n64 + 32 (n - n64) for writes.  The plain 1 GiB copy of --copy-calib
-    checks the byte conversion: its read and write bytes over 1 GiB are
-    reported as the calibration factors (they come out at 1.00).
+    --pmc runs of ``bench.py --copy-calib``: FETCH_SIZE in the first,
+    WRITE_SIZE in the second (KiB per dispatch, summed over the L2 channels).
+    The plain 1 GiB elementwise copy that --copy-calib runs first is the
+    reference kernel of known size: its FETCH_SIZE and WRITE_SIZE over 1 GiB
+    are the calibration factors, and the kernels' bytes are divided by them.
     """
     import csv
 
@@ -756,22 +753,21 @@ def traffic_from_counters(read_csv, write_csv):
     rd, wr = load(read_csv), load(write_csv)
 
     def rbytes(c):
-        n32, n64, n128 = c.get("TCC_EA0_RDREQ_32B", 0.0), c.get("TCC_EA0_RDREQ_64B", 0.0), c.get("TCC_EA0_RDREQ_128B", 0.0)
-        return 32 * n32 + 64 * n64 + 128 * n128
+        return 1024.0 * c.get("FETCH_SIZE", 0.0)
 
     def wbytes(c):
-        n, n64 = c.get("TCC_EA0_WRREQ", 0.0), c.get("TCC_EA0_WRREQ_64B", 0.0)
-        return 64 * n64 + 32 * (n - n64)
+        return 1024.0 * c.get("WRITE_SIZE", 0.0)
 
     copy_r = max((rbytes(c) for (d, k), c in rd.items() if "MulFunctor" in k), default=None)
     copy_w = max((wbytes(c) for (d, k), c in wr.items() if "MulFunctor" in k), default=None)
     if copy_r is None or copy_w is None:
         raise SystemExit("no copy-calibration kernel in the counter files (run bench.py --copy-calib)")
-    out = {"calibration": {"copy_bytes": COPY_CALIB_BYTES, "read_factor": copy_r / COPY_CALIB_BYTES,
-                           "write_factor": copy_w / COPY_CALIB_BYTES}}
+    fr, fw = copy_r / COPY_CALIB_BYTES, copy_w / COPY_CALIB_BYTES
+    out = {"counters": "FETCH_SIZE, WRITE_SIZE (rocprofv3 --pmc, one pass each)",
+           "calibration": {"copy_bytes": COPY_CALIB_BYTES, "read_factor": fr, "write_factor": fw}}
     for tag in TRAFFIC_TAGS:
-        r = [rbytes(c) for (d, k), c in rd.items() if tag in k]
-        w = [wbytes(c) for (d, k), c in wr.items() if tag in k]
+        r = [rbytes(c) / fr for (d, k), c in rd.items() if tag in k]
+        w = [wbytes(c) / fw for (d, k), c in wr.items() if tag in k]
         if r and w:
             out[tag] = {"read_bytes_per_launch": sum(r) / len(r), "write_bytes_per_launch": sum(w) / len(w),
                         "launches": len(r)}
