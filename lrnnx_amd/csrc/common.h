@@ -172,21 +172,47 @@ __device__ __forceinline__ void rs_step16(float* v) {
   }
 }
 
+// One reduce-scatter pairing of index bit 3 (kBit = 8: lanes i <-> 15 - i of
+// a 16-lane row) or bit 2 (kBit = 4: i <-> 7 - i of each 8): lanes whose bit
+// is clear return lo + the partner's lo, the others hi + the partner's hi.
+// The two halves are DPP bank groups (bit 3: banks 0-1 / 2-3; bit 2: banks
+// 0, 2 / 1, 3), so two v_add_f32_dpp with complementary bank masks do it,
+// with no selects: each writes only its banks.  Inline asm, because the
+// compiler does not form bank-masked DPP adds that keep the other lanes;
+// the s_nop covers the wait states a DPP read needs after a VALU write.
+template <int kBit>
+__device__ __forceinline__ float rs_pair_banked(float lo, float hi) {
+  static_assert(kBit == 8 || kBit == 4, "bank-group pairings are index bits 3 and 2");
+  float r;
+#if defined(__HIP_DEVICE_COMPILE__)
+  if constexpr (kBit == 8) {
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %0, %1, %1 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+        "v_add_f32_dpp %0, %2, %2 row_mirror row_mask:0xf bank_mask:0xc"
+        : "=&v"(r)
+        : "v"(lo), "v"(hi));
+  } else {
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+        "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0xa"
+        : "=&v"(r)
+        : "v"(lo), "v"(hi));
+  }
+#else
+  r = lo + hi;
+#endif
+  return r;
+}
+
 // Last four steps on 16 values (index bits 3..0); result in v[0].
 __device__ __forceinline__ void rs_tail16(float (&v)[16], int lane) {
-  const bool b3 = lane & 8, b2 = lane & 4, b1 = lane & 2, b0 = lane & 1;
+  const bool b1 = lane & 2, b0 = lane & 1;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const float keep = b3 ? v[k + 8] : v[k];
-    const float send = b3 ? v[k] : v[k + 8];
-    v[k] = keep + dpp_mov<kDppRowMirror>(send);
-  }
+  for (int k = 0; k < 8; ++k) v[k] = rs_pair_banked<8>(v[k], v[k + 8]);
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float keep = b2 ? v[k + 4] : v[k];
-    const float send = b2 ? v[k] : v[k + 4];
-    v[k] = keep + dpp_mov<kDppRowHalfMirror>(send);
-  }
+  for (int k = 0; k < 4; ++k) v[k] = rs_pair_banked<4>(v[k], v[k + 4]);
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const float keep = b1 ? v[k + 2] : v[k];

@@ -324,9 +324,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     };
     auto stream_dB = [&](int t, float v) __attribute__((always_inline)) {
       if (t >= 8) { r8[t - 8] = v; return; }
-      const float x3 = rs_pair(v, r8[t], lane & 8, std::integral_constant<int, kDppRowMirror>{});
+      const float x3 = rs_pair_banked<8>(v, r8[t]);
       if (t >= 4) { r4[t - 4] = x3; return; }
-      const float x2 = rs_pair(x3, r4[t], lane & 4, std::integral_constant<int, kDppRowHalfMirror>{});
+      const float x2 = rs_pair_banked<4>(x3, r4[t]);
       if (t >= 2) { r2[t - 2] = x2; return; }
       const float x1 = rs_pair(x2, r2[t], lane & 2, std::integral_constant<int, kDppQuadXor2>{});
       if (t == 1) { r1 = x1; return; }
