@@ -810,9 +810,10 @@ def summarize_trace(trace_csv):
 
 
 def summarize_counters(csv_paths, tags=("ssf_fwd_kernel", "ssf_bwd_kernel", "ss_reduce_bc4_kernel",
-                                         "ss_reduce_batch_kernel")):
+                                         "ss_reduce_batch_kernel", "MulFunctor")):
     """Markdown table of rocprofv3 --pmc counter_collection.csv files of this
-    bench: per kernel (by name tag) and counter, the mean per dispatch."""
+    bench: per kernel (by name tag) and counter, the mean per dispatch
+    (MulFunctor: the 1 GiB copy of --copy-calib)."""
     import csv
 
     agg = {}

@@ -17,8 +17,10 @@
 // sequence is walked from the end in tiles of 16 steps = one checkpoint
 // interval of the forward (fp32 states every 16 steps, layout (B, n_ck, N, D)).
 // Per tile k:
-//   compute(k)  issue the LDS-DMA fetch of raw tile k-1 (u, delta, dout, z,
-//               out, B, C) and of the checkpoint row that starts tile k-1;
+//   compute(k)  issue the LDS-DMA fetch of the checkpoint row that starts
+//               tile k-1 and, when tile k-1 lies in the next raw tile, of
+//               that raw tile (u, delta, dout, z, out, B, C over one or two
+//               16-step tiles, kRT);
 //               recompute A_bar and h over the 16 steps of tile k from its
 //               checkpoint into VGPRs; walk the steps backwards accumulating
 //               dA (per lane), the per-step sums over the wave's states of
@@ -28,7 +30,7 @@
 //               summed over blocks in a fixed order by ss_reduce_bc_kernel).
 //   finish(k)   wait + barrier; epilogue of tile k (du, ddelta; the dD and
 //               ddelta_bias terms stay in per-thread registers) and
-//               conversion of raw tile k-1 (delta' = softplus(delta + bias),
+//               conversion of tile k-1 from its raw tile (delta' = softplus(delta + bias),
 //               u, dy = dout silu(z) to fp32, dz written here, B / C rows).
 // The fp32 operands have one buffer: in the finish phase every thread reads
 // its own slots of tile k (epilogue) before it writes the same slots with
@@ -58,18 +60,25 @@ __device__ __forceinline__ float softplus20_sig(float x, float& sg) {
 }
 }  // namespace ssf
 
-template <typename IT, bool kSP, bool kZ>
+// kRT: steps of one raw-tile fetch, one tile (16) or two (32: 16-bit I/O,
+// L a multiple of 32).  A two-tile fetch reads 64 bytes of each row, half a
+// 128-byte line instead of a quarter, so each line is fetched from memory
+// about half as often; its 11 KB more LDS keep two workgroups per CU.
+template <typename IT, bool kSP, bool kZ, int kRT>
 __global__ void __launch_bounds__(ssf::kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __restrict__ ws, const SSBwdWs wo,
                const float* __restrict__ ckp, const int64_t seg_tiles) {
   using namespace ssf;
   constexpr int kT = 16;                  // steps per tile = checkpoint interval
   static_assert(kT == kCk, "one checkpoint interval per tile");
+  static_assert(kRT == kT || kRT == 2 * kT, "a raw fetch covers one or two tiles");
+  constexpr int kPair = kRT / kT;         // tiles per raw fetch
   constexpr int kG = kT / 4;              // groups of 4 steps
-  constexpr int kRow = kT * (int)sizeof(IT);   // bytes of one raw row of a tile
-  constexpr int kQ = kRow / 16;           // 16-byte blocks per raw row
-  constexpr int kRaw = kWave * kRow;      // [64][kT] raw tile
-  constexpr int kRawS = 16 * kRow;        // [16][kT] raw B or C tile
+  constexpr int kRow = kT * (int)sizeof(IT);    // bytes of one tile's part of a raw row
+  constexpr int kRowR = kRT * (int)sizeof(IT);  // bytes of one raw row
+  constexpr int kQ = kRowR / 16;          // 16-byte blocks per raw row
+  constexpr int kRaw = kWave * kRowR;     // [64][kRT] raw tile
+  constexpr int kRawS = 16 * kRowR;       // [16][kRT] raw B or C tile
   constexpr int kOp = kG * kWave * 4;     // floats of one [g][64][4] operand tile
 
   __shared__ __attribute__((aligned(16))) char s_raw_u[kRaw];
@@ -153,8 +162,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   const uint32_t off_os = kZ ? dma_lane_offset<IT, kQ>(sos, w, lane) : 0u;
   const uint32_t off_bc = dma_lane_offset<IT, kQ>(w == 2 ? sBn : sCn, 0, lane);
   const uint32_t off_ck = dma_lane_offset<float, kQck>((uint32_t)D, w, lane);
-  auto fetch = [&](int64_t tile) __attribute__((always_inline)) {
-    const int64_t t0 = tile * kT;
+  // raw tile r: steps [r kRT, (r + 1) kRT) of every input row
+  auto fetch_raw = [&](int64_t r) __attribute__((always_inline)) {
+    const int64_t t0 = r * kRT;
     tile_fetch_async_s<kQ>(gu + t0, off_u, kWave, s_raw_u, w, lane);
     tile_fetch_async_s<kQ>(gd + t0, off_d, kWave, s_raw_d, w, lane);
     tile_fetch_async_s<kQ>(gdo + t0, off_do, kWave, s_raw_do, w, lane);
@@ -164,16 +174,19 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     }
     if (w == 2) tile_fetch_async_s<kQ>(gB + t0, off_bc, N, s_raw_b, 0, lane);
     if (w == 3) tile_fetch_async_s<kQ>(gC + t0, off_bc, N, s_raw_c, 0, lane);
-    // h at the start of `tile` = checkpoint tile - 1 (none for tile 0)
+  };
+  // h at the start of `tile` = checkpoint tile - 1 (none for tile 0)
+  auto fetch_ck = [&](int64_t tile) __attribute__((always_inline)) {
     if (tile > 0)
       tile_fetch_async_s<kQck>(gck + (tile - 1) * N * D, off_ck, N, reinterpret_cast<char*>(s_ck[tile & 1]), w,
                                lane);
   };
 
-  // raw tile -> fp32 operands; dz is written here
+  // tile's part of its raw tile -> fp32 operands; dz is written here
   auto convert = [&](int64_t tile) __attribute__((always_inline)) {
     float vu[4], vd[4], vdo[4];
-    const int ro = er * kRow + eq * kEb;   // byte offset of this thread's 4 raw elements
+    const int half = (int)(tile % kPair) * kRow;   // the tile's bytes within a raw row
+    const int ro = er * kRowR + half + eq * kEb;   // byte offset of this thread's 4 raw elements
     raw4_to_f32<IT>(s_raw_u + ro, vu);
     raw4_to_f32<IT>(s_raw_d + ro, vd);
     raw4_to_f32<IT>(s_raw_do + ro, vdo);
@@ -210,7 +223,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       const int j = tid & 63;
       const int n = j >> 2, s4 = (j & 3) * 4;
       float v[4];
-      raw4_to_f32<IT>((isC ? s_raw_c : s_raw_b) + n * kRow + s4 * (int)sizeof(IT), v);
+      raw4_to_f32<IT>((isC ? s_raw_c : s_raw_b) + n * kRowR + half + s4 * (int)sizeof(IT), v);
       float* dst = (isC ? s_C : s_B) + s4 * 16 + n;
 #pragma unroll
       for (int i = 0; i < 4; ++i) dst[i * 16] = n < N ? v[i] : 0.f;
@@ -253,8 +266,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     store4<IT>(gddl + tile * kT, dd);
   };
 
-  // ---- prologue: the segment's last tile
-  fetch(te - 1);
+  // ---- prologue: the segment's last tile (segment bounds are multiples of kPair tiles)
+  fetch_raw((te - 1) / kPair);
+  fetch_ck(te - 1);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
   __syncthreads();
   convert(te - 1);
@@ -262,7 +276,11 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
 
   for (int64_t tile = te - 1; tile >= tb; --tile) {
     const int p = (int)(tile & 1);
-    if (tile > tb) fetch(tile - 1);
+    if (tile > tb) {
+      // tile - 1 starts a new raw tile when `tile` is the first of its own
+      if (tile % kPair == 0) fetch_raw((tile - 1) / kPair);
+      fetch_ck(tile - 1);
+    }
 
     // ---- compute(tile)
     float h0[kS];
@@ -497,6 +515,10 @@ inline int64_t ssf_bwd_segs(const lrnnx_selective_scan_args& a) {
 template <typename IT, bool kSP, bool kZ>
 inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                              const float* ckp, int64_t seg_steps, hipStream_t st) {
+  // Two-tile raw fetches for 16-bit I/O when every segment holds an even
+  // number of tiles: L a multiple of 32 (the split's segments are powers of
+  // two >= 128 steps).
+  constexpr bool kTwo = sizeof(IT) == 2;
   const int64_t S = wo.S, B = a.batch, D = a.dim, N = a.dstate;
   const int64_t seg_tiles = S > 1 ? seg_steps / ssf::kCk : a.seqlen / ssf::kCk;
   if (S > 1) {
@@ -507,7 +529,15 @@ inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g
                        ws, wo);
   }
   const dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch, (unsigned)S);
-  hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ>), grid, dim3(ssf::kNT), 0, st, a, g.n_ck, ws, wo, ckp, seg_tiles);
+  if constexpr (kTwo) {
+    if (a.seqlen % (2 * ssf::kCk) == 0) {
+      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk>), grid, dim3(ssf::kNT), 0, st, a, g.n_ck, ws, wo,
+                         ckp, seg_tiles);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk>), grid, dim3(ssf::kNT), 0, st, a, g.n_ck, ws, wo, ckp,
+                     seg_tiles);
 }
 
 template <typename IT>

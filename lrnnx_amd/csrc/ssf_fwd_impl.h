@@ -93,11 +93,17 @@ struct SsfSeg {
 // checkpoints.  Only the states run (no C, no y, no z, no out / x writes):
 // the per-step work drops to exp, two multiplies and the state FMA, and the
 // per-element work to softplus and delta' u.
-template <typename IT, bool kSP, bool kZ, bool kOut = true>
-__global__ void __launch_bounds__(ssf::kNT)
+// kW: waves per workgroup, 4 (4 states each) or 8 (2 states each).  Eight
+// waves give a grid of one workgroup per CU two waves per SIMD; the
+// per-element phases stay on the first four waves (kNT threads) and the
+// other four only run the recurrence.
+template <typename IT, bool kSP, bool kZ, bool kOut = true, int kW = ssf::kNW>
+__global__ void __launch_bounds__(kW * kWave)
 ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf::SsfSeg sg) {
   using namespace ssf;
   static_assert(kOut || !kZ, "the checkpoint rebuild reads no z");
+  static_assert(kW == 4 || kW == 8, "4 or 8 waves");
+  constexpr int kS = 16 / kW;            // states per wave
   constexpr int kT = tile_steps<IT>();   // steps per tile
   constexpr int kE = 16 / sizeof(IT);    // elements per 16-byte block
   constexpr int kQ = kT / kE;            // blocks per row (= 4)
@@ -117,7 +123,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   __shared__ __attribute__((aligned(16))) float s_x[kG * kWave * 4];        // [g][lane][4] delta' u
   __shared__ __attribute__((aligned(16))) float s_B[16 * kT];               // [n][t]
   __shared__ __attribute__((aligned(16))) float s_C[kOut ? 16 * kT : 4];
-  __shared__ __attribute__((aligned(16))) float s_Y[kOut ? (kNW + 1) * kG * kWave * 4 : 4];  // [w][g][lane][4]; w = 4: D u
+  __shared__ __attribute__((aligned(16))) float s_Y[kOut ? (kW + 1) * kG * kWave * 4 : 4];  // [w][g][lane][4]; w = kW: D u
   __shared__ __attribute__((aligned(16))) float s_dsum[kNT];                // [lane][q] chunk sums of delta'
 
   const int tid = threadIdx.x;
@@ -130,8 +136,9 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   const int64_t grp = d0 / (D / a.n_groups);
   const int n0 = w * kS;
 
-  // thread -> (row r, block q) of the per-element phases
-  const int er = tid / kQ, eq = tid % kQ;
+  // thread -> (row r, block q) of the per-element phases (threads < kNT)
+  const bool pe = kW == kNW || tid < kNT;
+  const int er = (tid & (kNT - 1)) / kQ, eq = tid % kQ;
 
   const IT* gu = static_cast<const IT*>(a.u.ptr) + b * a.u.s0 + d0 * a.u.s1;
   const IT* gd = static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d0 * a.delta.s1;
@@ -161,7 +168,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   const float e_D = a.D.ptr ? static_cast<const float*>(a.D.ptr)[(d0 + er) * a.D.s0] : 0.f;
   // sum of this thread's delta' over the current 2048-step chunk (a segment
   // that starts inside a chunk takes the chunk's earlier sum on one thread)
-  float e_dsum = (sg.dsum_pre && eq == 0) ? sg.dsum_pre[(blockIdx.z * a.batch + b) * D + d0 + er] : 0.f;
+  float e_dsum = (sg.dsum_pre && eq == 0 && pe) ? sg.dsum_pre[(blockIdx.z * a.batch + b) * D + d0 + er] : 0.f;
   float e_seg = 0.f;  // sum of this thread's delta' over the segment (summary pass)
 
   const int64_t n_tiles = L / kT;
@@ -208,7 +215,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
       *reinterpret_cast<float4*>(s_x + o) =
           make_float4(vd[i] * vu[i], vd[i + 1] * vu[i + 1], vd[i + 2] * vu[i + 2], vd[i + 3] * vu[i + 3]);
       if constexpr (kOut)
-        *reinterpret_cast<float4*>(s_Y + kNW * kG * kWave * 4 + o) =
+        *reinterpret_cast<float4*>(s_Y + kW * kG * kWave * 4 + o) =
             make_float4(e_D * vu[i], e_D * vu[i + 1], e_D * vu[i + 2], e_D * vu[i + 3]);
     }
     // B / C rows: threads [0, 64) convert B, [64, 128) C; rows >= N are zero
@@ -231,9 +238,9 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
 #pragma unroll
     for (int i = 0; i < kE; i += 4) {
       const int o = op_off<kSh>((eq * kE + i) >> 2, er);
-      float4 acc = *reinterpret_cast<const float4*>(s_Y + kNW * kG * kWave * 4 + o);
+      float4 acc = *reinterpret_cast<const float4*>(s_Y + kW * kG * kWave * 4 + o);
 #pragma unroll
-      for (int ww = 0; ww < kNW; ++ww) {
+      for (int ww = 0; ww < kW; ++ww) {
         const float4 p = *reinterpret_cast<const float4*>(s_Y + ww * kG * kWave * 4 + o);
         acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
       }
@@ -279,7 +286,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   fetch(tb);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
   __syncthreads();
-  convert();
+  if (pe) convert();
   __syncthreads();
 
   float* sYw = s_Y + w * kG * kWave * 4;
@@ -325,12 +332,14 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
     if (ckp != nullptr) store_ckpt(t0 + kT);
-    if constexpr (kOut) epilogue(tile);
-    if (chunk_end(tile)) {
-      s_dsum[tid] = e_dsum;
-      e_dsum = 0.f;
+    if (pe) {
+      if constexpr (kOut) epilogue(tile);
+      if (chunk_end(tile)) {
+        s_dsum[tid] = e_dsum;
+        e_dsum = 0.f;
+      }
+      if (tile + 1 < te) convert();
     }
-    if (tile + 1 < te) convert();
     __syncthreads();
   }
   if (xp && chunk_end(te - 1)) store_x(te - 1);
@@ -340,7 +349,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
       if (n0 + k < N) sg.h_end[((blockIdx.z * a.batch + b) * N + n0 + k) * D + d0 + lane] = h[k];
     e_seg += dpp_mov<kDppQuadXor1>(e_seg);  // the kQ = 4 threads of a channel are consecutive lanes
     e_seg += dpp_mov<kDppQuadXor2>(e_seg);
-    if (eq == 0) sg.dsum_seg[(blockIdx.z * a.batch + b) * D + d0 + er] = e_seg;
+    if (eq == 0 && pe) sg.dsum_seg[(blockIdx.z * a.batch + b) * D + d0 + er] = e_seg;
   }
 }
 
@@ -416,7 +425,8 @@ inline bool ssf_fwd_eligible(const lrnnx_selective_scan_args& a) {
   return ssf::rows_aligned<IT>(a.out, false) && ssf::rows_aligned<IT>(a.out_z, false);
 }
 
-bool l_split_enabled();  // capi.hip: LRNNX_SCAN_NO_SPLIT
+bool l_split_enabled();      // capi.hip: LRNNX_SCAN_NO_SPLIT
+int scan_waves_override();   // capi.hip: LRNNX_SCAN_WAVES
 
 namespace ssf {
 // Steps per segment of the L split: 0 (no split) when the split is switched
@@ -434,6 +444,15 @@ inline int64_t seg_steps(const lrnnx_selective_scan_args& a) {
   return steps < a.seqlen ? steps : 0;
 }
 inline int64_t n_segs(const lrnnx_selective_scan_args& a, int64_t steps) { return (a.seqlen + steps - 1) / steps; }
+// Waves per workgroup of an unsplit launch: 8 (two states each) for grids of
+// at most 256 workgroups, which hold one workgroup per CU and would otherwise
+// run one wave per SIMD; 4 for larger grids, where LDS allows two workgroups
+// per CU and 8 waves' y partials would not fit twice.
+inline int waves_for(const lrnnx_selective_scan_args& a) {
+  const int o = scan_waves_override();
+  if (o) return o;
+  return (a.dim / kWave) * a.batch <= 256 ? 8 : kNW;
+}
 // workspace of the split: h_end and h_init [seg][b][n][d], dsum_seg and dsum_pre [seg][b][d]
 inline int64_t split_ws_floats(const lrnnx_selective_scan_args& a, int64_t S) {
   return 2 * S * a.batch * a.dstate * a.dim + 2 * S * a.batch * a.dim;
@@ -453,19 +472,24 @@ namespace ssf {
 enum class FwdKind { kOutZ, kOut, kStates };  // with z gate / without / states and checkpoints only
 }
 
+// waves: 4 or 8 for the output kinds (ssf::waves_for); the states-only kind
+// (split summaries, checkpoint rebuild) always runs 4.
 template <typename IT, bool kSP>
 inline void ssf_fwd_launch_t(const lrnnx_selective_scan_args& a, int64_t n_ck, const ssf::SsfSeg& sg, unsigned nz,
-                             ssf::FwdKind kind, hipStream_t st) {
+                             ssf::FwdKind kind, int waves, hipStream_t st) {
   const dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch, nz);
+  const dim3 b4(4 * kWave), b8(8 * kWave);
   switch (kind) {
     case ssf::FwdKind::kOutZ:
-      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true>), grid, dim3(ssf::kNT), 0, st, a, n_ck, sg);
+      if (waves == 8) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 8>), grid, b8, 0, st, a, n_ck, sg);
+      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 4>), grid, b4, 0, st, a, n_ck, sg);
       break;
     case ssf::FwdKind::kOut:
-      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true>), grid, dim3(ssf::kNT), 0, st, a, n_ck, sg);
+      if (waves == 8) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 8>), grid, b8, 0, st, a, n_ck, sg);
+      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 4>), grid, b4, 0, st, a, n_ck, sg);
       break;
     case ssf::FwdKind::kStates:
-      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false>), grid, dim3(ssf::kNT), 0, st, a, n_ck, sg);
+      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false, 4>), grid, b4, 0, st, a, n_ck, sg);
       break;
   }
 }
@@ -484,9 +508,10 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
   const ssf::FwdKind kind = states_only             ? ssf::FwdKind::kStates
                             : a.z.ptr != nullptr    ? ssf::FwdKind::kOutZ
                                                     : ssf::FwdKind::kOut;
-  auto launch = [&](const lrnnx_selective_scan_args& x, const ssf::SsfSeg& sg, unsigned nz, ssf::FwdKind k) {
-    if (x.delta_softplus) ssf_fwd_launch_t<IT, true>(x, n_ck, sg, nz, k, st);
-    else ssf_fwd_launch_t<IT, false>(x, n_ck, sg, nz, k, st);
+  auto launch = [&](const lrnnx_selective_scan_args& x, const ssf::SsfSeg& sg, unsigned nz, ssf::FwdKind k,
+                    int waves) {
+    if (x.delta_softplus) ssf_fwd_launch_t<IT, true>(x, n_ck, sg, nz, k, waves, st);
+    else ssf_fwd_launch_t<IT, false>(x, n_ck, sg, nz, k, waves, st);
   };
   const int64_t steps = ssf::seg_steps(a);
   const int64_t need = ssf_fwd_ws_bytes<IT>(a);
@@ -494,9 +519,9 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
       (reinterpret_cast<uintptr_t>(a.workspace) & 15u) != 0) {
     const int64_t n_xc = (a.seqlen + kXChunk - 1) / kXChunk;
     if (states_only && x_seed != nullptr && n_xc > 1) {
-      launch(a, ssf::SsfSeg{kXChunk / kT, nullptr, nullptr, nullptr, nullptr, x_seed}, (unsigned)n_xc, kind);
+      launch(a, ssf::SsfSeg{kXChunk / kT, nullptr, nullptr, nullptr, nullptr, x_seed}, (unsigned)n_xc, kind, 4);
     } else {
-      launch(a, ssf::SsfSeg{n_tiles, nullptr, nullptr, nullptr, nullptr, nullptr}, 1, kind);
+      launch(a, ssf::SsfSeg{n_tiles, nullptr, nullptr, nullptr, nullptr, nullptr}, 1, kind, ssf::waves_for(a));
     }
     return hipGetLastError();
   }
@@ -514,7 +539,8 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
   s.z.ptr = nullptr;
   s.x = nullptr;
   s.ckpt = nullptr;
-  launch(s, ssf::SsfSeg{tiles, nullptr, nullptr, h_end, dsum_seg, nullptr}, (unsigned)(S - 1), ssf::FwdKind::kStates);
+  launch(s, ssf::SsfSeg{tiles, nullptr, nullptr, h_end, dsum_seg, nullptr}, (unsigned)(S - 1), ssf::FwdKind::kStates,
+         4);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const ssf::SsfSeg chain{tiles, nullptr, nullptr, h_end, dsum_seg, nullptr};
@@ -523,7 +549,7 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
                      (int)steps, h_init, dsum_pre);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  launch(a, ssf::SsfSeg{tiles, h_init, dsum_pre, nullptr, nullptr, nullptr}, (unsigned)S, kind);
+  launch(a, ssf::SsfSeg{tiles, h_init, dsum_pre, nullptr, nullptr, nullptr}, (unsigned)S, kind, 4);
   return hipGetLastError();
 }
 

@@ -10,6 +10,7 @@ autograd of the restated selective_scan_ref, lrnnx/ops/selective_scan.py:
   moderate L): bf16 B=3 D=2816 L=1024 and fp32 B=2 D=4160 L=512.
 * The small-grid split of L against the unsplit schedule
   (LRNNX_SCAN_NO_SPLIT=1) at B=1 D=64 L=4160, both against the oracle.
+* 4 and 8 waves per workgroup (LRNNX_SCAN_WAVES) on one unsplit grid.
 * The binding's own call sequence ``selective_scan_cuda.fwd`` -> ``bwd(x)``
   in both save modes: "checkpoints" (fwd attaches them to x) and "x" (the
   backward rebuilds them: split on small grids, one 2048-step chunk per grid
@@ -66,7 +67,8 @@ def _oracle(inp):
 
 def _run_fn(inp):
     """selective_scan_fn fwd + bwd (the autograd drop-in path)."""
-    lv = {k: inp[k].clone().requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")}
+    lv = {k: (inp[k].clone().requires_grad_(True) if inp[k] is not None else None)
+          for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")}
     out, last = selective_scan_fn(lv["u"], lv["delta"], lv["A"], lv["B"], lv["C"], lv["D"], lv["z"],
                                   lv["delta_bias"], None, True, True, "mamba")
     out.backward(inp["dout"])
@@ -74,7 +76,7 @@ def _run_fn(inp):
     res = {"out": out.detach(), "last_state": last.detach()}
     for k, gk in (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC"), ("D", "dD"),
                   ("z", "dz"), ("delta_bias", "ddelta_bias")):
-        res[gk] = lv[k].grad
+        res[gk] = lv[k].grad if lv[k] is not None else None
     return res
 
 
@@ -187,3 +189,30 @@ def test_binding_fwd_then_bwd_x_one_state_methods(dev, method, save_mode):
     close("out", got["out"], ro, 1e-4, 1e-5)
     for k, gk in (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC"), ("D", "dD")):
         close(gk, got[gk], rg[k], 1e-4, 1e-4 if gk in _REDUCED else 1e-5)
+
+
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("with_z", [True, False])
+def test_waves_per_workgroup_4_and_8_vs_oracle(dev, monkeypatch, itype, with_z):
+    """The fast kernels with 4 waves (4 states each) and with 8 (2 states
+    each; the default for grids of at most 256 workgroups), forced by
+    LRNNX_SCAN_WAVES on the same unsplit grid, against the oracle and each
+    other (fwd + bwd through selective_scan_fn)."""
+    inp = _gpu_inputs(dev, 2, 128, 4160, 16, 23, itype)
+    if not with_z:
+        inp["z"] = None
+    ref = OF.selective_scan_mamba(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                                  inp["delta_bias"], True, inp["dout"])
+    monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", "1")
+    rt, at, aa = _tol(itype)
+    res = {}
+    for waves in ("4", "8"):
+        monkeypatch.setenv("LRNNX_SCAN_WAVES", waves)
+        print(f"[waves {waves}] {itype} z={with_z}", flush=True)
+        res[waves] = _run_fn(inp)
+        names = ["out", "last_state", "du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias"] + (["dz"] if with_z else [])
+        for name in names:
+            close_dev(f"{name} waves={waves}", res[waves][name], ref[name], rt, at, aa)
+    for name in res["4"]:
+        if res["4"][name] is not None:
+            close_dev(f"{name} 8 vs 4 waves", res["8"][name], res["4"][name].double(), rt, at, aa)
