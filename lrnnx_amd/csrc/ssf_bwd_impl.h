@@ -88,9 +88,10 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   __shared__ __attribute__((aligned(16))) char s_raw_o[kZ ? kRaw : 16];
   __shared__ __attribute__((aligned(16))) char s_raw_b[kRawS];
   __shared__ __attribute__((aligned(16))) char s_raw_c[kRawS];
-  __shared__ __attribute__((aligned(16))) float s_ck[2][16 * kWave];   // [buf][n][lane] h at the tile start
+  __shared__ __attribute__((aligned(16))) float s_ck[16 * kWave];      // [n][lane] h at the tile start
   __shared__ __attribute__((aligned(16))) float s_dl[kOp];             // [g][lane][4] delta'
-  __shared__ __attribute__((aligned(16))) float s_u[kOp];              // u
+  __shared__ __attribute__((aligned(16))) float s_u[kOp];              // u (epilogue)
+  __shared__ __attribute__((aligned(16))) float s_x[kOp];              // delta' u (compute phases)
   __shared__ __attribute__((aligned(16))) float s_dy[kOp];             // dout silu(z)
   __shared__ __attribute__((aligned(16))) float s_sg[kSP ? kOp : 4];   // sigmoid(delta + bias)
   __shared__ __attribute__((aligned(16))) float s_B[kT * 16];          // [t][n]
@@ -178,7 +179,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   // h at the start of `tile` = checkpoint tile - 1 (none for tile 0)
   auto fetch_ck = [&](int64_t tile) __attribute__((always_inline)) {
     if (tile > 0)
-      tile_fetch_async_s<kQck>(gck + (tile - 1) * N * D, off_ck, N, reinterpret_cast<char*>(s_ck[tile & 1]), w,
+      tile_fetch_async_s<kQck>(gck + (tile - 1) * N * D, off_ck, N, reinterpret_cast<char*>(s_ck), w,
                                lane);
   };
 
@@ -213,6 +214,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     const int o = op_off<0>(eq, er);
     *reinterpret_cast<float4*>(&s_dl[o]) = make_float4(vd[0], vd[1], vd[2], vd[3]);
     *reinterpret_cast<float4*>(&s_u[o]) = make_float4(vu[0], vu[1], vu[2], vu[3]);
+    *reinterpret_cast<float4*>(&s_x[o]) = make_float4(vd[0] * vu[0], vd[1] * vu[1], vd[2] * vu[2], vd[3] * vu[3]);
     *reinterpret_cast<float4*>(&s_dy[o]) = make_float4(dy[0], dy[1], dy[2], dy[3]);
     // read back by this thread only, in the epilogue
     if constexpr (kSP) *reinterpret_cast<float4*>(&s_sg[o]) = make_float4(sg[0], sg[1], sg[2], sg[3]);
@@ -275,17 +277,19 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   __syncthreads();
 
   for (int64_t tile = te - 1; tile >= tb; --tile) {
-    const int p = (int)(tile & 1);
+    // ---- compute(tile).  The state at the tile start first: the checkpoint
+    // rows a wave reads are the rows its own fetch instruction writes (states
+    // 4w..4w+3), so once its reads have returned (lgkmcnt(0)) the wave can
+    // fetch the next tile's rows into the same buffer.
+    float h0[kS];
+#pragma unroll
+    for (int k = 0; k < kS; ++k) h0[k] = (tile > 0 && n0 + k < N) ? s_ck[(n0 + k) * kWave + lane] : 0.f;
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     if (tile > tb) {
       // tile - 1 starts a new raw tile when `tile` is the first of its own
       if (tile % kPair == 0) fetch_raw((tile - 1) / kPair);
       fetch_ck(tile - 1);
     }
-
-    // ---- compute(tile)
-    float h0[kS];
-#pragma unroll
-    for (int k = 0; k < kS; ++k) h0[k] = (tile > 0 && n0 + k < N) ? s_ck[p][(n0 + k) * kWave + lane] : 0.f;
     // recompute A_bar and h over the tile; dC_t = sum_d dy_t h_t is complete
     // here, so its reduce-scatter runs before the reverse walk
     float AB[kT][kS], H[kT][kS], accC[kT];
@@ -299,16 +303,16 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
         // hoisted above this group's arithmetic (that would exceed 256 VGPRs)
         __builtin_amdgcn_sched_barrier(0);
         const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[op_off<0>(g, lane)]);
-        const float4 u4 = *reinterpret_cast<const float4*>(&s_u[op_off<0>(g, lane)]);
+        const float4 x4 = *reinterpret_cast<const float4*>(&s_x[op_off<0>(g, lane)]);
         const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[op_off<0>(g, lane)]);
-        const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, uu[4] = {u4.x, u4.y, u4.z, u4.w};
+        const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, xx[4] = {x4.x, x4.y, x4.z, x4.w};
         const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = 4 * g + i;
           const float4 b4 = *reinterpret_cast<const float4*>(s_B + t * 16 + n0);
           const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
-          const float x = dl[i] * uu[i];
+          const float x = xx[i];
           float vC[kS];
 #pragma unroll
           for (int k = 0; k < kS; ++k) {
@@ -354,10 +358,10 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     for (int g = kG - 1; g >= 0; --g) {
       __builtin_amdgcn_sched_barrier(0);
       const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[op_off<0>(g, lane)]);
-      const float4 u4 = *reinterpret_cast<const float4*>(&s_u[op_off<0>(g, lane)]);
+      const float4 x4 = *reinterpret_cast<const float4*>(&s_x[op_off<0>(g, lane)]);
       const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[op_off<0>(g, lane)]);
       const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
-      const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
+      const float xx[4] = {x4.x, x4.y, x4.z, x4.w};
       float p1v[4], p2v[4];
 #pragma unroll
       for (int i = 3; i >= 0; --i) {
@@ -365,7 +369,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
         const float4 b4 = *reinterpret_cast<const float4*>(s_B + t * 16 + n0);
         const float4 c4 = *reinterpret_cast<const float4*>(s_C + t * 16 + n0);
         const float bv[4] = {b4.x, b4.y, b4.z, b4.w}, cv[4] = {c4.x, c4.y, c4.z, c4.w};
-        const float x = dl[i] * uu[i];
+        const float x = xx[i];
         float p1 = 0.f, p2 = 0.f, vB[kS];
 #pragma unroll
         for (int k = 0; k < kS; ++k) {
