@@ -216,3 +216,12 @@ def test_waves_per_workgroup_4_and_8_vs_oracle(dev, monkeypatch, itype, with_z):
     for name in res["4"]:
         if res["4"][name] is not None:
             close_dev(f"{name} 8 vs 4 waves", res["8"][name], res["4"][name].double(), rt, at, aa)
+
+
+def test_bf16_length_16_mod_32_vs_oracle(dev):
+    """bf16 with L = 16 (mod 32): the fast forward needs L % 32 == 0 and the
+    general forward runs; the fast backward takes its one-tile raw fetches
+    (the two-tile form needs an even tile count)."""
+    inp = _gpu_inputs(dev, 2, 128, 1040, 16, 29, torch.bfloat16)
+    ref = _oracle(inp)
+    _compare(_run_fn(inp), ref, torch.bfloat16)
