@@ -29,13 +29,13 @@ bool l_split_enabled() {
   return !(v && v[0] && v[0] != '0');
 }
 
-// LRNNX_SCAN_WAVES=4 or 8 forces the fast kernels' waves per workgroup
-// (cross-checks); 0 otherwise (the launch picks).
-int scan_waves_override() {
-  const char* v = getenv("LRNNX_SCAN_WAVES");
+// LRNNX_SCAN_CHANNELS=64 or 32 forces the fast forward's channels per
+// workgroup (cross-checks); 0 otherwise (the launch picks).
+int scan_channels_override() {
+  const char* v = getenv("LRNNX_SCAN_CHANNELS");
   if (!v) return 0;
-  const int w = atoi(v);
-  return (w == 4 || w == 8) ? w : 0;
+  const int c = atoi(v);
+  return (c == 64 || c == 32) ? c : 0;
 }
 
 hipError_t ss_fwd_mamba_f32(const lrnnx_selective_scan_args&, hipStream_t);

@@ -59,9 +59,9 @@ __device__ __forceinline__ float softplus20_fast(float x) {
 // (a permutation of 64 consecutive 16-byte slots), and the per-element phases,
 // where lane 4 r + q handles groups of one row r (consecutive lanes then hit
 // different 16-byte bank groups).  kSh = log2(4-step groups per thread).
-template <int kSh>
+template <int kSh, int kRows = kWave>
 __device__ __forceinline__ int op_off(int g, int r) {
-  return (g * kWave + (r ^ ((g >> kSh) << 1))) * 4;
+  return (g * kRows + (r ^ ((g >> kSh) << 1))) * 4;
 }
 
 __device__ __forceinline__ float sigmoidf_fast(float z) {
@@ -93,82 +93,93 @@ struct SsfSeg {
 // checkpoints.  Only the states run (no C, no y, no z, no out / x writes):
 // the per-step work drops to exp, two multiplies and the state FMA, and the
 // per-element work to softplus and delta' u.
-// kW: waves per workgroup, 4 (4 states each) or 8 (2 states each).  Eight
-// waves give a grid of one workgroup per CU two waves per SIMD; the
-// per-element phases stay on the first four waves (kNT threads) and the
-// other four only run the recurrence.
-template <typename IT, bool kSP, bool kZ, bool kOut = true, int kW = ssf::kNW>
-__global__ void __launch_bounds__(kW * kWave)
+// kCh: channels per workgroup.  64: lane = channel, 4 states per lane (wave
+// w: states 4w..4w+3).  32: lane = channel + 32 half, 2 states per lane (the
+// lower half of wave w holds states 4w, 4w+1, the upper half 4w+2, 4w+3), so
+// that a grid too small to give every CU two 64-channel workgroups (at most
+// 256 of them) runs twice as many workgroups, two per CU.  The 32-channel
+// form walks 32-step tiles whatever the element size.
+template <typename IT, bool kSP, bool kZ, bool kOut = true, int kCh = kWave>
+__global__ void __launch_bounds__(ssf::kNT)
 ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf::SsfSeg sg) {
   using namespace ssf;
   static_assert(kOut || !kZ, "the checkpoint rebuild reads no z");
-  static_assert(kW == 4 || kW == 8, "4 or 8 waves");
-  constexpr int kS = 16 / kW;            // states per wave
-  constexpr int kT = tile_steps<IT>();   // steps per tile
-  constexpr int kE = 16 / sizeof(IT);    // elements per 16-byte block
-  constexpr int kQ = kT / kE;            // blocks per row (= 4)
-  constexpr int kG = kT / 4;             // groups of 4 steps
-  static_assert(kQ * kWave == kNT, "one 16-byte block per thread and tile");
+  static_assert(kCh == kWave || kCh == kWave / 2, "64 or 32 channels per workgroup");
+  constexpr int kH = kWave / kCh;                                 // lane halves per wave
+  constexpr int kS = 16 / kNW / kH;                               // states per lane
+  constexpr int kT = kCh == kWave ? tile_steps<IT>() : 32;        // steps per tile
+  constexpr int kE = 16 / sizeof(IT);                             // elements per 16-byte block
+  constexpr int kQ = kT / kE;                                     // blocks per raw row
+  constexpr int kEt = kCh * kT / kNT;                             // elements per thread (per-element phases)
+  constexpr int kP = kT / kEt;                                    // threads per row
+  constexpr int kG = kT / 4;                                      // groups of 4 steps
+  constexpr int kSh = kEt == 8 ? 1 : 0;                           // log2(4-step groups per thread)
+  constexpr int kNP = kNW * kH;                                   // y partials per element
+  constexpr int kOp = kG * kCh * 4;                               // floats of a [g][ch][4] operand tile
+  constexpr int kRaw = kCh * kT * (int)sizeof(IT);                // [kCh][kT] raw tile, bytes
+  constexpr int kRawS = 16 * kT * (int)sizeof(IT);                // [16][kT] raw B or C tile
+  constexpr int kInR = kCh * kQ / kWave;                          // fetch instructions per channel tile
+  constexpr int kInS = (16 * kQ + kWave - 1) / kWave;             // fetch instructions per B / C tile
+  static_assert(kEt == 4 || kEt == 8, "a thread converts one or two 4-step groups");
+  static_assert(kEt == kE || (kEt == 4 && sizeof(IT) == 2), "a thread reads one block or half of one");
+  static_assert(kInR <= kNW && 2 * kInS <= kNW, "one fetch instruction per wave and tensor");
   static_assert(kCk % kT == 0 || kT % kCk == 0, "checkpoint interval vs tile");
-  constexpr int kRaw = kWave * kT * (int)sizeof(IT);   // [64][kT] raw tile, bytes
-  constexpr int kRawS = 16 * kT * (int)sizeof(IT);     // [16][kT] raw B or C tile
-  constexpr int kSh = kE == 8 ? 1 : 0;                 // log2(4-step groups per thread)
 
   __shared__ __attribute__((aligned(16))) char s_raw_u[kRaw];
   __shared__ __attribute__((aligned(16))) char s_raw_d[kRaw];
   __shared__ __attribute__((aligned(16))) char s_raw_z[kZ ? 2 * kRaw : 16];
   __shared__ __attribute__((aligned(16))) char s_raw_b[kRawS];
   __shared__ __attribute__((aligned(16))) char s_raw_c[kOut ? kRawS : 16];
-  __shared__ __attribute__((aligned(16))) float s_dl[kG * kWave * 4];       // [g][lane][4] delta'
-  __shared__ __attribute__((aligned(16))) float s_x[kG * kWave * 4];        // [g][lane][4] delta' u
+  __shared__ __attribute__((aligned(16))) float s_dl[kOp];                  // [g][ch][4] delta'
+  __shared__ __attribute__((aligned(16))) float s_x[kOp];                   // [g][ch][4] delta' u
   __shared__ __attribute__((aligned(16))) float s_B[16 * kT];               // [n][t]
   __shared__ __attribute__((aligned(16))) float s_C[kOut ? 16 * kT : 4];
-  __shared__ __attribute__((aligned(16))) float s_Y[kOut ? (kW + 1) * kG * kWave * 4 : 4];  // [w][g][lane][4]; w = kW: D u
-  __shared__ __attribute__((aligned(16))) float s_dsum[kNT];                // [lane][q] chunk sums of delta'
+  __shared__ __attribute__((aligned(16))) float s_Y[kOut ? (kNP + 1) * kOp : 4];  // [partial][g][ch][4]; kNP: D u
+  __shared__ __attribute__((aligned(16))) float s_dsum[kNT];                // [ch][kP] chunk sums of delta'
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ch = lane & (kCh - 1), hf = lane / kCh;   // the lane's channel and lane half
   const int64_t b = blockIdx.y;
   const int64_t D = a.dim, L = a.seqlen;
   const int N = (int)a.dstate;
-  const int64_t d0 = (int64_t)blockIdx.x * kWave;
+  const int64_t d0 = (int64_t)blockIdx.x * kCh;
   const int64_t grp = d0 / (D / a.n_groups);
-  const int n0 = w * kS;
+  const int n0 = w * (16 / kNW) + hf * kS;            // the lane's first state
 
-  // thread -> (row r, block q) of the per-element phases (threads < kNT)
-  const bool pe = kW == kNW || tid < kNT;
-  const int er = (tid & (kNT - 1)) / kQ, eq = tid % kQ;
+  // thread -> (row er, piece eq of kEt elements) of the per-element phases
+  const int er = tid / kP, eq = tid % kP;
 
   const IT* gu = static_cast<const IT*>(a.u.ptr) + b * a.u.s0 + d0 * a.u.s1;
   const IT* gd = static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d0 * a.delta.s1;
   const IT* gz = kZ ? static_cast<const IT*>(a.z.ptr) + b * a.z.s0 + d0 * a.z.s1 : nullptr;
   const IT* gB = static_cast<const IT*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1;
   const IT* gC = static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1;
-  IT* go = a.out.ptr ? static_cast<IT*>(a.out.ptr) + b * a.out.s0 + (d0 + er) * a.out.s1 + eq * kE : nullptr;
-  IT* goz = kZ ? static_cast<IT*>(a.out_z.ptr) + b * a.out_z.s0 + (d0 + er) * a.out_z.s1 + eq * kE : nullptr;
+  IT* go = a.out.ptr ? static_cast<IT*>(a.out.ptr) + b * a.out.s0 + (d0 + er) * a.out.s1 + eq * kEt : nullptr;
+  IT* goz = kZ ? static_cast<IT*>(a.out_z.ptr) + b * a.out_z.s0 + (d0 + er) * a.out_z.s1 + eq * kEt : nullptr;
   const uint32_t su = (uint32_t)a.u.s1, sd = (uint32_t)a.delta.s1, sz = (uint32_t)a.z.s1;
   const uint32_t sBn = (uint32_t)a.B.s2, sCn = (uint32_t)a.C.s2;
   float* ckp = static_cast<float*>(a.ckpt);
   float* xp = kOut ? static_cast<float*>(a.x) : nullptr;
 
-  // per-lane constants of the recurrence (channel d0 + lane, states n0..n0+3)
+  // per-lane constants of the recurrence (channel d0 + ch, states n0 .. n0 + kS - 1)
   float a2[kS], h[kS];
 #pragma unroll
   for (int k = 0; k < kS; ++k) {
     const int n = n0 + k;
-    const float Av = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + lane) * a.A.s0 + n * a.A.s1] : -1.f;
+    const float Av = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + ch) * a.A.s0 + n * a.A.s1] : -1.f;
     a2[k] = Av * kLog2e;
-    h[k] = (sg.h_init && n < N) ? sg.h_init[((blockIdx.z * a.batch + b) * N + n) * D + d0 + lane] : 0.f;
+    h[k] = (sg.h_init && n < N) ? sg.h_init[((blockIdx.z * a.batch + b) * N + n) * D + d0 + ch] : 0.f;
     if (!kOut && sg.x_seed && blockIdx.z > 0 && n < N)   // the state at the end of chunk z - 1
-      h[k] = sg.x_seed[((b * D + d0 + lane) * ((L + kXChunk - 1) / kXChunk) + blockIdx.z - 1) * 2 * N + 2 * n + 1];
+      h[k] = sg.x_seed[((b * D + d0 + ch) * ((L + kXChunk - 1) / kXChunk) + blockIdx.z - 1) * 2 * N + 2 * n + 1];
   }
   // per-thread constants of the per-element phases (channel d0 + er)
   const float e_bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[(d0 + er) * a.delta_bias.s0] : 0.f;
   const float e_D = a.D.ptr ? static_cast<const float*>(a.D.ptr)[(d0 + er) * a.D.s0] : 0.f;
   // sum of this thread's delta' over the current 2048-step chunk (a segment
   // that starts inside a chunk takes the chunk's earlier sum on one thread)
-  float e_dsum = (sg.dsum_pre && eq == 0 && pe) ? sg.dsum_pre[(blockIdx.z * a.batch + b) * D + d0 + er] : 0.f;
+  float e_dsum = (sg.dsum_pre && eq == 0) ? sg.dsum_pre[(blockIdx.z * a.batch + b) * D + d0 + er] : 0.f;
   float e_seg = 0.f;  // sum of this thread's delta' over the segment (summary pass)
 
   const int64_t n_tiles = L / kT;
@@ -176,31 +187,43 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   const int64_t te = tb + sg.tiles < n_tiles ? tb + sg.tiles : n_tiles;
   const int64_t n_xc = (L + kXChunk - 1) / kXChunk;
 
-  // Tile fetches: one LDS-DMA instruction per wave and tensor (64 rows x kQ
-  // blocks), with per-lane byte offsets fixed along L; per tile only the
-  // scalar base moves.  B on wave 0, C on wave 1 (N * kQ <= 64 blocks each).
-  static_assert(kQ <= kNW, "a channel tile is one fetch instruction per wave");
+  // Tile fetches: at most one LDS-DMA instruction per wave and tensor (kCh
+  // rows x kQ blocks: waves 0 .. kInR - 1), with per-lane byte offsets fixed
+  // along L; per tile only the scalar base moves.  B on waves [0, kInS), C on
+  // waves [kInS, 2 kInS) (N * kQ blocks each).
+  const bool bc_b = w < kInS;
+  const int bc_i = bc_b ? w : w - kInS;
   const uint32_t off_u = dma_lane_offset<IT, kQ>(su, w, lane);
   const uint32_t off_d = dma_lane_offset<IT, kQ>(sd, w, lane);
   const uint32_t off_z = kZ ? dma_lane_offset<IT, kQ>(sz, w, lane) : 0u;
-  const uint32_t off_bc = dma_lane_offset<IT, kQ>(w == 0 ? sBn : sCn, 0, lane);
+  const uint32_t off_bc = dma_lane_offset<IT, kQ>(bc_b ? sBn : sCn, bc_i, lane);
   auto fetch = [&](int64_t tile) __attribute__((always_inline)) {
     const int64_t t0 = tile * kT;
-    tile_fetch_async_s<kQ>(gu + t0, off_u, kWave, s_raw_u, w, lane);
-    tile_fetch_async_s<kQ>(gd + t0, off_d, kWave, s_raw_d, w, lane);
-    if constexpr (kZ) tile_fetch_async_s<kQ>(gz + t0, off_z, kWave, s_raw_z + (tile & 1) * kRaw, w, lane);
-    if (w == 0) tile_fetch_async_s<kQ>(gB + t0, off_bc, N, s_raw_b, 0, lane);
-    if (kOut && w == 1) tile_fetch_async_s<kQ>(gC + t0, off_bc, N, s_raw_c, 0, lane);
+    tile_fetch_async_s<kQ>(gu + t0, off_u, kCh, s_raw_u, w, lane);
+    tile_fetch_async_s<kQ>(gd + t0, off_d, kCh, s_raw_d, w, lane);
+    if constexpr (kZ) tile_fetch_async_s<kQ>(gz + t0, off_z, kCh, s_raw_z + (tile & 1) * kRaw, w, lane);
+    if (bc_b) tile_fetch_async_s<kQ>(gB + t0, off_bc, N, s_raw_b, bc_i, lane);
+    else if (kOut && w < 2 * kInS) tile_fetch_async_s<kQ>(gC + t0, off_bc, N, s_raw_c, bc_i, lane);
   };
 
-  // raw tile -> fp32 operands; thread tid owns row er, steps eq*kE .. +kE
+  // kEt raw elements of this thread (byte offset kEt * sizeof(IT) * tid of a raw tile) -> floats
+  auto load_el = [&](const char* raw, float* v) __attribute__((always_inline)) {
+    if constexpr (kEt == kE) raw_to_f32<IT>(*reinterpret_cast<const uint4*>(raw + 16 * tid), v);
+    else raw4_to_f32<IT>(raw + kEt * (int)sizeof(IT) * tid, v);
+  };
+  auto store_el = [&](IT* p, const float* v) __attribute__((always_inline)) {
+    if constexpr (kEt == kE) *reinterpret_cast<uint4*>(p) = f32_to_raw<IT>(v);
+    else store4<IT>(p, v);
+  };
+
+  // raw tile -> fp32 operands; thread tid owns row er, steps eq*kEt .. +kEt
   auto convert = [&]() __attribute__((always_inline)) {
-    float vu[kE], vd[kE];
-    raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_u + 16 * tid), vu);
-    raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_d + 16 * tid), vd);
+    float vu[kEt], vd[kEt];
+    load_el(s_raw_u, vu);
+    load_el(s_raw_d, vd);
     float dsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < kE; ++i) {
+    for (int i = 0; i < kEt; ++i) {
       const float x = vd[i] + e_bias;
       const float dl = kSP ? softplus20_fast(x) : x;
       dsum += dl;
@@ -209,16 +232,17 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
     e_dsum += dsum;
     e_seg += dsum;
 #pragma unroll
-    for (int i = 0; i < kE; i += 4) {
-      const int o = op_off<kSh>((eq * kE + i) >> 2, er);
+    for (int i = 0; i < kEt; i += 4) {
+      const int o = op_off<kSh, kCh>((eq * kEt + i) >> 2, er);
       *reinterpret_cast<float4*>(s_dl + o) = make_float4(vd[i], vd[i + 1], vd[i + 2], vd[i + 3]);
       *reinterpret_cast<float4*>(s_x + o) =
           make_float4(vd[i] * vu[i], vd[i + 1] * vu[i + 1], vd[i + 2] * vu[i + 2], vd[i + 3] * vu[i + 3]);
       if constexpr (kOut)
-        *reinterpret_cast<float4*>(s_Y + kW * kG * kWave * 4 + o) =
+        *reinterpret_cast<float4*>(s_Y + kNP * kOp + o) =
             make_float4(e_D * vu[i], e_D * vu[i + 1], e_D * vu[i + 2], e_D * vu[i + 3]);
     }
-    // B / C rows: threads [0, 64) convert B, [64, 128) C; rows >= N are zero
+    // B / C rows: threads [0, 16 kQ) convert B, [16 kQ, 32 kQ) C, one 16-byte
+    // block each; rows >= N are zero
     if (tid < (kOut ? 2 : 1) * 16 * kQ) {
       const bool isC = tid >= 16 * kQ;
       const int j = isC ? tid - 16 * kQ : tid;
@@ -234,35 +258,39 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   };
 
   auto epilogue = [&](int64_t tile) __attribute__((always_inline)) {
-    float y[kE];
+    float y[kEt];
 #pragma unroll
-    for (int i = 0; i < kE; i += 4) {
-      const int o = op_off<kSh>((eq * kE + i) >> 2, er);
-      float4 acc = *reinterpret_cast<const float4*>(s_Y + kW * kG * kWave * 4 + o);
+    for (int i = 0; i < kEt; i += 4) {
+      const int o = op_off<kSh, kCh>((eq * kEt + i) >> 2, er);
+      float4 acc = *reinterpret_cast<const float4*>(s_Y + kNP * kOp + o);
 #pragma unroll
-      for (int ww = 0; ww < kW; ++ww) {
-        const float4 p = *reinterpret_cast<const float4*>(s_Y + ww * kG * kWave * 4 + o);
-        acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
+      for (int p = 0; p < kNP; ++p) {
+        const float4 q = *reinterpret_cast<const float4*>(s_Y + p * kOp + o);
+        acc.x += q.x; acc.y += q.y; acc.z += q.z; acc.w += q.w;
       }
       y[i] = acc.x; y[i + 1] = acc.y; y[i + 2] = acc.z; y[i + 3] = acc.w;
     }
     const int64_t t0 = tile * kT;
-    if (go) *reinterpret_cast<uint4*>(go + t0) = f32_to_raw<IT>(y);
+    if (go) store_el(go + t0, y);
     if constexpr (kZ) {
-      float vz[kE];
-      raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_z + (tile & 1) * kRaw + 16 * tid), vz);
+      float vz[kEt];
+      load_el(s_raw_z + (tile & 1) * kRaw, vz);
 #pragma unroll
-      for (int i = 0; i < kE; ++i) y[i] *= vz[i] * sigmoidf_fast(vz[i]);
-      *reinterpret_cast<uint4*>(goz + t0) = f32_to_raw<IT>(y);
+      for (int i = 0; i < kEt; ++i) y[i] *= vz[i] * sigmoidf_fast(vz[i]);
+      store_el(goz + t0, y);
     }
   };
 
   // chunk carry after the last step of `tile`: (exp(A sum delta'), h) per state
   auto store_x = [&](int64_t tile) __attribute__((always_inline)) {
-    const float4 s4 = *reinterpret_cast<const float4*>(s_dsum + lane * 4);
-    const float S = (s4.x + s4.y) + (s4.z + s4.w);
+    float S = 0.f;
+#pragma unroll
+    for (int q = 0; q < kP; q += 4) {
+      const float4 s4 = *reinterpret_cast<const float4*>(s_dsum + ch * kP + q);
+      S += (s4.x + s4.y) + (s4.z + s4.w);
+    }
     const int64_t c = (tile * kT) / kXChunk;
-    float* xr = xp + ((b * D + d0 + lane) * n_xc + c) * 2 * N;
+    float* xr = xp + ((b * D + d0 + ch) * n_xc + c) * 2 * N;
 #pragma unroll
     for (int k = 0; k < kS; ++k) {
       if (n0 + k < N) {
@@ -273,7 +301,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   };
   // fp32 state after step t_end - 1 (t_end a multiple of kCk): checkpoint t_end / kCk - 1
   auto store_ckpt = [&](int64_t t_end) __attribute__((always_inline)) {
-    float* cp = ckp + ((b * n_ck + t_end / kCk - 1) * N + n0) * D + d0 + lane;
+    float* cp = ckp + ((b * n_ck + t_end / kCk - 1) * N + n0) * D + d0 + ch;
 #pragma unroll
     for (int k = 0; k < kS; ++k)
       if (n0 + k < N) cp[(int64_t)k * D] = h[k];
@@ -286,10 +314,10 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   fetch(tb);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
   __syncthreads();
-  if (pe) convert();
+  convert();
   __syncthreads();
 
-  float* sYw = s_Y + w * kG * kWave * 4;
+  float* sYw = s_Y + (w * kH + hf) * kOp;   // this lane's y partial slot
   for (int64_t tile = tb; tile < te; ++tile) {
     if (tile + 1 < te) fetch(tile + 1);
     if (tile > tb && xp && chunk_end(tile - 1)) store_x(tile - 1);
@@ -298,7 +326,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
     const int64_t t0 = tile * kT;
 #pragma unroll
     for (int g = 0; g < kG; ++g) {
-      const int og = op_off<kSh>(g, lane);
+      const int og = op_off<kSh, kCh>(g, ch);
       const float4 dl4 = *reinterpret_cast<const float4*>(s_dl + og);
       const float4 x4 = *reinterpret_cast<const float4*>(s_x + og);
       float4 b4[kS], c4[kS];
@@ -332,24 +360,24 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
     if (ckp != nullptr) store_ckpt(t0 + kT);
-    if (pe) {
-      if constexpr (kOut) epilogue(tile);
-      if (chunk_end(tile)) {
-        s_dsum[tid] = e_dsum;
-        e_dsum = 0.f;
-      }
-      if (tile + 1 < te) convert();
+    if constexpr (kOut) epilogue(tile);
+    if (chunk_end(tile)) {
+      s_dsum[tid] = e_dsum;
+      e_dsum = 0.f;
     }
+    if (tile + 1 < te) convert();
     __syncthreads();
   }
   if (xp && chunk_end(te - 1)) store_x(te - 1);
   if (sg.h_end) {  // summary pass: the segment's final state and sum of delta'
 #pragma unroll
     for (int k = 0; k < kS; ++k)
-      if (n0 + k < N) sg.h_end[((blockIdx.z * a.batch + b) * N + n0 + k) * D + d0 + lane] = h[k];
-    e_seg += dpp_mov<kDppQuadXor1>(e_seg);  // the kQ = 4 threads of a channel are consecutive lanes
+      if (n0 + k < N) sg.h_end[((blockIdx.z * a.batch + b) * N + n0 + k) * D + d0 + ch] = h[k];
+    // the kP threads of a channel are consecutive lanes
+    e_seg += dpp_mov<kDppQuadXor1>(e_seg);
     e_seg += dpp_mov<kDppQuadXor2>(e_seg);
-    if (eq == 0 && pe) sg.dsum_seg[(blockIdx.z * a.batch + b) * D + d0 + er] = e_seg;
+    if constexpr (kP == 8) e_seg += __shfl_xor(e_seg, 4);
+    if (eq == 0) sg.dsum_seg[(blockIdx.z * a.batch + b) * D + d0 + er] = e_seg;
   }
 }
 
@@ -425,8 +453,8 @@ inline bool ssf_fwd_eligible(const lrnnx_selective_scan_args& a) {
   return ssf::rows_aligned<IT>(a.out, false) && ssf::rows_aligned<IT>(a.out_z, false);
 }
 
-bool l_split_enabled();      // capi.hip: LRNNX_SCAN_NO_SPLIT
-int scan_waves_override();   // capi.hip: LRNNX_SCAN_WAVES
+bool l_split_enabled();         // capi.hip: LRNNX_SCAN_NO_SPLIT
+int scan_channels_override();   // capi.hip: LRNNX_SCAN_CHANNELS
 
 namespace ssf {
 // Steps per segment of the L split: 0 (no split) when the split is switched
@@ -444,14 +472,16 @@ inline int64_t seg_steps(const lrnnx_selective_scan_args& a) {
   return steps < a.seqlen ? steps : 0;
 }
 inline int64_t n_segs(const lrnnx_selective_scan_args& a, int64_t steps) { return (a.seqlen + steps - 1) / steps; }
-// Waves per workgroup of an unsplit launch: 8 (two states each) for grids of
-// at most 256 workgroups, which hold one workgroup per CU and would otherwise
-// run one wave per SIMD; 4 for larger grids, where LDS allows two workgroups
-// per CU and 8 waves' y partials would not fit twice.
-inline int waves_for(const lrnnx_selective_scan_args& a) {
-  const int o = scan_waves_override();
-  if (o) return o;
-  return (a.dim / kWave) * a.batch <= 256 ? 8 : kNW;
+// Channels per workgroup of an unsplit output launch: 32 when 64-channel
+// workgroups would number at most 256 (one per CU, one wave per SIMD), so
+// that the doubled grid puts two independent workgroups on a CU; 64
+// otherwise.  The 32-channel form needs L a multiple of its 32-step tile.
+inline int chans_for(const lrnnx_selective_scan_args& a) {
+  const int o = scan_channels_override();
+  const bool can32 = a.seqlen % 32 == 0;
+  if (o == 32 && can32) return 32;
+  if (o) return kWave;
+  return (can32 && (a.dim / kWave) * a.batch <= 256) ? 32 : kWave;
 }
 // workspace of the split: h_end and h_init [seg][b][n][d], dsum_seg and dsum_pre [seg][b][d]
 inline int64_t split_ws_floats(const lrnnx_selective_scan_args& a, int64_t S) {
@@ -472,24 +502,25 @@ namespace ssf {
 enum class FwdKind { kOutZ, kOut, kStates };  // with z gate / without / states and checkpoints only
 }
 
-// waves: 4 or 8 for the output kinds (ssf::waves_for); the states-only kind
-// (split summaries, checkpoint rebuild) always runs 4.
+// chans: 64 or 32 for the output kinds (ssf::chans_for); the states-only
+// kind (split summaries, checkpoint rebuild) always runs 64.
 template <typename IT, bool kSP>
 inline void ssf_fwd_launch_t(const lrnnx_selective_scan_args& a, int64_t n_ck, const ssf::SsfSeg& sg, unsigned nz,
-                             ssf::FwdKind kind, int waves, hipStream_t st) {
-  const dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch, nz);
-  const dim3 b4(4 * kWave), b8(8 * kWave);
+                             ssf::FwdKind kind, int chans, hipStream_t st) {
+  const dim3 grid64((unsigned)(a.dim / kWave), (unsigned)a.batch, nz);
+  const dim3 grid32((unsigned)(a.dim / (kWave / 2)), (unsigned)a.batch, nz);
+  const dim3 blk(ssf::kNT);
   switch (kind) {
     case ssf::FwdKind::kOutZ:
-      if (waves == 8) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 8>), grid, b8, 0, st, a, n_ck, sg);
-      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 4>), grid, b4, 0, st, a, n_ck, sg);
+      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 32>), grid32, blk, 0, st, a, n_ck, sg);
+      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 64>), grid64, blk, 0, st, a, n_ck, sg);
       break;
     case ssf::FwdKind::kOut:
-      if (waves == 8) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 8>), grid, b8, 0, st, a, n_ck, sg);
-      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 4>), grid, b4, 0, st, a, n_ck, sg);
+      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 32>), grid32, blk, 0, st, a, n_ck, sg);
+      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 64>), grid64, blk, 0, st, a, n_ck, sg);
       break;
     case ssf::FwdKind::kStates:
-      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false, 4>), grid, b4, 0, st, a, n_ck, sg);
+      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false, 64>), grid64, blk, 0, st, a, n_ck, sg);
       break;
   }
 }
@@ -509,9 +540,9 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
                             : a.z.ptr != nullptr    ? ssf::FwdKind::kOutZ
                                                     : ssf::FwdKind::kOut;
   auto launch = [&](const lrnnx_selective_scan_args& x, const ssf::SsfSeg& sg, unsigned nz, ssf::FwdKind k,
-                    int waves) {
-    if (x.delta_softplus) ssf_fwd_launch_t<IT, true>(x, n_ck, sg, nz, k, waves, st);
-    else ssf_fwd_launch_t<IT, false>(x, n_ck, sg, nz, k, waves, st);
+                    int chans) {
+    if (x.delta_softplus) ssf_fwd_launch_t<IT, true>(x, n_ck, sg, nz, k, chans, st);
+    else ssf_fwd_launch_t<IT, false>(x, n_ck, sg, nz, k, chans, st);
   };
   const int64_t steps = ssf::seg_steps(a);
   const int64_t need = ssf_fwd_ws_bytes<IT>(a);
@@ -519,9 +550,12 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
       (reinterpret_cast<uintptr_t>(a.workspace) & 15u) != 0) {
     const int64_t n_xc = (a.seqlen + kXChunk - 1) / kXChunk;
     if (states_only && x_seed != nullptr && n_xc > 1) {
-      launch(a, ssf::SsfSeg{kXChunk / kT, nullptr, nullptr, nullptr, nullptr, x_seed}, (unsigned)n_xc, kind, 4);
+      launch(a, ssf::SsfSeg{kXChunk / kT, nullptr, nullptr, nullptr, nullptr, x_seed}, (unsigned)n_xc, kind, kWave);
     } else {
-      launch(a, ssf::SsfSeg{n_tiles, nullptr, nullptr, nullptr, nullptr, nullptr}, 1, kind, ssf::waves_for(a));
+      const int chans = states_only ? kWave : ssf::chans_for(a);
+      // the 32-channel form walks 32-step tiles
+      launch(a, ssf::SsfSeg{chans == 32 ? a.seqlen / 32 : n_tiles, nullptr, nullptr, nullptr, nullptr, nullptr}, 1,
+             kind, chans);
     }
     return hipGetLastError();
   }
@@ -540,7 +574,7 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
   s.x = nullptr;
   s.ckpt = nullptr;
   launch(s, ssf::SsfSeg{tiles, nullptr, nullptr, h_end, dsum_seg, nullptr}, (unsigned)(S - 1), ssf::FwdKind::kStates,
-         4);
+         kWave);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const ssf::SsfSeg chain{tiles, nullptr, nullptr, h_end, dsum_seg, nullptr};
@@ -549,7 +583,7 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
                      (int)steps, h_init, dsum_pre);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  launch(a, ssf::SsfSeg{tiles, h_init, dsum_pre, nullptr, nullptr, nullptr}, (unsigned)S, kind, 4);
+  launch(a, ssf::SsfSeg{tiles, h_init, dsum_pre, nullptr, nullptr, nullptr}, (unsigned)S, kind, kWave);
   return hipGetLastError();
 }
 
