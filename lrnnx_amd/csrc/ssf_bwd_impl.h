@@ -64,7 +64,14 @@ __device__ __forceinline__ float softplus20_sig(float x, float& sg) {
 // L a multiple of 32).  A two-tile fetch reads 64 bytes of each row, half a
 // 128-byte line instead of a quarter, so each line is fetched from memory
 // about half as often; its 11 KB more LDS keep two workgroups per CU.
-template <typename IT, bool kSP, bool kZ, int kRT>
+// kCh: channels per workgroup, as in the forward.  64: lane = channel, 4
+// states per lane.  32: lane = channel + 32 half, 2 states per lane (the
+// lower half of wave w holds states 4w, 4w+1, the upper half 4w+2, 4w+3);
+// a grid of at most 256 64-channel workgroups then runs twice as many, two
+// per CU.  The channel reductions lose their cross-half stage (the halves
+// hold different states), and the per-element phases take 2 elements per
+// thread.
+template <typename IT, bool kSP, bool kZ, int kRT, int kCh = kWave>
 __global__ void __launch_bounds__(ssf::kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __restrict__ ws, const SSBwdWs wo,
                const float* __restrict__ ckp, const int64_t seg_tiles) {
@@ -72,14 +79,22 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   constexpr int kT = 16;                  // steps per tile = checkpoint interval
   static_assert(kT == kCk, "one checkpoint interval per tile");
   static_assert(kRT == kT || kRT == 2 * kT, "a raw fetch covers one or two tiles");
+  static_assert(kCh == kWave || kCh == kWave / 2, "64 or 32 channels per workgroup");
+  constexpr int kH = kWave / kCh;         // lane halves per wave
+  constexpr int kS = 4 / kH;              // states per lane
   constexpr int kPair = kRT / kT;         // tiles per raw fetch
   constexpr int kG = kT / 4;              // groups of 4 steps
   constexpr int kRow = kT * (int)sizeof(IT);    // bytes of one tile's part of a raw row
   constexpr int kRowR = kRT * (int)sizeof(IT);  // bytes of one raw row
   constexpr int kQ = kRowR / 16;          // 16-byte blocks per raw row
-  constexpr int kRaw = kWave * kRowR;     // [64][kRT] raw tile
+  constexpr int kRaw = kCh * kRowR;       // [kCh][kRT] raw tile
   constexpr int kRawS = 16 * kRowR;       // [16][kRT] raw B or C tile
-  constexpr int kOp = kG * kWave * 4;     // floats of one [g][64][4] operand tile
+  constexpr int kOp = kG * kCh * 4;       // floats of one [g][ch][4] operand tile
+  constexpr int kNP = kNW * kH;           // per-step partial sums per element (waves x halves)
+  constexpr int kEt = kCh * kT / kNT;     // elements per thread in the per-element phases (4 or 2)
+  constexpr int kP = kT / kEt;            // threads per row
+  constexpr int kQck = kCh * 4 / 16;      // 16-byte blocks of one checkpoint row (kCh fp32)
+  static_assert(kCh * kQ <= kNW * kWave && 16 * kQ <= kWave, "one fetch instruction per wave and tensor");
 
   __shared__ __attribute__((aligned(16))) char s_raw_u[kRaw];
   __shared__ __attribute__((aligned(16))) char s_raw_d[kRaw];
@@ -88,30 +103,34 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   __shared__ __attribute__((aligned(16))) char s_raw_o[kZ ? kRaw : 16];
   __shared__ __attribute__((aligned(16))) char s_raw_b[kRawS];
   __shared__ __attribute__((aligned(16))) char s_raw_c[kRawS];
-  __shared__ __attribute__((aligned(16))) float s_ck[16 * kWave];      // [n][lane] h at the tile start
-  __shared__ __attribute__((aligned(16))) float s_dl[kOp];             // [g][lane][4] delta'
+  __shared__ __attribute__((aligned(16))) float s_ck[16 * kCh];        // [n][ch] h at the tile start
+  __shared__ __attribute__((aligned(16))) float s_dl[kOp];             // [g][ch][4] delta'
   __shared__ __attribute__((aligned(16))) float s_u[kOp];              // u (epilogue)
   __shared__ __attribute__((aligned(16))) float s_x[kOp];              // delta' u (compute phases)
   __shared__ __attribute__((aligned(16))) float s_dy[kOp];             // dout silu(z)
   __shared__ __attribute__((aligned(16))) float s_sg[kSP ? kOp : 4];   // sigmoid(delta + bias)
   __shared__ __attribute__((aligned(16))) float s_B[kT * 16];          // [t][n]
   __shared__ __attribute__((aligned(16))) float s_C[kT * 16];
-  __shared__ __attribute__((aligned(16))) float s_P1[kNW * kOp];       // [w][g][lane][4] sum_k dh B
-  __shared__ __attribute__((aligned(16))) float s_P2[kNW * kOp];       // sum_k A log2(e) A_bar h_{t-1} dh
+  __shared__ __attribute__((aligned(16))) float s_P1[kNP * kOp];       // [w, half][g][ch][4] sum_k dh B
+  __shared__ __attribute__((aligned(16))) float s_P2[kNP * kOp];       // sum_k A log2(e) A_bar h_{t-1} dh
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ch = lane & (kCh - 1), hf = lane / kCh;   // the lane's channel and lane half
   const int64_t b = blockIdx.y;
   const int64_t D = a.dim, L = a.seqlen;
   const int N = (int)a.dstate;
   const int64_t cb = blockIdx.x;
-  const int64_t d0 = cb * kWave;
+  const int64_t d0 = cb * kCh;
   const int64_t grp = d0 / (D / a.n_groups);
-  const int n0 = w * kS;
-  // thread -> (row er, 4-step group eq) of the per-element phases
-  const int er = tid >> 2, eq = tid & 3;
-  constexpr int kEb = 4 * (int)sizeof(IT);  // bytes of a thread's 4 raw elements
+  const int n0w = w * 4;                 // the wave's first state
+  const int n0 = n0w + hf * kS;          // the lane's first state
+  // thread -> (row er, piece eq of kEt elements) of the per-element phases
+  const int er = tid / kP, eq = tid % kP;
+  constexpr int kEb = kEt * (int)sizeof(IT);  // bytes of a thread's raw elements
+  // the piece's slot in the [g][ch][4] operand tiles
+  const int eo = op_off<0, kCh>((eq * kEt) >> 2, er) + ((eq * kEt) & 3);
 
   const IT* gu = static_cast<const IT*>(a.u.ptr) + b * a.u.s0 + d0 * a.u.s1;
   const IT* gd = static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d0 * a.delta.s1;
@@ -120,25 +139,28 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   const IT* gos = kZ ? static_cast<const IT*>(a.out_saved.ptr) + b * a.out_saved.s0 + d0 * a.out_saved.s1 : nullptr;
   const IT* gB = static_cast<const IT*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1;
   const IT* gC = static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1;
-  IT* gdu = static_cast<IT*>(a.du.ptr) + b * a.du.s0 + (d0 + er) * a.du.s1 + 4 * eq;
-  IT* gddl = static_cast<IT*>(a.ddelta.ptr) + b * a.ddelta.s0 + (d0 + er) * a.ddelta.s1 + 4 * eq;
-  IT* gdz = kZ ? static_cast<IT*>(a.dz.ptr) + b * a.dz.s0 + (d0 + er) * a.dz.s1 + 4 * eq : nullptr;
+  IT* gdu = static_cast<IT*>(a.du.ptr) + b * a.du.s0 + (d0 + er) * a.du.s1 + kEt * eq;
+  IT* gddl = static_cast<IT*>(a.ddelta.ptr) + b * a.ddelta.s0 + (d0 + er) * a.ddelta.s1 + kEt * eq;
+  IT* gdz = kZ ? static_cast<IT*>(a.dz.ptr) + b * a.dz.s0 + (d0 + er) * a.dz.s1 + kEt * eq : nullptr;
   const uint32_t su = (uint32_t)a.u.s1, sd = (uint32_t)a.delta.s1, sdo = (uint32_t)a.dout.s1;
   const uint32_t sz = (uint32_t)a.z.s1, sos = (uint32_t)a.out_saved.s1;
   const uint32_t sBn = (uint32_t)a.B.s2, sCn = (uint32_t)a.C.s2;
-  const float* gck = ckp + b * n_ck * N * D + d0;   // checkpoint kk, state n: gck[(kk * N + n) * D + lane]
-  float* wsB = ws + wo.dBv + ((cb * a.batch + b) * N + n0 + (lane >> 4)) * L + (lane & 15);
-  float* wsC = ws + wo.dCv + ((cb * a.batch + b) * N + n0 + (lane >> 4)) * L + (lane & 15);
-  const bool wr_bc = n0 + (lane >> 4) < N;
+  const float* gck = ckp + b * n_ck * N * D + d0;   // checkpoint kk, state n: gck[(kk * N + n) * D + ch]
+  // after the reduce-scatters lane l holds state n0w + l / 16, step l % 16,
+  // summed over the block's channels (with 32 channels bit 4 pairs the lane
+  // half's two states, which puts the half's states in rows 2 hf, 2 hf + 1)
+  float* wsB = ws + wo.dBv + ((cb * a.batch + b) * N + n0w + (lane >> 4)) * L + (lane & 15);
+  float* wsC = ws + wo.dCv + ((cb * a.batch + b) * N + n0w + (lane >> 4)) * L + (lane & 15);
+  const bool wr_bc = n0w + (lane >> 4) < N;
 
   float a2[kS], gn[kS], dA_acc[kS];
 #pragma unroll
   for (int k = 0; k < kS; ++k) {
     const int n = n0 + k;
-    const float A_ = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + lane) * a.A.s0 + n * a.A.s1] : -1.f;
+    const float A_ = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + ch) * a.A.s0 + n * a.A.s1] : -1.f;
     a2[k] = A_ * kLog2e;
     // split of L: the adjoint entering this segment from the right
-    gn[k] = (wo.S > 1 && n < N) ? ws[wo.g_init + ((blockIdx.z * a.batch + b) * N + n) * D + d0 + lane] : 0.f;
+    gn[k] = (wo.S > 1 && n < N) ? ws[wo.g_init + ((blockIdx.z * a.batch + b) * N + n) * D + d0 + ch] : 0.f;
     dA_acc[k] = 0.f;
   }
   const float e_bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[(d0 + er) * a.delta_bias.s0] : 0.f;
@@ -150,74 +172,74 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   const int64_t te = tb + seg_tiles < n_tiles ? tb + seg_tiles : n_tiles;
   const int64_t prow = (int64_t)blockIdx.z * a.batch + b;  // row of the (segment, b) partials
 
-  // Tile fetches: at most one LDS-DMA instruction per wave and tensor (64
-  // rows x kQ blocks; the checkpoint row: N rows x 16 blocks), with per-lane
-  // byte offsets fixed along L; per tile only the scalar base moves.  B on
-  // wave 2, C on wave 3 (N * kQ <= 64 blocks each).
-  constexpr int kQck = kWave * 4 / 16;  // 16-byte blocks of one checkpoint row (64 fp32)
-  static_assert(kQ <= kNW, "a channel tile is at most one fetch instruction per wave");
+  // Tile fetches: at most one LDS-DMA instruction per wave and tensor (kCh
+  // rows x kQ blocks), with per-lane byte offsets fixed along L; per tile
+  // only the scalar base moves.  B on wave 2, C on wave 3 (N * kQ <= 64
+  // blocks each).  The checkpoint row: wave w fetches the 4 state rows it
+  // reads itself (4 kQck blocks).
   const uint32_t off_u = dma_lane_offset<IT, kQ>(su, w, lane);
   const uint32_t off_d = dma_lane_offset<IT, kQ>(sd, w, lane);
   const uint32_t off_do = dma_lane_offset<IT, kQ>(sdo, w, lane);
   const uint32_t off_z = kZ ? dma_lane_offset<IT, kQ>(sz, w, lane) : 0u;
   const uint32_t off_os = kZ ? dma_lane_offset<IT, kQ>(sos, w, lane) : 0u;
   const uint32_t off_bc = dma_lane_offset<IT, kQ>(w == 2 ? sBn : sCn, 0, lane);
-  const uint32_t off_ck = dma_lane_offset<float, kQck>((uint32_t)D, w, lane);
+  const int ck_row = n0w + lane / kQck;                       // state row of this lane's checkpoint block
+  const bool ck_on = lane < 4 * kQck && ck_row < N;
+  const uint32_t off_ck = ((uint32_t)ck_row * (uint32_t)D + (uint32_t)(lane % kQck) * 4u) * 4u;
   // raw tile r: steps [r kRT, (r + 1) kRT) of every input row
   auto fetch_raw = [&](int64_t r) __attribute__((always_inline)) {
     const int64_t t0 = r * kRT;
-    tile_fetch_async_s<kQ>(gu + t0, off_u, kWave, s_raw_u, w, lane);
-    tile_fetch_async_s<kQ>(gd + t0, off_d, kWave, s_raw_d, w, lane);
-    tile_fetch_async_s<kQ>(gdo + t0, off_do, kWave, s_raw_do, w, lane);
+    tile_fetch_async_s<kQ>(gu + t0, off_u, kCh, s_raw_u, w, lane);
+    tile_fetch_async_s<kQ>(gd + t0, off_d, kCh, s_raw_d, w, lane);
+    tile_fetch_async_s<kQ>(gdo + t0, off_do, kCh, s_raw_do, w, lane);
     if constexpr (kZ) {
-      tile_fetch_async_s<kQ>(gz + t0, off_z, kWave, s_raw_z, w, lane);
-      tile_fetch_async_s<kQ>(gos + t0, off_os, kWave, s_raw_o, w, lane);
+      tile_fetch_async_s<kQ>(gz + t0, off_z, kCh, s_raw_z, w, lane);
+      tile_fetch_async_s<kQ>(gos + t0, off_os, kCh, s_raw_o, w, lane);
     }
     if (w == 2) tile_fetch_async_s<kQ>(gB + t0, off_bc, N, s_raw_b, 0, lane);
     if (w == 3) tile_fetch_async_s<kQ>(gC + t0, off_bc, N, s_raw_c, 0, lane);
   };
   // h at the start of `tile` = checkpoint tile - 1 (none for tile 0)
   auto fetch_ck = [&](int64_t tile) __attribute__((always_inline)) {
-    if (tile > 0)
-      tile_fetch_async_s<kQck>(gck + (tile - 1) * N * D, off_ck, N, reinterpret_cast<char*>(s_ck), w,
-                               lane);
+    if (tile > 0 && ck_on)
+      lds_dma_16_s(gck + (tile - 1) * N * D, off_ck, reinterpret_cast<char*>(s_ck) + w * 64 * kQck);
   };
 
   // tile's part of its raw tile -> fp32 operands; dz is written here
   auto convert = [&](int64_t tile) __attribute__((always_inline)) {
-    float vu[4], vd[4], vdo[4];
+    float vu[kEt], vd[kEt], vdo[kEt];
     const int half = (int)(tile % kPair) * kRow;   // the tile's bytes within a raw row
-    const int ro = er * kRowR + half + eq * kEb;   // byte offset of this thread's 4 raw elements
-    raw4_to_f32<IT>(s_raw_u + ro, vu);
-    raw4_to_f32<IT>(s_raw_d + ro, vd);
-    raw4_to_f32<IT>(s_raw_do + ro, vdo);
-    float dy[4], sg[4];
+    const int ro = er * kRowR + half + eq * kEb;   // byte offset of this thread's raw elements
+    rawn_to_f32<IT, kEt>(s_raw_u + ro, vu);
+    rawn_to_f32<IT, kEt>(s_raw_d + ro, vd);
+    rawn_to_f32<IT, kEt>(s_raw_do + ro, vdo);
+    float dy[kEt], sg[kEt], xu[kEt];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kEt; ++i) {
       const float x = vd[i] + e_bias;
       vd[i] = kSP ? softplus20_sig(x, sg[i]) : x;
       dy[i] = vdo[i];
+      xu[i] = vd[i] * vu[i];
     }
     if constexpr (kZ) {
-      float vz[4], vo[4], dz[4];
-      raw4_to_f32<IT>(s_raw_z + ro, vz);
-      raw4_to_f32<IT>(s_raw_o + ro, vo);
+      float vz[kEt], vo[kEt], dz[kEt];
+      rawn_to_f32<IT, kEt>(s_raw_z + ro, vz);
+      rawn_to_f32<IT, kEt>(s_raw_o + ro, vo);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float sg = sigmoidf_fast(vz[i]);
-        const float zs = vz[i] * sg;
-        dz[i] = vdo[i] * vo[i] * fmaf(zs, 1.f - sg, sg);   // sg (1 + z (1 - sg))
+      for (int i = 0; i < kEt; ++i) {
+        const float sgz = sigmoidf_fast(vz[i]);
+        const float zs = vz[i] * sgz;
+        dz[i] = vdo[i] * vo[i] * fmaf(zs, 1.f - sgz, sgz);   // sg (1 + z (1 - sg))
         dy[i] = vdo[i] * zs;
       }
-      store4<IT>(gdz + tile * kT, dz);
+      storen<IT, kEt>(gdz + tile * kT, dz);
     }
-    const int o = op_off<0>(eq, er);
-    *reinterpret_cast<float4*>(&s_dl[o]) = make_float4(vd[0], vd[1], vd[2], vd[3]);
-    *reinterpret_cast<float4*>(&s_u[o]) = make_float4(vu[0], vu[1], vu[2], vu[3]);
-    *reinterpret_cast<float4*>(&s_x[o]) = make_float4(vd[0] * vu[0], vd[1] * vu[1], vd[2] * vu[2], vd[3] * vu[3]);
-    *reinterpret_cast<float4*>(&s_dy[o]) = make_float4(dy[0], dy[1], dy[2], dy[3]);
+    lds_stv<kEt>(&s_dl[eo], vd);
+    lds_stv<kEt>(&s_u[eo], vu);
+    lds_stv<kEt>(&s_x[eo], xu);
+    lds_stv<kEt>(&s_dy[eo], dy);
     // read back by this thread only, in the epilogue
-    if constexpr (kSP) *reinterpret_cast<float4*>(&s_sg[o]) = make_float4(sg[0], sg[1], sg[2], sg[3]);
+    if constexpr (kSP) lds_stv<kEt>(&s_sg[eo], sg);
     // B / C rows, transposed to step-major: threads [0, 64) B, [64, 128) C,
     // 4 steps of one state each; states >= N are zero
     if (tid < 2 * 16 * 4) {
@@ -234,38 +256,36 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
 
   // epilogue of tile: du, ddelta; dD / ddelta_bias terms
   auto epilogue = [&](int64_t tile) __attribute__((always_inline)) {
-    const int o = op_off<0>(eq, er);
-    float4 P1 = *reinterpret_cast<const float4*>(&s_P1[o]);
-    float4 P2 = *reinterpret_cast<const float4*>(&s_P2[o]);
+    float p1[kEt], p2[kEt];
+    lds_ldv<kEt>(&s_P1[eo], p1);
+    lds_ldv<kEt>(&s_P2[eo], p2);
 #pragma unroll
-    for (int ww = 1; ww < kNW; ++ww) {
-      const float4 q1 = *reinterpret_cast<const float4*>(&s_P1[ww * kOp + o]);
-      const float4 q2 = *reinterpret_cast<const float4*>(&s_P2[ww * kOp + o]);
-      P1.x += q1.x; P1.y += q1.y; P1.z += q1.z; P1.w += q1.w;
-      P2.x += q2.x; P2.y += q2.y; P2.z += q2.z; P2.w += q2.w;
-    }
-    const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[o]);
-    const float4 u4 = *reinterpret_cast<const float4*>(&s_u[o]);
-    const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[o]);
-    const float p1[4] = {P1.x, P1.y, P1.z, P1.w}, p2[4] = {P2.x, P2.y, P2.z, P2.w};
-    const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, uu[4] = {u4.x, u4.y, u4.z, u4.w};
-    const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
-    float sg[4] = {1.f, 1.f, 1.f, 1.f};
-    if constexpr (kSP) {
-      const float4 sg4 = *reinterpret_cast<const float4*>(&s_sg[o]);
-      sg[0] = sg4.x; sg[1] = sg4.y; sg[2] = sg4.z; sg[3] = sg4.w;
-    }
-    float du[4], dd[4];
+    for (int p = 1; p < kNP; ++p) {
+      float q1[kEt], q2[kEt];
+      lds_ldv<kEt>(&s_P1[p * kOp + eo], q1);
+      lds_ldv<kEt>(&s_P2[p * kOp + eo], q2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kEt; ++i) {
+        p1[i] += q1[i];
+        p2[i] += q2[i];
+      }
+    }
+    float dl[kEt], uu[kEt], dy[kEt], sg[kEt];
+    lds_ldv<kEt>(&s_dl[eo], dl);
+    lds_ldv<kEt>(&s_u[eo], uu);
+    lds_ldv<kEt>(&s_dy[eo], dy);
+    if constexpr (kSP) lds_ldv<kEt>(&s_sg[eo], sg);
+    float du[kEt], dd[kEt];
+#pragma unroll
+    for (int i = 0; i < kEt; ++i) {
       du[i] = fmaf(dl[i], p1[i], e_D * dy[i]);
       const float ddl = fmaf(uu[i], p1[i], kLn2 * p2[i]);
       dd[i] = kSP ? ddl * sg[i] : ddl;
       e_dD = fmaf(dy[i], uu[i], e_dD);
       e_dbias += dd[i];
     }
-    store4<IT>(gdu + tile * kT, du);
-    store4<IT>(gddl + tile * kT, dd);
+    storen<IT, kEt>(gdu + tile * kT, du);
+    storen<IT, kEt>(gddl + tile * kT, dd);
   };
 
   // ---- prologue: the segment's last tile (segment bounds are multiples of kPair tiles)
@@ -278,12 +298,12 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
 
   for (int64_t tile = te - 1; tile >= tb; --tile) {
     // ---- compute(tile).  The state at the tile start first: the checkpoint
-    // rows a wave reads are the rows its own fetch instruction writes (states
-    // 4w..4w+3), so once its reads have returned (lgkmcnt(0)) the wave can
-    // fetch the next tile's rows into the same buffer.
+    // rows a wave reads are the rows its own fetch writes (states 4w..4w+3),
+    // so once its reads have returned (lgkmcnt(0)) the wave can fetch the
+    // next tile's rows into the same buffer.
     float h0[kS];
 #pragma unroll
-    for (int k = 0; k < kS; ++k) h0[k] = (tile > 0 && n0 + k < N) ? s_ck[(n0 + k) * kWave + lane] : 0.f;
+    for (int k = 0; k < kS; ++k) h0[k] = (tile > 0 && n0 + k < N) ? s_ck[(n0 + k) * kCh + ch] : 0.f;
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     if (tile > tb) {
       // tile - 1 starts a new raw tile when `tile` is the first of its own
@@ -302,16 +322,17 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
         // scheduling fence: the LDS operand loads of later groups are not
         // hoisted above this group's arithmetic (that would exceed 256 VGPRs)
         __builtin_amdgcn_sched_barrier(0);
-        const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[op_off<0>(g, lane)]);
-        const float4 x4 = *reinterpret_cast<const float4*>(&s_x[op_off<0>(g, lane)]);
-        const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[op_off<0>(g, lane)]);
+        const int og = op_off<0, kCh>(g, ch);
+        const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[og]);
+        const float4 x4 = *reinterpret_cast<const float4*>(&s_x[og]);
+        const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[og]);
         const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, xx[4] = {x4.x, x4.y, x4.z, x4.w};
         const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = 4 * g + i;
-          const float4 b4 = *reinterpret_cast<const float4*>(s_B + t * 16 + n0);
-          const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+          float bv[kS];
+          lds_ldv<kS>(s_B + t * 16 + n0, bv);
           const float x = xx[i];
           float vC[kS];
 #pragma unroll
@@ -322,15 +343,18 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
             H[t][k] = hc[k];
             vC[k] = dy[i] * hc[k];
           }
-          // index bits 5, 4 of the reduce-scatter (= the wave's state k): lanes
-          // 0-31 keep states 0-1, lanes 32-63 states 2-3, then odd rows keep k odd
-          rs_step32<2>(vC);
+          // index bits 5, 4 of the reduce-scatter (= the wave's state): with 64
+          // channels lanes 0-31 keep states 0-1, lanes 32-63 states 2-3, then odd
+          // rows keep the odd state; with 32 channels the halves already hold
+          // states 0-1 and 2-3, and bit 4 (channel c with c + 16) gives odd rows
+          // the odd state
+          if constexpr (kH == 1) rs_step32<2>(vC);
           rs_step16<1>(vC);
           accC[t] = vC[0];
         }
       }
     }
-    // index bits 3..0 = step; lane l ends with state n0 + l / 16, step l % 16
+    // index bits 3..0 = step; lane l ends with state n0w + l / 16, step l % 16
     rs_tail16(accC, lane);
     const float dC_part = accC[0];
 
@@ -354,21 +378,24 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       if (t == 1) { r1 = x1; return; }
       dB_part = rs_pair(x1, r1, lane & 1, std::integral_constant<int, kDppQuadXor1>{});
     };
+    float* sP1w = s_P1 + (w * kH + hf) * kOp;   // this lane's partial slots
+    float* sP2w = s_P2 + (w * kH + hf) * kOp;
 #pragma unroll
     for (int g = kG - 1; g >= 0; --g) {
       __builtin_amdgcn_sched_barrier(0);
-      const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[op_off<0>(g, lane)]);
-      const float4 x4 = *reinterpret_cast<const float4*>(&s_x[op_off<0>(g, lane)]);
-      const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[op_off<0>(g, lane)]);
+      const int og = op_off<0, kCh>(g, ch);
+      const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[og]);
+      const float4 x4 = *reinterpret_cast<const float4*>(&s_x[og]);
+      const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[og]);
       const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
       const float xx[4] = {x4.x, x4.y, x4.z, x4.w};
       float p1v[4], p2v[4];
 #pragma unroll
       for (int i = 3; i >= 0; --i) {
         const int t = 4 * g + i;
-        const float4 b4 = *reinterpret_cast<const float4*>(s_B + t * 16 + n0);
-        const float4 c4 = *reinterpret_cast<const float4*>(s_C + t * 16 + n0);
-        const float bv[4] = {b4.x, b4.y, b4.z, b4.w}, cv[4] = {c4.x, c4.y, c4.z, c4.w};
+        float bv[kS], cv[kS];
+        lds_ldv<kS>(s_B + t * 16 + n0, bv);
+        lds_ldv<kS>(s_C + t * 16 + n0, cv);
         const float x = xx[i];
         float p1 = 0.f, p2 = 0.f, vB[kS];
 #pragma unroll
@@ -384,12 +411,12 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
         }
         p1v[i] = p1;
         p2v[i] = p2;
-        rs_step32<2>(vB);
+        if constexpr (kH == 1) rs_step32<2>(vB);
         rs_step16<1>(vB);
         stream_dB(t, vB[0]);
       }
-      *reinterpret_cast<float4*>(&s_P1[w * kOp + op_off<0>(g, lane)]) = make_float4(p1v[0], p1v[1], p1v[2], p1v[3]);
-      *reinterpret_cast<float4*>(&s_P2[w * kOp + op_off<0>(g, lane)]) = make_float4(p2v[0], p2v[1], p2v[2], p2v[3]);
+      *reinterpret_cast<float4*>(&sP1w[og]) = make_float4(p1v[0], p1v[1], p1v[2], p1v[3]);
+      *reinterpret_cast<float4*>(&sP2w[og]) = make_float4(p2v[0], p2v[1], p2v[2], p2v[3]);
     }
 
     // ---- finish(tile).  The wait covers the fetch of tile - 1 and the stores
@@ -409,12 +436,16 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   // the rows by ss_reduce_batch_kernel
 #pragma unroll
   for (int k = 0; k < kS; ++k)
-    if (n0 + k < N) ws[wo.dA + (prow * D + d0 + lane) * N + n0 + k] = dA_acc[k];
-  // dD / ddelta_bias: the 4 threads of a channel are consecutive lanes
+    if (n0 + k < N) ws[wo.dA + (prow * D + d0 + ch) * N + n0 + k] = dA_acc[k];
+  // dD / ddelta_bias: the kP threads of a channel are consecutive lanes
   e_dD += dpp_mov<kDppQuadXor1>(e_dD);
   e_dD += dpp_mov<kDppQuadXor2>(e_dD);
   e_dbias += dpp_mov<kDppQuadXor1>(e_dbias);
   e_dbias += dpp_mov<kDppQuadXor2>(e_dbias);
+  if constexpr (kP == 8) {
+    e_dD += __shfl_xor(e_dD, 4);
+    e_dbias += __shfl_xor(e_dbias, 4);
+  }
   if (eq == 0) {
     ws[wo.dD + prow * D + d0 + er] = e_dD;
     ws[wo.dbias + prow * D + d0 + er] = e_dbias;
@@ -516,6 +547,32 @@ inline int64_t ssf_bwd_segs(const lrnnx_selective_scan_args& a) {
   return steps ? ssf::n_segs(a, steps) : 1;
 }
 
+// Channels per workgroup of the fast backward (64 or 32), from shapes and
+// options only, so that the workspace layout and the launch agree: 32 for an
+// unsplit grid of at most 256 64-channel workgroups (with 16-bit I/O only
+// together with two-tile fetches, L a multiple of 32), else 64.
+// LRNNX_SCAN_CHANNELS forces either where 32 is possible.
+template <typename IT>
+inline int ssf_bwd_chans(const lrnnx_selective_scan_args& a) {
+  if (!ssf::shape_ok<IT>(a, ssf::kCk) || ssf_bwd_segs<IT>(a) > 1) return kWave;
+  if (sizeof(IT) == 2 && a.seqlen % (2 * ssf::kCk) != 0) return kWave;
+  const int o = scan_channels_override();
+  if (o) return o;
+  return (a.dim / kWave) * a.batch <= 256 ? kWave / 2 : kWave;
+}
+
+// The backward's geometry: channel blocks of the fast kernel's width (the
+// dB / dC partials are per channel block).
+template <typename IT>
+inline SSGeom ssf_bwd_geom(const lrnnx_selective_scan_args& a) {
+  SSGeom g = ss_geom(a);
+  if (ssf_bwd_chans<IT>(a) == kWave / 2) {
+    g.CB = kWave / 2;
+    g.n_cb = (int)(a.dim / g.CB);
+  }
+  return g;
+}
+
 template <typename IT, bool kSP, bool kZ>
 inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                              const float* ckp, int64_t seg_steps, hipStream_t st) {
@@ -523,6 +580,7 @@ inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g
   // number of tiles: L a multiple of 32 (the split's segments are powers of
   // two >= 128 steps).
   constexpr bool kTwo = sizeof(IT) == 2;
+  const bool c32 = g.CB == kWave / 2;
   const int64_t S = wo.S, B = a.batch, D = a.dim, N = a.dstate;
   const int64_t seg_tiles = S > 1 ? seg_steps / ssf::kCk : a.seqlen / ssf::kCk;
   if (S > 1) {
@@ -532,21 +590,34 @@ inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g
     hipLaunchKernelGGL(ssf_bwd_adj_chain_kernel<IT>, dim3((unsigned)((nch + 255) / 256)), dim3(256), 0, st, a, (int)S,
                        ws, wo);
   }
-  const dim3 grid((unsigned)(a.dim / kWave), (unsigned)a.batch, (unsigned)S);
+  const dim3 grid((unsigned)(a.dim / g.CB), (unsigned)a.batch, (unsigned)S);
+  const dim3 blk(ssf::kNT);
   if constexpr (kTwo) {
     if (a.seqlen % (2 * ssf::kCk) == 0) {
-      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk>), grid, dim3(ssf::kNT), 0, st, a, g.n_ck, ws, wo,
-                         ckp, seg_tiles);
+      if (c32)
+        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave / 2>), grid, blk, 0, st, a, g.n_ck, ws,
+                           wo, ckp, seg_tiles);
+      else
+        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave>), grid, blk, 0, st, a, g.n_ck, ws, wo,
+                           ckp, seg_tiles);
       return;
     }
+    // (the 32-channel form comes with two-tile fetches only: ssf_bwd_chans)
+    hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+                       seg_tiles);
+  } else {
+    if (c32)
+      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave / 2>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+                         seg_tiles);
+    else
+      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+                         seg_tiles);
   }
-  hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk>), grid, dim3(ssf::kNT), 0, st, a, g.n_ck, ws, wo, ckp,
-                     seg_tiles);
 }
 
 template <typename IT>
 inline hipError_t ssf_bwd_launch(const lrnnx_selective_scan_args& a, float* ws, const float* ckp, hipStream_t st) {
-  const SSGeom g = ss_geom(a);
+  const SSGeom g = ssf_bwd_geom<IT>(a);
   const int64_t S = ssf_bwd_segs<IT>(a);
   const SSBwdWs wo = ss_bwd_ws(a, g, a.ckpt == nullptr, S);
   const int64_t steps = S > 1 ? ssf::seg_steps(a) : 0;

@@ -217,6 +217,40 @@ __device__ __forceinline__ void raw4_to_f32(const char* p, float* out) {
   }
 }
 
+// 2 consecutive elements at LDS byte address p (4-byte aligned for 16-bit
+// types, 8-byte for f32) -> floats
+template <typename IT>
+__device__ __forceinline__ void raw2_to_f32(const char* p, float* out) {
+  if constexpr (sizeof(IT) == 4) {
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    out[0] = v.x; out[1] = v.y;
+  } else {
+    const uint32_t raw = *reinterpret_cast<const uint32_t*>(p);
+    const IT* e = reinterpret_cast<const IT*>(&raw);
+    out[0] = to_f32(e[0]);
+    out[1] = to_f32(e[1]);
+  }
+}
+
+// kN (4 or 2) consecutive raw elements at LDS byte address p -> floats
+template <typename IT, int kN>
+__device__ __forceinline__ void rawn_to_f32(const char* p, float* out) {
+  if constexpr (kN == 4) raw4_to_f32<IT>(p, out);
+  else raw2_to_f32<IT>(p, out);
+}
+
+// 2 floats -> 2 consecutive elements at global address p (one 4- or 8-byte store)
+template <typename IT>
+__device__ __forceinline__ void store2(IT* p, const float* v) {
+  if constexpr (sizeof(IT) == 4) {
+    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+  } else {
+    float w8[8] = {v[0], v[1], 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const uint4 raw = f32_to_raw<IT>(w8);
+    *reinterpret_cast<uint32_t*>(p) = raw.x;
+  }
+}
+
 // 4 floats -> 4 consecutive elements at global address p (one 8- or 16-byte store)
 template <typename IT>
 __device__ __forceinline__ void store4(IT* p, const float* v) {
@@ -227,6 +261,12 @@ __device__ __forceinline__ void store4(IT* p, const float* v) {
     const uint4 raw = f32_to_raw<IT>(w8);
     *reinterpret_cast<uint2*>(p) = make_uint2(raw.x, raw.y);
   }
+}
+
+template <typename IT, int kN>
+__device__ __forceinline__ void storen(IT* p, const float* v) {
+  if constexpr (kN == 4) store4<IT>(p, v);
+  else store2<IT>(p, v);
 }
 
 // fast transcendental helpers (v_exp_f32 / v_log_f32 / v_rcp_f32)
