@@ -458,15 +458,17 @@ int scan_channels_override();   // capi.hip: LRNNX_SCAN_CHANNELS
 
 namespace ssf {
 // Steps per segment of the L split: 0 (no split) when the split is switched
-// off (l_split_enabled) or for grids of more than 128
-// workgroups (B * D / 64; half the CUs), where the summary pass costs more than
-// the added parallelism gains (measured: 192 workgroups ran 16 % slower
-// split), else the shortest power of two >= 128 steps that keeps the grid at
-// most 512 workgroups.  Powers of two keep every 2048-step chunk boundary on a
+// off (l_split_enabled) or for grids of more than 64 workgroups (B * D / 64),
+// which run unsplit in 32-channel workgroups (chans_for) on at least half the
+// CUs; there the split's summary pass costs more than its parallelism gains
+// (measured at 96 and 128 workgroups, L = 2048: unsplit fwd 0.145-0.151 ms /
+// bwd 0.37-0.39 ms against split 0.155-0.167 / 0.41-0.47 ms).  Otherwise the
+// shortest power of two >= 128 steps that keeps the grid at most 512
+// workgroups.  Powers of two keep every 2048-step chunk boundary on a
 // segment boundary and are multiples of every tile length.
 inline int64_t seg_steps(const lrnnx_selective_scan_args& a) {
   const int64_t wgs = (a.dim / kWave) * a.batch;
-  if (wgs > 128 || !l_split_enabled()) return 0;
+  if (wgs > 64 || !l_split_enabled()) return 0;
   int64_t steps = 128;
   while (steps < a.seqlen && wgs * ((a.seqlen + steps - 1) / steps) > 512) steps *= 2;
   return steps < a.seqlen ? steps : 0;
