@@ -116,6 +116,14 @@ __device__ __forceinline__ float dpp_mov(float v) {
   return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), CTRL, 0xf, 0xf, false));
 }
 
+// The same with no old value (every lane of these patterns reads a lane of
+// its own row): nothing to initialise, so the move can fold into an FMA's
+// addend or a VOP2 operand without an extra v_mov.
+template <int CTRL>
+__device__ __forceinline__ float dpp_get(float v) {
+  return __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(v), CTRL, 0xf, 0xf, true));
+}
+
 // DPP control words (GFX9 encoding)
 constexpr int kDppQuadXor1 = 0xb1;        // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4e;        // quad_perm [2,3,0,1]

@@ -126,6 +126,17 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   const int64_t grp = d0 / (D / a.n_groups);
   const int n0w = w * 4;                 // the wave's first state
   const int n0 = n0w + hf * kS;          // the lane's first state
+  // State order of the lane's registers: register k holds state n0 + (k ^ sm)
+  // with sm from lane bits 3 and 2 (4 states: 2 b3 + (b2 ^ b3)) or bit 3 (2
+  // states).  The DPP row mirror (lane i <-> 15 - i) flips sm's bit 1 (bit 0
+  // with 2 states) and the half-row mirror (i <-> 7 - i) its bit 0, so the
+  // first dB / dC reduce-scatter stages, over lane bits 3 and 2, pair
+  // registers that hold the same state in both lanes: one DPP add per pair.
+  const int lb2 = (lane >> 2) & 1, lb3 = (lane >> 3) & 1;
+  const int sm = kS == 4 ? 2 * lb3 + (lb2 ^ lb3) : lb3;
+  int ns[kS];
+#pragma unroll
+  for (int k = 0; k < kS; ++k) ns[k] = n0 + (k ^ sm);
   // thread -> (row er, piece eq of kEt elements) of the per-element phases
   const int er = tid / kP, eq = tid % kP;
   constexpr int kEb = kEt * (int)sizeof(IT);  // bytes of a thread's raw elements
@@ -146,17 +157,19 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   const uint32_t sz = (uint32_t)a.z.s1, sos = (uint32_t)a.out_saved.s1;
   const uint32_t sBn = (uint32_t)a.B.s2, sCn = (uint32_t)a.C.s2;
   const float* gck = ckp + b * n_ck * N * D + d0;   // checkpoint kk, state n: gck[(kk * N + n) * D + ch]
-  // after the reduce-scatters lane l holds state n0w + l / 16, step l % 16,
-  // summed over the block's channels (with 32 channels bit 4 pairs the lane
-  // half's two states, which puts the half's states in rows 2 hf, 2 hf + 1)
-  float* wsB = ws + wo.dBv + ((cb * a.batch + b) * N + n0w + (lane >> 4)) * L + (lane & 15);
-  float* wsC = ws + wo.dCv + ((cb * a.batch + b) * N + n0w + (lane >> 4)) * L + (lane & 15);
-  const bool wr_bc = n0w + (lane >> 4) < N;
+  // after the reduce-scatters lane l holds state ns[0] = n0 + sm and step
+  // rs_step(l) of the tile, summed over the block's channels
+  const int rs_n = ns[0];
+  const int rs_t = kH == 1 ? 8 * ((lane >> 4) & 1) + 4 * ((lane >> 5) & 1) + (lane & 3)
+                           : 8 * lb2 + 4 * ((lane >> 4) & 1) + (lane & 3);
+  float* wsB = ws + wo.dBv + ((cb * a.batch + b) * N + rs_n) * L + rs_t;
+  float* wsC = ws + wo.dCv + ((cb * a.batch + b) * N + rs_n) * L + rs_t;
+  const bool wr_bc = rs_n < N;
 
   float a2[kS], gn[kS], dA_acc[kS];
 #pragma unroll
   for (int k = 0; k < kS; ++k) {
-    const int n = n0 + k;
+    const int n = ns[k];
     const float A_ = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + ch) * a.A.s0 + n * a.A.s1] : -1.f;
     a2[k] = A_ * kLog2e;
     // split of L: the adjoint entering this segment from the right
@@ -303,16 +316,76 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     // next tile's rows into the same buffer.
     float h0[kS];
 #pragma unroll
-    for (int k = 0; k < kS; ++k) h0[k] = (tile > 0 && n0 + k < N) ? s_ck[(n0 + k) * kCh + ch] : 0.f;
+    for (int k = 0; k < kS; ++k) h0[k] = (tile > 0 && ns[k] < N) ? s_ck[ns[k] * kCh + ch] : 0.f;
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     if (tile > tb) {
       // tile - 1 starts a new raw tile when `tile` is the first of its own
       if (tile % kPair == 0) fetch_raw((tile - 1) / kPair);
       fetch_ck(tile - 1);
     }
+    // Reduce-scatter of the dB / dC values over the block's channels (the
+    // lanes, with 32 channels each lane half on its own).  Stage 1, per step:
+    // the lane's kS states over lane bits 3 (row mirror) and 2 (half-row
+    // mirror, 4 states only), one DPP add per pair thanks to the register
+    // order above; the lane keeps state ns[0].  Stage 2, streamed over the
+    // tile's 16 steps as they exist: step bit 3 pairs t with t + 8 over lane
+    // bit 4 (32 channels: bit 2, bank-masked DPP), step bit 2 t with t + 4
+    // over lane bit 5 (32 channels: bit 4), then step bits 1 and 0 over lane
+    // bits 1 and 0 (quad DPP), so at most 8 partials live; the lane ends with
+    // step rs_t.
+    auto rs_states = [&](const float (&v)[kS]) __attribute__((always_inline)) {
+      if constexpr (kS == 4) {
+        const float a0 = v[0] + dpp_get<kDppRowMirror>(v[2]);
+        const float a1 = v[1] + dpp_get<kDppRowMirror>(v[3]);
+        return a0 + dpp_get<kDppRowHalfMirror>(a1);
+      } else {
+        return v[0] + dpp_get<kDppRowMirror>(v[1]);
+      }
+    };
+    auto rs_pair = [&](float lo, float hi, bool bit, auto ctrl) __attribute__((always_inline)) {
+      const float keep = bit ? hi : lo;
+      const float send = bit ? lo : hi;
+      return keep + dpp_mov<decltype(ctrl)::value>(send);
+    };
+    auto swap_add16 = [&](float lo, float hi) __attribute__((always_inline)) {   // even rows keep lo
+      auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+      return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    };
+    auto swap_add32 = [&](float lo, float hi) __attribute__((always_inline)) {   // lanes < 32 keep lo
+      auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+      return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    };
+    auto rs_b3 = [&](float lo, float hi) __attribute__((always_inline)) {
+      if constexpr (kH == 1) return swap_add16(lo, hi);
+      else return rs_pair_banked<4>(lo, hi);
+    };
+    auto rs_b2 = [&](float lo, float hi) __attribute__((always_inline)) {
+      if constexpr (kH == 1) return swap_add32(lo, hi);
+      else return swap_add16(lo, hi);
+    };
+    auto rs_b1 = [&](float lo, float hi) __attribute__((always_inline)) {
+      return rs_pair(lo, hi, lane & 2, std::integral_constant<int, kDppQuadXor2>{});
+    };
+    auto rs_b0 = [&](float lo, float hi) __attribute__((always_inline)) {
+      return rs_pair(lo, hi, lane & 1, std::integral_constant<int, kDppQuadXor1>{});
+    };
     // recompute A_bar and h over the tile; dC_t = sum_d dy_t h_t is complete
-    // here, so its reduce-scatter runs before the reverse walk
-    float AB[kT][kS], H[kT][kS], accC[kT];
+    // here, so its reduce-scatter runs with it (steps in increasing order)
+    float AB[kT][kS], H[kT][kS];
+    float c8[8], c4[4], c2[2], c1 = 0.f, dC_part = 0.f;
+    auto stream_dC = [&](int t, float v) __attribute__((always_inline)) {
+      if (t < 8) { c8[t] = v; return; }
+      const int j = t - 8;
+      const float x3 = rs_b3(c8[j], v);
+      if (j < 4) { c4[j] = x3; return; }
+      const int k = j - 4;
+      const float x2 = rs_b2(c4[k], x3);
+      if (k < 2) { c2[k] = x2; return; }
+      const int q = k - 2;
+      const float x1 = rs_b1(c2[q], x2);
+      if (q == 0) { c1 = x1; return; }
+      dC_part = rs_b0(c1, x1);
+    };
     {
       float hc[kS];
 #pragma unroll
@@ -332,7 +405,8 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
         for (int i = 0; i < 4; ++i) {
           const int t = 4 * g + i;
           float bv[kS];
-          lds_ldv<kS>(s_B + t * 16 + n0, bv);
+#pragma unroll
+          for (int k = 0; k < kS; ++k) bv[k] = s_B[t * 16 + ns[k]];
           const float x = xx[i];
           float vC[kS];
 #pragma unroll
@@ -343,40 +417,22 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
             H[t][k] = hc[k];
             vC[k] = dy[i] * hc[k];
           }
-          // index bits 5, 4 of the reduce-scatter (= the wave's state): with 64
-          // channels lanes 0-31 keep states 0-1, lanes 32-63 states 2-3, then odd
-          // rows keep the odd state; with 32 channels the halves already hold
-          // states 0-1 and 2-3, and bit 4 (channel c with c + 16) gives odd rows
-          // the odd state
-          if constexpr (kH == 1) rs_step32<2>(vC);
-          rs_step16<1>(vC);
-          accC[t] = vC[0];
+          stream_dC(t, rs_states(vC));
         }
       }
     }
-    // index bits 3..0 = step; lane l ends with state n0w + l / 16, step l % 16
-    rs_tail16(accC, lane);
-    const float dC_part = accC[0];
 
-    // reverse walk; the last four reduce-scatter stages of dB (index bits 3..0
-    // = step) run as a butterfly that consumes step t as soon as it exists:
-    // bit 3 pairs t with t + 8, bit 2 t with t + 4, bit 1 t with t + 2, bit 0
-    // 0 with 1 (rs_tail16 applied in step order), so at most 8 partials live
+    // reverse walk; dB's reduce-scatter as dC's, steps in decreasing order
     float r8[8], r4[4], r2[2], r1 = 0.f, dB_part = 0.f;
-    auto rs_pair = [&](float lo, float hi, bool bit, auto ctrl) __attribute__((always_inline)) {
-      const float keep = bit ? hi : lo;
-      const float send = bit ? lo : hi;
-      return keep + dpp_mov<decltype(ctrl)::value>(send);
-    };
     auto stream_dB = [&](int t, float v) __attribute__((always_inline)) {
       if (t >= 8) { r8[t - 8] = v; return; }
-      const float x3 = rs_pair_banked<8>(v, r8[t]);
+      const float x3 = rs_b3(v, r8[t]);
       if (t >= 4) { r4[t - 4] = x3; return; }
-      const float x2 = rs_pair_banked<4>(x3, r4[t]);
+      const float x2 = rs_b2(x3, r4[t]);
       if (t >= 2) { r2[t - 2] = x2; return; }
-      const float x1 = rs_pair(x2, r2[t], lane & 2, std::integral_constant<int, kDppQuadXor2>{});
+      const float x1 = rs_b1(x2, r2[t]);
       if (t == 1) { r1 = x1; return; }
-      dB_part = rs_pair(x1, r1, lane & 1, std::integral_constant<int, kDppQuadXor1>{});
+      dB_part = rs_b0(x1, r1);
     };
     float* sP1w = s_P1 + (w * kH + hf) * kOp;   // this lane's partial slots
     float* sP2w = s_P2 + (w * kH + hf) * kOp;
@@ -394,8 +450,11 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       for (int i = 3; i >= 0; --i) {
         const int t = 4 * g + i;
         float bv[kS], cv[kS];
-        lds_ldv<kS>(s_B + t * 16 + n0, bv);
-        lds_ldv<kS>(s_C + t * 16 + n0, cv);
+#pragma unroll
+        for (int k = 0; k < kS; ++k) {
+          bv[k] = s_B[t * 16 + ns[k]];
+          cv[k] = s_C[t * 16 + ns[k]];
+        }
         const float x = xx[i];
         float p1 = 0.f, p2 = 0.f, vB[kS];
 #pragma unroll
@@ -411,9 +470,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
         }
         p1v[i] = p1;
         p2v[i] = p2;
-        if constexpr (kH == 1) rs_step32<2>(vB);
-        rs_step16<1>(vB);
-        stream_dB(t, vB[0]);
+        stream_dB(t, rs_states(vB));
       }
       *reinterpret_cast<float4*>(&sP1w[og]) = make_float4(p1v[0], p1v[1], p1v[2], p1v[3]);
       *reinterpret_cast<float4*>(&sP2w[og]) = make_float4(p2v[0], p2v[1], p2v[2], p2v[3]);
@@ -436,7 +493,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   // the rows by ss_reduce_batch_kernel
 #pragma unroll
   for (int k = 0; k < kS; ++k)
-    if (n0 + k < N) ws[wo.dA + (prow * D + d0 + ch) * N + n0 + k] = dA_acc[k];
+    if (ns[k] < N) ws[wo.dA + (prow * D + d0 + ch) * N + ns[k]] = dA_acc[k];
   // dD / ddelta_bias: the kP threads of a channel are consecutive lanes
   e_dD += dpp_mov<kDppQuadXor1>(e_dD);
   e_dD += dpp_mov<kDppQuadXor2>(e_dD);
