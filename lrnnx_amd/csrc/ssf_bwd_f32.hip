@@ -9,26 +9,6 @@ bool ssf_bwd_f32(const lrnnx_selective_scan_args& a, float* ws, const float* ckp
   return true;
 }
 
-// Checkpoint rebuild of a backward given no checkpoints, on the fast
-// forward's states-only kernel: into `ckpt` (the workspace's section), split
-// like the forward on small grids (`fws`: the section for its summaries) or
-// chunk-parallel from the x carries; returns false when the fast forward does
-// not cover the call.
-bool ssf_ckpt_rebuild_f32(const lrnnx_selective_scan_args& a, float* ckpt, float* fws, int64_t fws_bytes,
-                        const float* x, hipStream_t st, hipError_t* err) {
-  if (!ssf::shape_ok<float>(a, ssf::tile_steps<float>())) return false;
-  lrnnx_selective_scan_args f = a;
-  f.ckpt = ckpt;
-  f.out.ptr = nullptr;
-  f.out_z.ptr = nullptr;
-  f.z.ptr = nullptr;
-  f.x = nullptr;
-  f.workspace = fws;
-  f.workspace_bytes = fws_bytes;
-  *err = ssf_fwd_launch<float>(f, ss_geom(a).n_ck, st, true, x);
-  return true;
-}
-
 // The backward's geometry for this call (the fast kernel's channel blocks
 // when it covers the call), for the workspace layout queries.
 SSGeom ssf_bwd_geometry(const lrnnx_selective_scan_args& a) {

@@ -16,4 +16,24 @@ int64_t ssf_fwd_workspace_bytes(const lrnnx_selective_scan_args& a) {
     default: return ssf_fwd_ws_bytes<f16>(a);
   }
 }
+
+// Checkpoint rebuild of a backward given no checkpoints, on the fast
+// forward's states-only kernel: into `ckpt` (the workspace's section), split
+// like the forward on small grids (`fws`: the section for its summaries) or
+// chunk-parallel from the x carries; returns false when the fast forward does
+// not cover the call.
+bool ssf_ckpt_rebuild_f32(const lrnnx_selective_scan_args& a, float* ckpt, float* fws, int64_t fws_bytes,
+                        const float* x, hipStream_t st, hipError_t* err) {
+  if (!ssf::shape_ok<float>(a, ssf::tile_steps<float>())) return false;
+  lrnnx_selective_scan_args f = a;
+  f.ckpt = ckpt;
+  f.out.ptr = nullptr;
+  f.out_z.ptr = nullptr;
+  f.z.ptr = nullptr;
+  f.x = nullptr;
+  f.workspace = fws;
+  f.workspace_bytes = fws_bytes;
+  *err = ssf_fwd_launch<float>(f, ss_geom(a).n_ck, st, true, x);
+  return true;
+}
 }  // namespace lrnnx

@@ -299,12 +299,12 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
       }
     }
   };
-  // fp32 state after step t_end - 1 (t_end a multiple of kCk): checkpoint t_end / kCk - 1
-  auto store_ckpt = [&](int64_t t_end) __attribute__((always_inline)) {
+  // fp32 state hv after step t_end - 1 (t_end a multiple of kCk): checkpoint t_end / kCk - 1
+  auto store_ckpt = [&](int64_t t_end, const float* hv) __attribute__((always_inline)) {
     float* cp = ckp + ((b * n_ck + t_end / kCk - 1) * N + n0) * D + d0 + ch;
 #pragma unroll
     for (int k = 0; k < kS; ++k)
-      if (n0 + k < N) cp[(int64_t)k * D] = h[k];
+      if (n0 + k < N) cp[(int64_t)k * D] = hv[k];
   };
   auto chunk_end = [&](int64_t tile) __attribute__((always_inline)) {
     return ((tile + 1) * kT) % kXChunk == 0 || tile + 1 == n_tiles;
@@ -324,6 +324,8 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
 
     // ---- compute(tile)
     const int64_t t0 = tile * kT;
+    constexpr int kMid = kT > kCk ? kT / kCk - 1 : 0;   // checkpoints inside a tile
+    float hmid[kMid > 0 ? kMid : 1][kS];
 #pragma unroll
     for (int g = 0; g < kG; ++g) {
       const int og = op_off<kSh, kCh>(g, ch);
@@ -350,16 +352,24 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
         y[i] = acc;
       }
       if constexpr (kOut) *reinterpret_cast<float4*>(sYw + og) = make_float4(y[0], y[1], y[2], y[3]);
-      // checkpoints inside the tile; the one at the tile end is stored after
-      // the barrier below, so that the wait before it does not wait for it
-      if (ckp != nullptr && ((4 * g + 4) % kCk) == 0 && 4 * g + 4 < kT) store_ckpt(t0 + 4 * g + 4);
+      // checkpoints inside the tile: kept in registers and stored after the
+      // barrier below with the one at the tile end, so that the wait before
+      // the barrier (for the next tile's fetch) does not wait for them
+      if (ckp != nullptr && ((4 * g + 4) % kCk) == 0 && 4 * g + 4 < kT) {
+#pragma unroll
+        for (int k = 0; k < kS; ++k) hmid[(4 * g + 4) / kCk - 1][k] = h[k];
+      }
     }
 
     // ---- finish(tile).  The wait covers the fetch of tile + 1 and the stores
     // of the previous finish phase.
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
-    if (ckp != nullptr) store_ckpt(t0 + kT);
+    if (ckp != nullptr) {
+#pragma unroll
+      for (int m = 0; m < kMid; ++m) store_ckpt(t0 + (m + 1) * kCk, hmid[m]);
+      store_ckpt(t0 + kT, h);
+    }
     if constexpr (kOut) epilogue(tile);
     if (chunk_end(tile)) {
       s_dsum[tid] = e_dsum;
