@@ -10,7 +10,8 @@ autograd of the restated selective_scan_ref, lrnnx/ops/selective_scan.py:
   moderate L): bf16 B=3 D=2816 L=1024 and fp32 B=2 D=4160 L=512.
 * The small-grid split of L against the unsplit schedule
   (LRNNX_SCAN_NO_SPLIT=1) at B=1 D=64 L=4160, both against the oracle.
-* 64 and 32 channels per workgroup (LRNNX_SCAN_CHANNELS) on one unsplit grid, and the
+* 64 and 32 channels per workgroup (LRNNX_SCAN_CHANNELS) on one unsplit grid, both forms
+  with d_state 9 and 13 (waves whose states are part real, part padding), and the
   32-channel form with padded states, groups and several chunk ends.
 * The binding's own call sequence ``selective_scan_cuda.fwd`` -> ``bwd(x)``
   in both save modes: "checkpoints" (fwd attaches them to x) and "x" (the
@@ -231,6 +232,25 @@ def test_channels_per_workgroup_64_and_32_vs_oracle(dev, monkeypatch, itype, wit
     for name in res["64"]:
         if res["64"][name] is not None:
             close_dev(f"{name} 32 vs 64 channels", res["32"][name], res["64"][name].double(), *_tol_of(name, itype))
+
+
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N", [9, 13])
+@pytest.mark.parametrize("chans", ["64", "32"])
+def test_partially_padded_wave_states_vs_oracle(dev, monkeypatch, itype, N, chans):
+    """d_state 9 and 13: one wave's four states are part real, part padding,
+    in both channel forms (LRNNX_SCAN_CHANNELS).  The backward's dB / dC
+    reduce-scatter gives each lane its states in a lane-dependent register
+    order, so real and padded states share registers across lanes, and a
+    lane writes its partial only where the state it ends with is real."""
+    monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", "1")
+    monkeypatch.setenv("LRNNX_SCAN_CHANNELS", chans)
+    inp = _gpu_inputs(dev, 2, 128, 512, N, 41 + N, itype)
+    ref = _oracle(inp)
+    print(f"[padded states] N={N} channels={chans} {itype}", flush=True)
+    got = _run_fn(inp)
+    for name in ("out", "last_state", "du", "ddelta", "dz", "dA", "dB", "dC", "dD", "ddelta_bias"):
+        close_dev(f"{name} N={N} channels={chans}", got[name], ref[name], *_tol_of(name, itype))
 
 
 @pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
