@@ -531,9 +531,10 @@ def cpu_configs(torch, R):
 def method_configs(torch, dev):
     """fwd+bwd through the autograd wrappers for the other discretisations and
     weight types at B=8, D=1536, L=2048 (fp32, event-timed medians of 10): the
-    general kernels (zoh / bilinear / dirac, N=16, variable B/C), the
-    one-state fast path (rglru N=1; the s7 binding call with 256 S7 states) and
-    the complex-weight kernels (N=16)."""
+    general kernels (zoh / bilinear, N=16, variable B/C), dirac on the fast
+    kernels and, for comparison, on the general ones (LRNNX_SCAN_GENERIC=1),
+    the one-state fast path (rglru N=1; the s7 binding call with 256 S7 states)
+    and the complex-weight kernels (N=16)."""
     import lrnnx_amd as lx
     from lrnnx_amd import selective_scan_cuda as ssb
 
@@ -562,6 +563,17 @@ def method_configs(torch, dev):
         def fb(m=m):
             lx.selective_scan_fn(u, dl, A, B, C, None, None, None, None, True, discretization=m).backward(dout)
         res[f"{m}_n16_fwd_bwd_ms"] = med(fb)
+    prev = os.environ.get("LRNNX_SCAN_GENERIC")
+    os.environ["LRNNX_SCAN_GENERIC"] = "1"
+    try:
+        res["dirac_n16_generic_fwd_bwd_ms"] = med(
+            lambda: lx.selective_scan_fn(u, dl, A, B, C, None, None, None, None, True,
+                                         discretization="dirac").backward(dout))
+    finally:
+        if prev is None:
+            del os.environ["LRNNX_SCAN_GENERIC"]
+        else:
+            os.environ["LRNNX_SCAN_GENERIC"] = prev
     dr = (8 * torch.rand(Bt, D, L, device=dev, generator=g)).requires_grad_()
     a1 = (0.5 * torch.rand(D, 1, device=dev, generator=g) + 0.45).requires_grad_()
     res["rglru_n1_fwd_bwd_ms"] = med(lambda: lx.rglru_scan_fn(u, dr, a1).backward(dout))

@@ -90,7 +90,7 @@ int64_t lrnnx_selective_scan_ckpt_size(const lrnnx_selective_scan_args *a);
 
 /* Bytes of workspace the call needs (bwd = 0: forward, 1: backward).  The
  * forward's is optional: given at least this many bytes (16-byte aligned), the
- * mamba fast path splits L into segments when batch * dim / 64 workgroups are
+ * fast path (methods mamba and dirac) splits L into segments when batch * dim / 64 workgroups are
  * too few to fill the GPU (a segment summary pass, a carry chain, then every
  * segment from its initial state); without it the forward runs unsplit.  It
  * is 0 when the call would not split.  No reference counterpart (the

@@ -112,6 +112,10 @@ const char* method_name(int m) {
 }
 
 
+// Methods with a fast path: "mamba" at every input type, "dirac" (whose
+// input is fp32).
+bool has_fast_path(int method) { return method == LRNNX_MAMBA || method == LRNNX_DIRAC; }
+
 // Forward of the "mamba" method: fast path when it covers the call, else the
 // generic kernel.
 hipError_t fwd_mamba(const lrnnx_selective_scan_args& a, hipStream_t st) {
@@ -144,6 +148,19 @@ hipError_t bwd_mamba(const lrnnx_selective_scan_args& a, float* ws, const float*
     case LRNNX_BF16: return ss_bwd_mamba_bf16(a, ws, ckp, st);
     default: return ss_bwd_mamba_f16(a, ws, ckp, st);
   }
+}
+
+// Forward / backward of the other real methods (fp32 input): the fast path
+// for "dirac" when it covers the call, else the generic kernels.
+hipError_t fwd_other(const lrnnx_selective_scan_args& a, hipStream_t st) {
+  hipError_t e = hipSuccess;
+  if (a.method == LRNNX_DIRAC && fast_paths_enabled() && ssf_fwd_f32(a, st, &e)) return e;
+  return ss_fwd_other_f32(a, st);
+}
+hipError_t bwd_other(const lrnnx_selective_scan_args& a, float* ws, const float* ckp, hipStream_t st) {
+  hipError_t e = hipSuccess;
+  if (a.method == LRNNX_DIRAC && fast_paths_enabled() && ssf_bwd_f32(a, ws, ckp, st, &e)) return e;
+  return ss_bwd_other_f32(a, ws, ckp, st);
 }
 
 int check_ss(const lrnnx_selective_scan_args* a, bool bwd) {
@@ -233,7 +250,7 @@ int64_t lrnnx_selective_scan_ckpt_size(const lrnnx_selective_scan_args* a) {
 int64_t lrnnx_selective_scan_workspace_size(const lrnnx_selective_scan_args* a, int bwd) {
   if (!a) return -1;
   if (!bwd) {  // optional: lets the fast path split L for grids too small to fill the chip
-    if (a->wtype == LRNNX_C64 || a->method != LRNNX_MAMBA || !fast_paths_enabled()) return 0;
+    if (a->wtype == LRNNX_C64 || !has_fast_path(a->method) || !fast_paths_enabled()) return 0;
     return ssf_fwd_workspace_bytes(*a);
   }
   if (a->wtype == LRNNX_C64) return ssc_bwd_ws_bytes(*a);
@@ -248,7 +265,7 @@ int lrnnx_selective_scan_fwd(const lrnnx_selective_scan_args* a, void* stream) {
   if (a->method == LRNNX_MAMBA) {
     e = fwd_mamba(*a, st);
   } else {
-    e = ss_fwd_other_f32(*a, st);
+    e = fwd_other(*a, st);
   }
   return from_hip(e, "selective_scan_fwd");
 }
@@ -283,15 +300,15 @@ int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args* a, void* stream) {
                                              "selective_scan_bwd (complex)");
   const float* ckp = static_cast<const float*>(a->ckpt);
   if (!ckp) {
-    // rebuild the fine checkpoints into the workspace.  The mamba fast path
-    // has a states-only forward: split like the forward on small grids, or
+    // rebuild the fine checkpoints into the workspace.  The fast path (mamba,
+    // dirac) has a states-only forward: split like the forward on small grids, or
     // with the caller's x carries (the reference's seeds,
     // selective_scan_backward.cuh:330) one 2048-step chunk per grid slice.
     char* wsb = reinterpret_cast<char*>(a->workspace);
     float* ck = reinterpret_cast<float*>(wsb + ss_bwd_ckpt_offset_bytes(*a));
     hipError_t e = hipSuccess;
     bool done = false;
-    if (a->method == LRNNX_MAMBA && fast_paths_enabled()) {
+    if (has_fast_path(a->method) && fast_paths_enabled()) {
       int64_t fws_bytes = 0;
       float* fws = reinterpret_cast<float*>(wsb + ss_bwd_fws_offset_bytes(*a, &fws_bytes));
       if (fws_bytes == 0) fws = nullptr;
@@ -309,7 +326,7 @@ int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args* a, void* stream) {
       f.ckpt = ck;
       f.workspace = nullptr;  // unsplit
       f.workspace_bytes = 0;
-      e = a->method == LRNNX_MAMBA ? fwd_mamba(f, st) : ss_fwd_other_f32(f, st);
+      e = a->method == LRNNX_MAMBA ? fwd_mamba(f, st) : fwd_other(f, st);
     }
     if (from_hip(e, "selective_scan_bwd (checkpoint rebuild)")) return 1;
     ckp = ck;
@@ -318,7 +335,7 @@ int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args* a, void* stream) {
   if (a->method == LRNNX_MAMBA) {
     e = bwd_mamba(*a, ws, ckp, st);
   } else {
-    e = ss_bwd_other_f32(*a, ws, ckp, st);
+    e = bwd_other(*a, ws, ckp, st);
   }
   return from_hip(e, "selective_scan_bwd");
 }

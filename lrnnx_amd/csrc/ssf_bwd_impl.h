@@ -1,8 +1,9 @@
 // Selective scan backward, fast path of the headline case (gfx950).
 //
-// Same coverage as the fast forward (ssf_fwd_eligible): method "mamba",
-// variable B and C, no deltaA, 8 < d_state <= 16, f32 / bf16 / f16 I/O, 64
-// channels per group block, L a multiple of 16, 16-byte aligned rows.
+// Same coverage as the fast forward (ssf_fwd_eligible): method "mamba" (f32 /
+// bf16 / f16 I/O) and "dirac" (f32 I/O), variable B and C, no deltaA,
+// 8 < d_state <= 16, 64 channels per group block, L a multiple of 16,
+// 16-byte aligned rows.
 // Gradients of the reference kernel
 // csrc/selective_scan/selective_scan_backward.cuh:86-845 for this method:
 //   dh_t  = A_bar_{t+1} dh_{t+1} + C_t dy_t      (dy = dout silu(z))
@@ -11,6 +12,8 @@
 //   dA    = sum_t delta' A_bar h_{t-1} dh,  dB_t = sum_d dh delta' u,
 //   dC_t  = sum_d dy h_t,  dD = sum dy u,  ddelta_bias = sum ddelta,
 //   dz    = dout out sigma(z) (1 + z (1 - sigma(z)))      (:218-219)
+// For "dirac" (input term B u) delta' drops out of du and dB, and ddelta'
+// keeps the A term only.
 //
 // Decomposition as in the forward (ssf_fwd_impl.h): one workgroup = one batch
 // row and 64 channels, wave w owns states 4w..4w+3, lane = channel.  The
@@ -71,7 +74,7 @@ __device__ __forceinline__ float softplus20_sig(float x, float& sg) {
 // per CU.  The channel reductions lose their cross-half stage (the halves
 // hold different states), and the per-element phases take 2 elements per
 // thread.
-template <typename IT, bool kSP, bool kZ, int kRT, int kCh = kWave>
+template <typename IT, bool kSP, bool kZ, int kRT, int kCh = kWave, bool kDi = false>
 __global__ void __launch_bounds__(ssf::kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __restrict__ ws, const SSBwdWs wo,
                const float* __restrict__ ckp, const int64_t seg_tiles) {
@@ -80,6 +83,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   static_assert(kT == kCk, "one checkpoint interval per tile");
   static_assert(kRT == kT || kRT == 2 * kT, "a raw fetch covers one or two tiles");
   static_assert(kCh == kWave || kCh == kWave / 2, "64 or 32 channels per workgroup");
+  static_assert(!kDi || sizeof(IT) == 4, "the dirac method takes fp32 input only");
   constexpr int kH = kWave / kCh;         // lane halves per wave
   constexpr int kS = 4 / kH;              // states per lane
   constexpr int kPair = kRT / kT;         // tiles per raw fetch
@@ -232,7 +236,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       const float x = vd[i] + e_bias;
       vd[i] = kSP ? softplus20_sig(x, sg[i]) : x;
       dy[i] = vdo[i];
-      xu[i] = vd[i] * vu[i];
+      xu[i] = kDi ? vu[i] : vd[i] * vu[i];
     }
     if constexpr (kZ) {
       float vz[kEt], vo[kEt], dz[kEt];
@@ -291,8 +295,8 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     float du[kEt], dd[kEt];
 #pragma unroll
     for (int i = 0; i < kEt; ++i) {
-      du[i] = fmaf(dl[i], p1[i], e_D * dy[i]);
-      const float ddl = fmaf(uu[i], p1[i], kLn2 * p2[i]);
+      du[i] = kDi ? fmaf(e_D, dy[i], p1[i]) : fmaf(dl[i], p1[i], e_D * dy[i]);
+      const float ddl = kDi ? kLn2 * p2[i] : fmaf(uu[i], p1[i], kLn2 * p2[i]);
       dd[i] = kSP ? ddl * sg[i] : ddl;
       e_dD = fmaf(dy[i], uu[i], e_dD);
       e_dbias += dd[i];
@@ -630,7 +634,7 @@ inline SSGeom ssf_bwd_geom(const lrnnx_selective_scan_args& a) {
   return g;
 }
 
-template <typename IT, bool kSP, bool kZ>
+template <typename IT, bool kSP, bool kZ, bool kDi>
 inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                              const float* ckp, int64_t seg_steps, hipStream_t st) {
   // Two-tile raw fetches for 16-bit I/O when every segment holds an even
@@ -652,22 +656,22 @@ inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g
   if constexpr (kTwo) {
     if (a.seqlen % (2 * ssf::kCk) == 0) {
       if (c32)
-        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave / 2>), grid, blk, 0, st, a, g.n_ck, ws,
+        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave / 2, kDi>), grid, blk, 0, st, a, g.n_ck, ws,
                            wo, ckp, seg_tiles);
       else
-        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave>), grid, blk, 0, st, a, g.n_ck, ws, wo,
+        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave, kDi>), grid, blk, 0, st, a, g.n_ck, ws, wo,
                            ckp, seg_tiles);
       return;
     }
     // (the 32-channel form comes with two-tile fetches only: ssf_bwd_chans)
-    hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+    hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave, kDi>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
                        seg_tiles);
   } else {
     if (c32)
-      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave / 2>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave / 2, kDi>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
                          seg_tiles);
     else
-      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave, kDi>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
                          seg_tiles);
   }
 }
@@ -679,12 +683,24 @@ inline hipError_t ssf_bwd_launch(const lrnnx_selective_scan_args& a, float* ws, 
   const SSBwdWs wo = ss_bwd_ws(a, g, a.ckpt == nullptr, S);
   const int64_t steps = S > 1 ? ssf::seg_steps(a) : 0;
   const bool z = a.z.ptr != nullptr;
-  if (a.delta_softplus) {
-    if (z) ssf_bwd_launch_t<IT, true, true>(a, g, ws, wo, ckp, steps, st);
-    else ssf_bwd_launch_t<IT, true, false>(a, g, ws, wo, ckp, steps, st);
+  bool di = false;
+  if constexpr (sizeof(IT) == 4) di = a.method == LRNNX_DIRAC;   // dirac: fp32 input only (shape_ok)
+  if (di) {
+    if constexpr (sizeof(IT) == 4) {
+      if (a.delta_softplus) {
+        if (z) ssf_bwd_launch_t<IT, true, true, true>(a, g, ws, wo, ckp, steps, st);
+        else ssf_bwd_launch_t<IT, true, false, true>(a, g, ws, wo, ckp, steps, st);
+      } else {
+        if (z) ssf_bwd_launch_t<IT, false, true, true>(a, g, ws, wo, ckp, steps, st);
+        else ssf_bwd_launch_t<IT, false, false, true>(a, g, ws, wo, ckp, steps, st);
+      }
+    }
+  } else if (a.delta_softplus) {
+    if (z) ssf_bwd_launch_t<IT, true, true, false>(a, g, ws, wo, ckp, steps, st);
+    else ssf_bwd_launch_t<IT, true, false, false>(a, g, ws, wo, ckp, steps, st);
   } else {
-    if (z) ssf_bwd_launch_t<IT, false, true>(a, g, ws, wo, ckp, steps, st);
-    else ssf_bwd_launch_t<IT, false, false>(a, g, ws, wo, ckp, steps, st);
+    if (z) ssf_bwd_launch_t<IT, false, true, false>(a, g, ws, wo, ckp, steps, st);
+    else ssf_bwd_launch_t<IT, false, false, false>(a, g, ws, wo, ckp, steps, st);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -1,7 +1,8 @@
 // Selective scan forward, fast path of the headline case (gfx950).
 //
-// Covers: method "mamba", variable B and C of any group count, no deltaA,
-// 8 < d_state <= 16, real fp32 A, f32 / bf16 / f16 I/O, d_model a multiple
+// Covers: method "mamba" (f32 / bf16 / f16 I/O) and "dirac" (f32 I/O; the
+// input term B u without delta'), variable B and C of any group count, no
+// deltaA, 8 < d_state <= 16, real fp32 A, d_model a multiple
 // of 64 per group, L a multiple of the tile length, 16-byte aligned rows
 // (ssf_fwd_eligible).  Everything else runs the generic kernel of
 // ss_fwd_impl.h.  Semantics are those of the reference kernel
@@ -99,12 +100,13 @@ struct SsfSeg {
 // that a grid too small to give every CU two 64-channel workgroups (at most
 // 256 of them) runs twice as many workgroups, two per CU.  The 32-channel
 // form walks 32-step tiles whatever the element size.
-template <typename IT, bool kSP, bool kZ, bool kOut = true, int kCh = kWave>
+template <typename IT, bool kSP, bool kZ, bool kOut = true, int kCh = kWave, bool kDi = false>
 __global__ void __launch_bounds__(ssf::kNT)
 ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf::SsfSeg sg) {
   using namespace ssf;
   static_assert(kOut || !kZ, "the checkpoint rebuild reads no z");
   static_assert(kCh == kWave || kCh == kWave / 2, "64 or 32 channels per workgroup");
+  static_assert(!kDi || sizeof(IT) == 4, "the dirac method takes fp32 input only");
   constexpr int kH = kWave / kCh;                                 // lane halves per wave
   constexpr int kS = 16 / kNW / kH;                               // states per lane
   constexpr int kT = kCh == kWave ? tile_steps<IT>() : 32;        // steps per tile
@@ -131,7 +133,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   __shared__ __attribute__((aligned(16))) char s_raw_b[kRawS];
   __shared__ __attribute__((aligned(16))) char s_raw_c[kOut ? kRawS : 16];
   __shared__ __attribute__((aligned(16))) float s_dl[kOp];                  // [g][ch][4] delta'
-  __shared__ __attribute__((aligned(16))) float s_x[kOp];                   // [g][ch][4] delta' u
+  __shared__ __attribute__((aligned(16))) float s_x[kOp];                   // [g][ch][4] delta' u (dirac: u)
   __shared__ __attribute__((aligned(16))) float s_B[16 * kT];               // [n][t]
   __shared__ __attribute__((aligned(16))) float s_C[kOut ? 16 * kT : 4];
   __shared__ __attribute__((aligned(16))) float s_Y[kOut ? (kNP + 1) * kOp : 4];  // [partial][g][ch][4]; kNP: D u
@@ -235,8 +237,11 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
     for (int i = 0; i < kEt; i += 4) {
       const int o = op_off<kSh, kCh>((eq * kEt + i) >> 2, er);
       *reinterpret_cast<float4*>(s_dl + o) = make_float4(vd[i], vd[i + 1], vd[i + 2], vd[i + 3]);
-      *reinterpret_cast<float4*>(s_x + o) =
-          make_float4(vd[i] * vu[i], vd[i + 1] * vu[i + 1], vd[i + 2] * vu[i + 2], vd[i + 3] * vu[i + 3]);
+      if constexpr (kDi)
+        *reinterpret_cast<float4*>(s_x + o) = make_float4(vu[i], vu[i + 1], vu[i + 2], vu[i + 3]);
+      else
+        *reinterpret_cast<float4*>(s_x + o) =
+            make_float4(vd[i] * vu[i], vd[i + 1] * vu[i + 1], vd[i + 2] * vu[i + 2], vd[i + 3] * vu[i + 3]);
       if constexpr (kOut)
         *reinterpret_cast<float4*>(s_Y + kNP * kOp + o) =
             make_float4(e_D * vu[i], e_D * vu[i + 1], e_D * vu[i + 2], e_D * vu[i + 3]);
@@ -440,7 +445,9 @@ inline bool fetch_fits(const lrnnx_view& v, bool states, int64_t row_bytes) {
 // Shape / option part of the fast-path coverage (both directions).
 template <typename IT>
 inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile) {
-  if (a.method != LRNNX_MAMBA || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C || a.deltaA.ptr) return false;
+  // "mamba" (B u delta') at every input type, "dirac" (B u) at fp32 input
+  const bool di = a.method == LRNNX_DIRAC && sizeof(IT) == 4;
+  if ((a.method != LRNNX_MAMBA && !di) || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C || a.deltaA.ptr) return false;
   if (a.dstate <= 8 || a.dstate > 16 || a.seqlen <= 0 || a.seqlen % tile != 0) return false;
   if (a.n_groups <= 0 || a.dim % a.n_groups != 0 || (a.dim / a.n_groups) % kWave != 0) return false;
   // the checkpoint rows (d_state rows of 64 fp32, D apart) of the backward's fetch
@@ -516,7 +523,7 @@ enum class FwdKind { kOutZ, kOut, kStates };  // with z gate / without / states 
 
 // chans: 64 or 32 for the output kinds (ssf::chans_for); the states-only
 // kind (split summaries, checkpoint rebuild) always runs 64.
-template <typename IT, bool kSP>
+template <typename IT, bool kSP, bool kDi>
 inline void ssf_fwd_launch_t(const lrnnx_selective_scan_args& a, int64_t n_ck, const ssf::SsfSeg& sg, unsigned nz,
                              ssf::FwdKind kind, int chans, hipStream_t st) {
   const dim3 grid64((unsigned)(a.dim / kWave), (unsigned)a.batch, nz);
@@ -524,15 +531,15 @@ inline void ssf_fwd_launch_t(const lrnnx_selective_scan_args& a, int64_t n_ck, c
   const dim3 blk(ssf::kNT);
   switch (kind) {
     case ssf::FwdKind::kOutZ:
-      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 32>), grid32, blk, 0, st, a, n_ck, sg);
-      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 64>), grid64, blk, 0, st, a, n_ck, sg);
+      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 32, kDi>), grid32, blk, 0, st, a, n_ck, sg);
+      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 64, kDi>), grid64, blk, 0, st, a, n_ck, sg);
       break;
     case ssf::FwdKind::kOut:
-      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 32>), grid32, blk, 0, st, a, n_ck, sg);
-      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 64>), grid64, blk, 0, st, a, n_ck, sg);
+      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 32, kDi>), grid32, blk, 0, st, a, n_ck, sg);
+      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 64, kDi>), grid64, blk, 0, st, a, n_ck, sg);
       break;
     case ssf::FwdKind::kStates:
-      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false, 64>), grid64, blk, 0, st, a, n_ck, sg);
+      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false, 64, kDi>), grid64, blk, 0, st, a, n_ck, sg);
       break;
   }
 }
@@ -553,8 +560,15 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
                                                     : ssf::FwdKind::kOut;
   auto launch = [&](const lrnnx_selective_scan_args& x, const ssf::SsfSeg& sg, unsigned nz, ssf::FwdKind k,
                     int chans) {
-    if (x.delta_softplus) ssf_fwd_launch_t<IT, true>(x, n_ck, sg, nz, k, chans, st);
-    else ssf_fwd_launch_t<IT, false>(x, n_ck, sg, nz, k, chans, st);
+    if constexpr (sizeof(IT) == 4) {   // dirac: fp32 input only (shape_ok)
+      if (x.method == LRNNX_DIRAC) {
+        if (x.delta_softplus) ssf_fwd_launch_t<IT, true, true>(x, n_ck, sg, nz, k, chans, st);
+        else ssf_fwd_launch_t<IT, false, true>(x, n_ck, sg, nz, k, chans, st);
+        return;
+      }
+    }
+    if (x.delta_softplus) ssf_fwd_launch_t<IT, true, false>(x, n_ck, sg, nz, k, chans, st);
+    else ssf_fwd_launch_t<IT, false, false>(x, n_ck, sg, nz, k, chans, st);
   };
   const int64_t steps = ssf::seg_steps(a);
   const int64_t need = ssf_fwd_ws_bytes<IT>(a);

@@ -273,3 +273,80 @@ def test_fast_forward_split_matches_unsplit(dev, itype):
     tol = 1e-5 if itype == torch.float32 else 2e-2
     for name, s_, u_ in zip(("out", "out_z", "x", "ckpt"), res[0], res[1]):
         close(name, s_, u_.cpu().double(), tol if name in ("out", "out_z") else 1e-5, tol if name in ("out", "out_z") else 1e-5)
+
+
+# "dirac" (input term B u) on the fast kernels: fp32 input, 8 < d_state <= 16,
+# L a multiple of 16.  Small grids split L (the default) or run unsplit in
+# 64- or 32-channel workgroups (LRNNX_SCAN_NO_SPLIT, LRNNX_SCAN_CHANNELS).
+@pytest.mark.parametrize("schedule", ["split", "unsplit64", "unsplit32"])
+@pytest.mark.parametrize("opts", [dict(), dict(has_z=False, softplus=False, N=13), dict(groups=2, has_bias=False)],
+                         ids=["z_softplus", "noz_nosoftplus_n13", "groups2"])
+def test_dirac_fast_path_vs_oracle(dev, monkeypatch, schedule, opts):
+    if schedule != "split":
+        monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", "1")
+        monkeypatch.setenv("LRNNX_SCAN_CHANNELS", schedule[-2:])
+    opts = dict(opts)
+    N = opts.pop("N", 16)
+    print(f"dirac fast path, schedule {schedule}, N={N}, {opts}", flush=True)
+    _run(dev, 2, 128, 512, N, method="dirac", seed=51, **opts)
+
+
+@pytest.mark.parametrize("no_split", ["0", "1"])
+def test_dirac_fast_path_long_chunks(dev, monkeypatch, no_split):
+    # the 2048-step chunk carries (last_state) across two chunk ends and a
+    # ragged last chunk, split into segments and unsplit
+    monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", no_split)
+    _run(dev, 1, 64, 4160, 16, method="dirac", seed=52)
+
+
+def test_dirac_fast_path_matches_generic(dev, monkeypatch):
+    """The fast kernels and the generic kernels (LRNNX_SCAN_GENERIC=1) agree on
+    "dirac" (both fp32 state; only the order of the final sums differs)."""
+    inp = R.make_selective_inputs(2, 128, 512, 16, seed=53, groups=2)
+    dout = torch.randn(2, 128, 512, generator=torch.Generator().manual_seed(54)).to(dev)
+    d = to_dev(inp, dev)
+    res = []
+    for generic in ("0", "1"):
+        monkeypatch.setenv("LRNNX_SCAN_GENERIC", generic)
+        leaves = {k: d[k].clone().requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D", "z",
+                                                                 "delta_bias")}
+        out, last = selective_scan_fn(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"],
+                                      leaves["D"], leaves["z"], leaves["delta_bias"], None, True, True, "dirac")
+        out.backward(dout)
+        torch.cuda.synchronize()
+        res.append([out.detach(), last.detach()] + [leaves[k].grad for k in leaves])
+    names = ["out", "last_state"] + ["d" + k for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")]
+    for n, a, b in zip(names, res[0], res[1]):
+        close(n, a, b.cpu().double(), 1e-5, 1e-5)
+
+
+@pytest.mark.parametrize("save", ["checkpoints", "x"])
+@pytest.mark.parametrize("no_split", ["0", "1"])
+def test_dirac_binding_fwd_then_bwd(dev, monkeypatch, save, no_split):
+    """selective_scan_cuda.fwd -> bwd(x, out) for "dirac": with the forward's
+    checkpoints, or rebuilding them on the fast path's states-only forward
+    (split on this small grid, or one 2048-step chunk per grid slice from the
+    x carries when unsplit)."""
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", no_split)
+    prev = ssc.save_mode()
+    ssc.set_save_mode(save)
+    try:
+        Bt, D, L = 1, 64, 4160
+        inp = R.make_selective_inputs(Bt, D, L, 16, seed=55)
+        dout = torch.randn(Bt, D, L, generator=torch.Generator().manual_seed(56))
+        ro, rl, rg = oracle_selective(inp, "dirac", True, None, True, dout)
+        d = to_dev(inp, dev)
+        u, dl, A, B, C, Dv, z, db = (d[k] for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias"))
+        B, C = B.unsqueeze(1).contiguous(), C.unsqueeze(1).contiguous()  # (b, g, n, l), as the autograd wrapper
+        out, x, out_z = ssc.fwd(u, dl, A, B, C, Dv, z, db, None, True, "dirac")[:3]
+        g = ssc.bwd(u, dl, A, B, C, Dv, z, db, None, dout.to(dev), x, out, None, True, False, "dirac")
+        torch.cuda.synchronize()
+    finally:
+        ssc.set_save_mode(prev)
+    close("out", out_z, ro, 1e-4, 1e-5)
+    close("last_state", x[:, :, -1, 1::2], rl, 1e-4, 1e-5)
+    for i, k in enumerate(("u", "delta", "A", "B", "C", "D", "delta_bias")):
+        close(f"d{k}", g[i], rg[k], 1e-4, 1e-4 if k in ("A", "D", "delta_bias") else 1e-5)
+    close("dz", g[7], rg["z"], 1e-4, 1e-5)
