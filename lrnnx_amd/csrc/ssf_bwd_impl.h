@@ -2,7 +2,7 @@
 //
 // Same coverage as the fast forward (ssf_fwd_eligible): method "mamba" (f32 /
 // bf16 / f16 I/O) and "dirac" (f32 I/O), variable B and C, no deltaA,
-// 8 < d_state <= 16, 64 channels per group block, L a multiple of 16,
+// d_state <= 16, 64 channels per group block, L a multiple of 16,
 // 16-byte aligned rows.
 // Gradients of the reference kernel
 // csrc/selective_scan/selective_scan_backward.cuh:86-845 for this method:

@@ -2,7 +2,7 @@
 //
 // Covers: method "mamba" (f32 / bf16 / f16 I/O) and "dirac" (f32 I/O; the
 // input term B u without delta'), variable B and C of any group count, no
-// deltaA, 8 < d_state <= 16, real fp32 A, d_model a multiple
+// deltaA, d_state <= 16, real fp32 A, d_model a multiple
 // of 64 per group, L a multiple of the tile length, 16-byte aligned rows
 // (ssf_fwd_eligible).  Everything else runs the generic kernel of
 // ss_fwd_impl.h.  Semantics are those of the reference kernel
@@ -448,7 +448,7 @@ inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile) {
   // "mamba" (B u delta') at every input type, "dirac" (B u) at fp32 input
   const bool di = a.method == LRNNX_DIRAC && sizeof(IT) == 4;
   if ((a.method != LRNNX_MAMBA && !di) || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C || a.deltaA.ptr) return false;
-  if (a.dstate <= 8 || a.dstate > 16 || a.seqlen <= 0 || a.seqlen % tile != 0) return false;
+  if (a.dstate < 1 || a.dstate > 16 || a.seqlen <= 0 || a.seqlen % tile != 0) return false;
   if (a.n_groups <= 0 || a.dim % a.n_groups != 0 || (a.dim / a.n_groups) % kWave != 0) return false;
   // the checkpoint rows (d_state rows of 64 fp32, D apart) of the backward's fetch
   if (!dma_offsets_fit(a.dim, a.dstate, kWave * 4, 4)) return false;

@@ -11,7 +11,7 @@ autograd of the restated selective_scan_ref, lrnnx/ops/selective_scan.py:
 * The small-grid split of L against the unsplit schedule
   (LRNNX_SCAN_NO_SPLIT=1) at B=1 D=64 L=4160, both against the oracle.
 * 64 and 32 channels per workgroup (LRNNX_SCAN_CHANNELS) on one unsplit grid, both forms
-  with d_state 9 and 13 (waves whose states are part real, part padding), and the
+  with d_state 1, 3, 8, 9 and 13 (waves whose states are all or part padding), and the
   32-channel form with padded states, groups and several chunk ends.
 * The binding's own call sequence ``selective_scan_cuda.fwd`` -> ``bwd(x)``
   in both save modes: "checkpoints" (fwd attaches them to x) and "x" (the
@@ -235,11 +235,12 @@ def test_channels_per_workgroup_64_and_32_vs_oracle(dev, monkeypatch, itype, wit
 
 
 @pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("N", [9, 13])
+@pytest.mark.parametrize("N", [1, 3, 8, 9, 13])
 @pytest.mark.parametrize("chans", ["64", "32"])
 def test_partially_padded_wave_states_vs_oracle(dev, monkeypatch, itype, N, chans):
-    """d_state 9 and 13: one wave's four states are part real, part padding,
-    in both channel forms (LRNNX_SCAN_CHANNELS).  The backward's dB / dC
+    """d_state 9 and 13: one wave's four states are part real, part padding;
+    1, 3 and 8: whole waves hold padding only; in both channel forms
+    (LRNNX_SCAN_CHANNELS).  The backward's dB / dC
     reduce-scatter gives each lane its states in a lane-dependent register
     order, so real and padded states share registers across lanes, and a
     lane writes its partial only where the state it ends with is real."""

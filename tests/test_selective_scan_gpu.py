@@ -275,7 +275,7 @@ def test_fast_forward_split_matches_unsplit(dev, itype):
         close(name, s_, u_.cpu().double(), tol if name in ("out", "out_z") else 1e-5, tol if name in ("out", "out_z") else 1e-5)
 
 
-# "dirac" (input term B u) on the fast kernels: fp32 input, 8 < d_state <= 16,
+# "dirac" (input term B u) on the fast kernels: fp32 input, d_state <= 16,
 # L a multiple of 16.  Small grids split L (the default) or run unsplit in
 # 64- or 32-channel workgroups (LRNNX_SCAN_NO_SPLIT, LRNNX_SCAN_CHANNELS).
 @pytest.mark.parametrize("schedule", ["split", "unsplit64", "unsplit32"])
