@@ -528,6 +528,53 @@ def cpu_configs(torch, R):
     return res
 
 
+def dstate_sweep(torch, dev, ss, L_):
+    """fwd and bwd through the C ABI (SelectiveStep, preallocated) at the
+    config-2 shape (B=8, D=1536, L=2048, bf16, mamba, variable B/C, z) for
+    d_state 1 .. 256: the fast kernels up to 16, the general kernels above
+    (state blocks past 64).  Event-timed medians of 10 after 3 warm-ups; the
+    general kernels also at 16 (LRNNX_SCAN_GENERIC=1) for comparison."""
+    import statistics
+
+    Bt, D, L = 8, 1536, 2048
+    res = {}
+    for N, generic in ((1, "0"), (8, "0"), (16, "0"), (16, "1"), (32, "0"), (64, "0"), (65, "0"), (100, "0"),
+                       (128, "0"), (256, "0")):
+        prev = os.environ.get("LRNNX_SCAN_GENERIC")
+        os.environ["LRNNX_SCAN_GENERIC"] = generic
+        try:
+            inp = make_cfg3(dev, torch, None, Bt, D, L, N, seed=2)
+            st = SelectiveStep(inp, torch, ss, L_)
+            for _ in range(3):
+                st.fwd()
+                st.bwd()
+            torch.cuda.synchronize()
+            tf, tb = [], []
+            for _ in range(10):
+                e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+                e0.record()
+                st.fwd()
+                e1.record()
+                st.bwd()
+                e2.record()
+                e2.synchronize()
+                tf.append(e0.elapsed_time(e1))
+                tb.append(e1.elapsed_time(e2))
+        finally:
+            if prev is None:
+                del os.environ["LRNNX_SCAN_GENERIC"]
+            else:
+                os.environ["LRNNX_SCAN_GENERIC"] = prev
+        f, b = statistics.median(tf), statistics.median(tb)
+        key = f"n{N}" + ("_general" if generic == "1" else "")
+        res[key] = {"fwd_ms": round(f, 4), "bwd_ms": round(b, 4),
+                    "ns_per_1e3_state_steps": round((f + b) * 1e9 / (Bt * D * L * N), 3)}
+        _log(f"d_state sweep {key}: {res[key]}")
+        del st, inp
+        torch.cuda.empty_cache()
+    return res
+
+
 def method_configs(torch, dev):
     """fwd+bwd through the autograd wrappers for the other discretisations and
     weight types at B=8, D=1536, L=2048 (fp32, event-timed medians of 10): the
@@ -857,6 +904,8 @@ def main():
     ap.add_argument("--methods-only", action="store_true",
                     help="time only the other discretisations / one-state path / complex weights (for a kernel "
                          "trace of those kernels), print their JSON, then exit")
+    ap.add_argument("--dstate-sweep", action="store_true",
+                    help="time fwd / bwd at the config-2 shape for d_state 1 .. 256, print the JSON, then exit")
     ap.add_argument("--summarize-counters", nargs="+", metavar="COUNTER_CSV",
                     help="print a markdown table of rocprofv3 --pmc counter_collection.csv files, then exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
@@ -889,6 +938,9 @@ def main():
     L_.lib()
     if args.methods_only:
         print(json.dumps(method_configs(torch, dev)))
+        return
+    if args.dstate_sweep:
+        print(json.dumps(dstate_sweep(torch, dev, ss, L_)))
         return
     if args.copy_calib:
         _log(f"copy calibration: {COPY_CALIB_BYTES} bytes read + written")

@@ -89,12 +89,15 @@ typedef struct lrnnx_selective_scan_args {
 int64_t lrnnx_selective_scan_ckpt_size(const lrnnx_selective_scan_args *a);
 
 /* Bytes of workspace the call needs (bwd = 0: forward, 1: backward).  The
- * forward's is optional: given at least this many bytes (16-byte aligned), the
- * fast path (methods mamba and dirac) splits L into segments when batch * dim / 64 workgroups are
- * too few to fill the GPU (a segment summary pass, a carry chain, then every
- * segment from its initial state); without it the forward runs unsplit.  It
- * is 0 when the call would not split.  No reference counterpart (the
- * reference's forward allocates nothing beyond its outputs). */
+ * forward's is optional.  Given at least this many bytes (16-byte aligned):
+ * for d_state > 64 (real weights) the states run in blocks of at most 64,
+ * whose partial sums of y go there (batch * dim * L floats per block); the
+ * fast path (methods mamba and dirac) splits L into segments when
+ * batch * dim / 64 workgroups are too few to fill the GPU (a segment summary
+ * pass, a carry chain, then every segment from its initial state).  Without
+ * it the forward runs unsplit, and d_state > 64 in one slower block.  It is
+ * 0 when neither applies.  No reference counterpart (the reference's forward
+ * allocates nothing beyond its outputs). */
 int64_t lrnnx_selective_scan_workspace_size(const lrnnx_selective_scan_args *a, int bwd);
 
 /* Forward.  Writes out / out_z / x and, if ckpt != NULL, the checkpoints.
@@ -108,9 +111,10 @@ int lrnnx_selective_scan_fwd(const lrnnx_selective_scan_args *a, void *stream);
  * lrnnx_selective_scan_fwd; `workspace` / `workspace_bytes` are ignored and
  * the split's segment summaries go to a scratch array in device memory that
  * the library holds per GPU (LRNNX_FWD_NOALLOC_SCRATCH_BYTES: enough for
- * every call the split covers; a larger need is rejected).  Calls on one GPU
- * share that array, so calls that overlap on one GPU (concurrent streams)
- * race; nothing in it needs to start at zero. */
+ * every call the split covers; a larger need is rejected; d_state > 64 runs
+ * in one block, as lrnnx_selective_scan_fwd without a workspace).  Calls on
+ * one GPU share that array, so calls that overlap on one GPU (concurrent
+ * streams) race; nothing in it needs to start at zero. */
 int lrnnx_selective_scan_fwd_noalloc(const lrnnx_selective_scan_args *a, void *stream);
 #define LRNNX_FWD_NOALLOC_SCRATCH_BYTES 4456448
 

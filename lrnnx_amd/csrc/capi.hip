@@ -116,6 +116,12 @@ const char* method_name(int m) {
 // input is fp32).
 bool has_fast_path(int method) { return method == LRNNX_MAMBA || method == LRNNX_DIRAC; }
 
+// Forward workspace of the fast path's split of L (0: the call does not split).
+int64_t fwd_split_ws_bytes(const lrnnx_selective_scan_args& a) {
+  if (!has_fast_path(a.method) || !fast_paths_enabled()) return 0;
+  return ssf_fwd_workspace_bytes(a);
+}
+
 // Forward of the "mamba" method: fast path when it covers the call, else the
 // generic kernel.
 hipError_t fwd_mamba(const lrnnx_selective_scan_args& a, hipStream_t st) {
@@ -249,9 +255,10 @@ int64_t lrnnx_selective_scan_ckpt_size(const lrnnx_selective_scan_args* a) {
 
 int64_t lrnnx_selective_scan_workspace_size(const lrnnx_selective_scan_args* a, int bwd) {
   if (!a) return -1;
-  if (!bwd) {  // optional: lets the fast path split L for grids too small to fill the chip
-    if (a->wtype == LRNNX_C64 || !has_fast_path(a->method) || !fast_paths_enabled()) return 0;
-    return ssf_fwd_workspace_bytes(*a);
+  if (!bwd) {  // optional: the state blocks' partial y (d_state > 64), or the fast path's split of L
+    if (a->wtype == LRNNX_C64) return 0;
+    const int64_t blk = ss_fwd_blocks_ws_bytes(*a);
+    return blk > 0 ? blk : fwd_split_ws_bytes(*a);
   }
   if (a->wtype == LRNNX_C64) return ssc_bwd_ws_bytes(*a);
   return ss_bwd_ws_bytes(*a);
@@ -275,7 +282,9 @@ int lrnnx_selective_scan_fwd_noalloc(const lrnnx_selective_scan_args* a, void* s
   lrnnx_selective_scan_args f = *a;  // the caller's workspace fields are ignored
   f.workspace = nullptr;
   f.workspace_bytes = 0;
-  const int64_t need = lrnnx_selective_scan_workspace_size(&f, 0);
+  // the split's summaries (d_state > 64 runs without a workspace: one state
+  // block, no partial sums)
+  const int64_t need = a->wtype == LRNNX_C64 ? 0 : fwd_split_ws_bytes(f);
   if (need > kFwdScratchBytes)
     return fail("selective_scan_fwd_noalloc: the call needs %lld bytes of scratch, more than the %lld it holds",
                 (long long)need, (long long)kFwdScratchBytes);

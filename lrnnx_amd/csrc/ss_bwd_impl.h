@@ -40,13 +40,17 @@
 
 namespace lrnnx {
 
-template <int kMethod>
-__host__ __device__ constexpr bool needs_p3() {
-  return kMethod == LRNNX_ZOH || kMethod == LRNNX_BILINEAR || kMethod == LRNNX_RGLRU;
+__host__ __device__ constexpr bool needs_p3_m(int m) {
+  return m == LRNNX_ZOH || m == LRNNX_BILINEAR || m == LRNNX_RGLRU;
 }
+template <int kMethod>
+__host__ __device__ constexpr bool needs_p3() { return needs_p3_m(kMethod); }
 
 struct SSBwdWs {  // fp32 workspace sections (element offsets)
   int64_t dBv, dCv, dA, dBc, dCc, dD, dbias, ckpt, total;
+  // state blocks (SSGeom::nsb > 1): the blocks' sums over their states of the
+  // du / ddelta / ddeltaA terms, fp32 [block][term][b][d][L], n_terms of them
+  int64_t pp, n_terms;
   // split of L (fast path, small grids): S segments; the per-(b, ...) partials
   // dA / dD / ddelta_bias are per (segment, b); the adjoint buffers
   // g_loc, g_init [seg][b][n][d] and dsum [seg][b][d]
@@ -74,6 +78,8 @@ inline SSBwdWs ss_bwd_ws(const lrnnx_selective_scan_args& a, const SSGeom& g, bo
   w.g_loc = o; if (S > 1) o += align64(S * B * N * D);
   w.g_init = o; if (S > 1) o += align64(S * B * N * D);
   w.dsum = o; if (S > 1) o += align64(S * B * D);
+  w.n_terms = needs_p3_m(a.method) ? 3 : 2;
+  w.pp = o; if (g.nsb > 1) o += align64((int64_t)g.nsb * w.n_terms * B * D * L);
   w.ckpt = o; if (need_ckpt) o += align64(B * g.n_ck * N * D);
   w.fws = o;
   w.fws_floats = (need_ckpt && S > 1) ? 2 * S * B * N * D + 2 * S * B * D : 0;
@@ -118,7 +124,7 @@ __device__ __forceinline__ void lds_states(const float* p, float* o) {
 template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
 __global__ void __launch_bounds__(512)
 ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_ck, float* __restrict__ ws,
-              const SSBwdWs wo, const float* __restrict__ ckp, const int flags) {
+              const SSBwdWs wo, const float* __restrict__ ckp, const int flags, const int nsb) {
   constexpr int kCk = ck_for(kS);
   constexpr int kTB = tb_for(kS);
   constexpr int kEl = 16 / sizeof(IT);  // elements per 16-byte block
@@ -165,7 +171,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int64_t b = blockIdx.y;
   const int64_t D = a.dim, L = a.seqlen;
-  const int N = (int)a.dstate;
+  const int N = (int)a.dstate;                 // all states (layout of the checkpoints, dA, dB, dC)
   const int64_t cb = blockIdx.x;
   const int64_t d0 = cb * CB;
   const int rows = (int)((D - d0) < CB ? (D - d0) : CB);
@@ -174,6 +180,12 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   const int64_t grp = (a.var_B || a.var_C) ? d0 / (D / a.n_groups) : 0;
   const int n0 = w * kS;
   const int NP = nW * kS;
+  const int nb = (int)blockIdx.z * NP;               // first state of this state block
+  const int Nb = N - nb < NP ? N - nb : NP;          // its real states
+  // state blocks: the epilogue writes the block's du / ddelta terms here (a
+  // combine kernel finishes them, with dD and ddelta_bias)
+  float* gpp = nsb > 1 ? ws + wo.pp + (((int64_t)blockIdx.z * wo.n_terms * a.batch + b) * D + d0) * L : nullptr;
+  const int64_t pp_term = a.batch * D * L;           // between the terms of one block
   const bool has_dA_in = a.deltaA.ptr != nullptr;
   const bool has_bias = a.delta_bias.ptr != nullptr;
   const bool has_D = a.D.ptr != nullptr;
@@ -188,8 +200,8 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   const IT* gos =
       has_z ? static_cast<const IT*>(a.out_saved.ptr) + b * a.out_saved.s0 + d0 * a.out_saved.s1 : nullptr;
   const IT* gdA = kDA ? static_cast<const IT*>(a.deltaA.ptr) + b * a.deltaA.s0 + d0 * a.deltaA.s1 : nullptr;
-  const IT* gB = kVarB ? static_cast<const IT*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1 : nullptr;
-  const IT* gC = kVarC ? static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1 : nullptr;
+  const IT* gB = kVarB ? static_cast<const IT*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1 + nb * a.B.s2 : nullptr;
+  const IT* gC = kVarC ? static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1 + nb * a.C.s2 : nullptr;
   IT* gdu = static_cast<IT*>(a.du.ptr) + b * a.du.s0 + d0 * a.du.s1;
   IT* gddl = static_cast<IT*>(a.ddelta.ptr) + b * a.ddelta.s0 + d0 * a.ddelta.s1;
   IT* gddA = has_dA_in ? static_cast<IT*>(a.ddeltaA.ptr) + b * a.ddeltaA.s0 + d0 * a.ddeltaA.s1 : nullptr;
@@ -200,7 +212,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   const uint32_t sdu = (uint32_t)a.du.s1, sddl = (uint32_t)a.ddelta.s1, sddA = (uint32_t)a.ddeltaA.s1;
   const uint32_t sdz = (uint32_t)a.dz.s1;
   // checkpoint rows: state n of interval kk at ckp[((b * n_ck + kk) * N + n) * D + d]
-  const float* gck = ckp + b * n_ck * N * D + d0;
+  const float* gck = ckp + b * n_ck * N * D + nb * D + d0;
 
   float a2[kS], Araw[kS], invA[kS], bcst[kS], ccst[kS], cout_c[kS];
   // dh: gradient of the state at the current step; gn: A_bar_{t+1} dh_{t+1}
@@ -212,13 +224,14 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
 #pragma unroll
     for (int k = 0; k < kS; ++k) {
       const int n = n0 + k;
-      const bool ok = lane_ok && n < N;
-      const float Av = ok ? Ap[d * a.A.s0 + n * a.A.s1] : (kMethod == LRNNX_RGLRU ? 0.5f : -1.f);
+      const bool ok = lane_ok && n < Nb;
+      const int64_t ng = nb + n;
+      const float Av = ok ? Ap[d * a.A.s0 + ng * a.A.s1] : (kMethod == LRNNX_RGLRU ? 0.5f : -1.f);
       Araw[k] = Av;
       invA[k] = 1.f / Av;
       a2[k] = prep_a2<kMethod>(Av);
-      bcst[k] = (!kVarB && ok) ? Bp[d * a.B.s0 + n * a.B.s1] : 1.f;
-      ccst[k] = (!kVarC && ok) ? Cp[d * a.C.s0 + n * a.C.s1] : 1.f;
+      bcst[k] = (!kVarB && ok) ? Bp[d * a.B.s0 + ng * a.B.s1] : 1.f;
+      ccst[k] = (!kVarC && ok) ? Cp[d * a.C.s0 + ng * a.C.s1] : 1.f;
       cout_c[k] = ok ? (kVarB ? 1.f : bcst[k]) * (kVarC ? 1.f : ccst[k]) : 0.f;
       dh[k] = 0.f; gn[k] = 0.f; dA_acc[k] = 0.f; dBc_acc[k] = 0.f; dCc_acc[k] = 0.f;
     }
@@ -247,11 +260,11 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
       tile_fetch_async<IT, kQ>(gos + t0, sos, CB, s_raw_os, w, nW, lane);
     }
     if constexpr (kDA) tile_fetch_async<IT, kQ>(gdA + t0, sdA, CB, s_raw_dA, w, nW, lane);
-    if constexpr (kVarB) tile_fetch_async<IT, kQ>(gB + t0, sBn, N, s_raw_bc, w, nW, lane);
-    if constexpr (kVarC) tile_fetch_async<IT, kQ>(gC + t0, sCn, N, s_raw_bc + kRawBC, w, nW, lane);
+    if constexpr (kVarB) tile_fetch_async<IT, kQ>(gB + t0, sBn, Nb, s_raw_bc, w, nW, lane);
+    if constexpr (kVarC) tile_fetch_async<IT, kQ>(gC + t0, sCn, Nb, s_raw_bc + kRawBC, w, nW, lane);
     if constexpr (kCkLds) {
-      if (tile > 0)  // h at the tile start = checkpoint of interval tile - 1 (64 channels x N states)
-        tile_fetch_async<float, kWave * 4 / 16>(gck + (tile - 1) * N * D, (uint32_t)D, N,
+      if (tile > 0)  // h at the tile start = checkpoint of interval tile - 1 (64 channels x Nb states)
+        tile_fetch_async<float, kWave * 4 / 16>(gck + (tile - 1) * N * D, (uint32_t)D, Nb,
                                                  reinterpret_cast<char*>(s_ck + buf * kNPmax * kWave), w, nW, lane);
     }
   };
@@ -266,13 +279,13 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
       tile_fetch_sync<IT, kQ>(gos + t0, sos, kWave, rows, nt, s_raw_os, tid, blockDim.x);
     }
     if constexpr (kDA) tile_fetch_sync<IT, kQ>(gdA + t0, sdA, kWave, rows, nt, s_raw_dA, tid, blockDim.x);
-    if constexpr (kVarB) tile_fetch_sync<IT, kQ>(gB + t0, sBn, NP, N, nt, s_raw_bc, tid, blockDim.x);
-    if constexpr (kVarC) tile_fetch_sync<IT, kQ>(gC + t0, sCn, NP, N, nt, s_raw_bc + kRawBC, tid, blockDim.x);
+    if constexpr (kVarB) tile_fetch_sync<IT, kQ>(gB + t0, sBn, NP, Nb, nt, s_raw_bc, tid, blockDim.x);
+    if constexpr (kVarC) tile_fetch_sync<IT, kQ>(gC + t0, sCn, NP, Nb, nt, s_raw_bc + kRawBC, tid, blockDim.x);
     if constexpr (kCkLds) {
       if (tile > 0) {
         const float* src = gck + (tile - 1) * N * D;
         float* dst = s_ck + buf * kNPmax * kWave;
-        for (int j = tid; j < N * kWave; j += blockDim.x) {
+        for (int j = tid; j < Nb * kWave; j += blockDim.x) {
           const int n = j / kWave, c = j % kWave;
           dst[j] = c < rows ? src[(int64_t)n * D + c] : 0.f;
         }
@@ -319,7 +332,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
         if constexpr (kDA) vda[i] = valid ? vda[i] : 0.f;
       }
       const int n_ = kFull ? kEl : nt - q * kEl;
-      if (has_z && (kFull || (r < rows && n_ > 0))) {
+      if (has_z && blockIdx.z == 0 && (kFull || (r < rows && n_ > 0))) {   // one state block writes dz
         IT* pz = gdz + r * sdz + t0 + q * kEl;
         if ((kFull && out_al) || (n_ >= kEl && (reinterpret_cast<uintptr_t>(pz) & 15u) == 0))
           *reinterpret_cast<uint4*>(pz) = f32_to_raw<IT>(dzv);
@@ -338,7 +351,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
     }
     if constexpr (kVarB || kVarC) {
       for (int j = tid; j < NP * kQ; j += blockDim.x) {
-        const bool st_ok = j / kQ < N;  // padded states read B = C = 0
+        const bool st_ok = j / kQ < Nb;  // padded states read B = C = 0
         float v[kEl];
         const int n = j / kQ, s0 = (j % kQ) * kEl;
         if constexpr (kVarB) {
@@ -388,6 +401,19 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
             for (int m = 0; m < 4; ++m) P3[m] += x[m];
           }
         }
+        if (gpp) {  // state block: its sums of the terms, fp32 (the combine kernel finishes them)
+          if (!kFull && (r >= rows || q * kEl + i >= nt)) continue;
+          float* pp = gpp + r * L + t0 + q * kEl + i;
+          const int nv = kFull ? 4 : (nt - (q * kEl + i) < 4 ? nt - (q * kEl + i) : 4);
+          auto put4 = [&](float* dst, const float* v) __attribute__((always_inline)) {
+            if (nv == 4 && (L & 3) == 0) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            else for (int m = 0; m < nv; ++m) dst[m] = v[m];
+          };
+          put4(pp, P1);
+          put4(pp + pp_term, P2);
+          if constexpr (kP3) put4(pp + 2 * pp_term, P3);
+          continue;
+        }
         float dlv[4], uv[4], dyv[4], q1[4], q2[4];
         lds_ldv<4>(&s_dl[p][o], dlv);
         lds_ldv<4>(&s_u[p][o], uv);
@@ -417,6 +443,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
         lds_stv<4>(&s_P1[o], q1);
         lds_stv<4>(&s_P2[o], q2);
       }
+      if (gpp) continue;
       const int n_ = kFull ? kEl : nt - q * kEl;
       if (!kFull && (r >= rows || n_ <= 0)) continue;
       auto put = [&](IT* pp, const float* v) __attribute__((always_inline)) {
@@ -441,9 +468,9 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
 #pragma unroll
     for (int k = 0; k < kS; ++k) {
       if constexpr (kCkLds) {
-        h0[k] = (kk > 0 && n0 + k < N) ? s_ck[(p * kNPmax + n0 + k) * kWave + lane] : 0.f;
+        h0[k] = (kk > 0 && n0 + k < Nb) ? s_ck[(p * kNPmax + n0 + k) * kWave + lane] : 0.f;
       } else {
-        h0[k] = (kk > 0 && lane_ok && n0 + k < N) ? ckp[((b * n_ck + kk - 1) * N + n0 + k) * D + d] : 0.f;
+        h0[k] = (kk > 0 && lane_ok && n0 + k < Nb) ? ckp[((b * n_ck + kk - 1) * N + nb + n0 + k) * D + d] : 0.f;
       }
     }
     // recompute h (and, where kAbLive, A_bar) over the interval.  Otherwise
@@ -639,7 +666,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
     // dB / dC over the wave's channels -> one partial per (cb, b, n, t)
     if constexpr (kVarB || kVarC) {
       const int kq = lane / kCk, jq = lane % kCk;  // lane now owns index v = k * kCk + j
-      const bool wr = lane < kNV && n0 + kq < N && (kFull || jq < Ls);
+      const bool wr = lane < kNV && n0 + kq < Nb && (kFull || jq < Ls);
       const int64_t tg = tile * kTB + ts + jq;
       if constexpr (kVarB) {
         float r;
@@ -652,7 +679,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
           for (int i = 0; i < 64; ++i) r64[i] = i < kNV ? accB[i] : 0.f;
           r = reduce_scatter64(r64, lane);
         }
-        if (wr) ws[wo.dBv + ((cb * a.batch + b) * N + n0 + kq) * L + tg] = r;
+        if (wr) ws[wo.dBv + ((cb * a.batch + b) * N + nb + n0 + kq) * L + tg] = r;
       }
       if constexpr (kVarC) {
         float r;
@@ -665,7 +692,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
           for (int i = 0; i < 64; ++i) r64[i] = i < kNV ? accC[i] : 0.f;
           r = reduce_scatter64(r64, lane);
         }
-        if (wr) ws[wo.dCv + ((cb * a.batch + b) * N + n0 + kq) * L + tg] = r;
+        if (wr) ws[wo.dCv + ((cb * a.batch + b) * N + nb + n0 + kq) * L + tg] = r;
       }
     }
   };
@@ -714,7 +741,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
       else convert(std::false_type{}, tile - 1, p ^ 1);
     }
     __syncthreads();
-    if (w == 0) {  // dD / ddelta_bias terms of this tile, in step order
+    if (w == 0 && !gpp) {  // dD / ddelta_bias terms of this tile, in step order
 #pragma unroll
       for (int g = 0; g < kG; ++g) {
         float q1[4], q2[4];
@@ -734,14 +761,14 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   // per-(b, d, n) and per-(b, d) partials; summed over b by ss_reduce_batch_kernel
 #pragma unroll
   for (int k = 0; k < kS; ++k) {
-    if (lane_ok && n0 + k < N) {
-      const int64_t o = (b * D + d) * N + n0 + k;
+    if (lane_ok && n0 + k < Nb) {
+      const int64_t o = (b * D + d) * N + nb + n0 + k;
       ws[wo.dA + o] = dA_acc[k];
       if constexpr (!kVarB) ws[wo.dBc + o] = dBc_acc[k];
       if constexpr (!kVarC) ws[wo.dCc + o] = dCc_acc[k];
     }
   }
-  if (w == 0 && lane_ok) {
+  if (w == 0 && lane_ok && !gpp) {
     ws[wo.dD + b * D + d] = dD_acc;
     ws[wo.dbias + b * D + d] = dbias_acc;
   }
@@ -805,10 +832,82 @@ template <typename IT, bool kVarB, bool kVarC>
 static hipError_t ss_bwd_reductions(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws,
                                     const SSBwdWs& wo, hipStream_t st, bool batch_only = false);
 
+// State blocks: du, ddelta, ddeltaA from the blocks' term sums (added in block
+// order), by the formulas of ss_bwd_kernel's epilogue, and the per-(b, d) dD
+// (sum of dy u) and ddelta_bias (sum of ddelta) terms for ss_bwd_reductions.
+// One wave per (b, d) row, lanes along L; the lane sums are added across the
+// wave in a fixed order.
+template <typename IT>
+__global__ void __launch_bounds__(256)
+ss_bwd_combine_kernel(const lrnnx_selective_scan_args a, float* __restrict__ ws, const SSBwdWs wo, const int nsb) {
+  const int64_t L = a.seqlen, D = a.dim, BD = a.batch * a.dim;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;   // b * D + d
+  if (r >= BD) return;
+  const int64_t b = r / D, d = r % D;
+  const bool mamba = a.method == LRNNX_MAMBA;
+  const bool p3 = wo.n_terms == 3;
+  const bool has_dA = a.deltaA.ptr != nullptr;
+  const bool dA_on = has_dA && a.method != LRNNX_S7 && a.method != LRNNX_RGLRU;   // deltaA drives A_bar
+  const bool has_z = a.z.ptr != nullptr;
+  const float Dv = a.D.ptr ? static_cast<const float*>(a.D.ptr)[d * a.D.s0] : 0.f;
+  const float bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[d * a.delta_bias.s0] : 0.f;
+  const IT* pu = static_cast<const IT*>(a.u.ptr) + b * a.u.s0 + d * a.u.s1;
+  const IT* pd = static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d * a.delta.s1;
+  const IT* pdo = static_cast<const IT*>(a.dout.ptr) + b * a.dout.s0 + d * a.dout.s1;
+  const IT* pz = has_z ? static_cast<const IT*>(a.z.ptr) + b * a.z.s0 + d * a.z.s1 : nullptr;
+  IT* pdu = static_cast<IT*>(a.du.ptr) + b * a.du.s0 + d * a.du.s1;
+  IT* pddl = static_cast<IT*>(a.ddelta.ptr) + b * a.ddelta.s0 + d * a.ddelta.s1;
+  IT* pddA = has_dA ? static_cast<IT*>(a.ddeltaA.ptr) + b * a.ddeltaA.s0 + d * a.ddeltaA.s1 : nullptr;
+  const float* pp = ws + wo.pp + r * L;
+  const int64_t term = BD * L, blk = wo.n_terms * term;
+  float dD = 0.f, dbias = 0.f;
+  for (int64_t t = lane; t < L; t += kWave) {
+    float P1 = 0.f, P2 = 0.f, P3 = 0.f;
+    for (int z = 0; z < nsb; ++z) {
+      P1 += pp[z * blk + t];
+      P2 += pp[z * blk + term + t];
+      if (p3) P3 += pp[z * blk + 2 * term + t];
+    }
+    const float x = to_f32(pd[t]) + bias;
+    const float dl = a.delta_softplus ? softplus_fast(x) : x;
+    const float uu = to_f32(pu[t]);
+    float dy = to_f32(pdo[t]);
+    if (has_z) {
+      const float zv = to_f32(pz[t]);
+      dy = dy * zv * sigmoid_fast(zv);
+    }
+    float du, ddl;
+    if (mamba) {
+      du = fmaf(dl, P1, Dv * dy);
+      ddl = uu * P1;
+    } else {
+      du = fmaf(Dv, dy, P1);
+      ddl = P3;
+    }
+    if (!dA_on) ddl += P2;
+    const float dd = a.delta_softplus ? ddl * one_minus_exp_neg(dl) : ddl;
+    pdu[t] = from_f32<IT>(du);
+    pddl[t] = from_f32<IT>(dd);
+    if (has_dA) pddA[t] = from_f32<IT>(dA_on ? P2 : 0.f);
+    dD = fmaf(dy, uu, dD);
+    dbias += dd;
+  }
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m >>= 1) {
+    dD += __shfl_xor(dD, m);
+    dbias += __shfl_xor(dbias, m);
+  }
+  if (lane == 0) {
+    ws[wo.dD + r] = dD;
+    ws[wo.dbias + r] = dbias;
+  }
+}
+
 template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
 static hipError_t launch_bwd_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                                const float* ckp, hipStream_t st) {
-  dim3 grid(g.n_cb, (unsigned)a.batch);
+  dim3 grid(g.n_cb, (unsigned)a.batch, (unsigned)g.nsb);
   dim3 block(g.nW * kWave);
   if (g.nW > fwd_nw_max(kS)) return hipErrorInvalidConfiguration;
   // async LDS fetches need 16-byte aligned row starts for every fetched tensor
@@ -828,9 +927,16 @@ static hipError_t launch_bwd_t(const lrnnx_selective_scan_args& a, const SSGeom&
                       al(a.ddeltaA.ptr, a.ddeltaA.s0, a.ddeltaA.s1) && (!has_z || al(a.dz.ptr, a.dz.s0, a.dz.s1));
   const int flags = (in_ok ? kFlagAsyncIn : 0) | (out_ok ? kFlagAlignedOut : 0);
   hipLaunchKernelGGL((ss_bwd_kernel<IT, kS, kMethod, kVarB, kVarC, kDA>), grid, block, 0, st, a, g.CB, g.n_ck, ws,
-                     wo, ckp, flags);
+                     wo, ckp, flags, g.nsb);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (g.nsb > 1) {
+    const int64_t rows = a.batch * a.dim;
+    hipLaunchKernelGGL(ss_bwd_combine_kernel<IT>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, a, ws, wo,
+                       g.nsb);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   return ss_bwd_reductions<IT, kVarB, kVarC>(a, g, ws, wo, st);
 }
 
@@ -905,7 +1011,6 @@ static hipError_t launch_bwd_s(const lrnnx_selective_scan_args& a, const SSGeom&
     case 1: return launch_bwd_bc<IT, 1, kMethod>(a, g, ws, wo, ckp, st);
     case 4: return launch_bwd_bc<IT, 4, kMethod>(a, g, ws, wo, ckp, st);
     case 8: return launch_bwd_bc<IT, 8, kMethod>(a, g, ws, wo, ckp, st);
-    case 32: return launch_bwd_bc<IT, 32, kMethod>(a, g, ws, wo, ckp, st);
   }
   return hipErrorInvalidValue;
 }

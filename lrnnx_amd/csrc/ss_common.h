@@ -16,10 +16,12 @@
 
 namespace lrnnx {
 
-// States per wave by d_state; the backward stores kS * kCk values of A_bar
-// and h per lane, so kS * kCk <= 64 keeps that at <= 128 VGPRs and fits the
-// per-lane dB/dC block into one 64-value reduce-scatter.
-__host__ __device__ constexpr int ck_for(int kS) { return kS == 1 ? 16 : 64 / kS; }
+// Checkpoint interval by states per wave; the backward stores kS * kCk values
+// of A_bar and h per lane, so kS * kCk <= 64 keeps that at <= 128 VGPRs and
+// fits the per-lane dB/dC block into one 64-value reduce-scatter.  kS = 32 is
+// the forward's fallback for d_state > 64 without a workspace (ss_geom); it
+// writes the interval of the state-block backward (kS = 8) that reads them.
+__host__ __device__ constexpr int ck_for(int kS) { return kS == 1 ? 16 : (kS == 32 ? 8 : 64 / kS); }
 // backward tile length along L (a whole number of checkpoint intervals) and
 // forward tile length, sized so that every instantiation fits 160 KB of LDS
 __host__ __device__ constexpr int tb_for(int kS) { return kS >= 8 ? 8 : 16; }
@@ -33,8 +35,7 @@ constexpr int kFlagAlignedOut = 2;  // every written sequence tensor has 16-byte
 inline int pick_kS(int64_t N) {
   if (N <= 4) return 1;
   if (N <= 16) return 4;
-  if (N <= 64) return 8;
-  return 32;
+  return 8;
 }
 
 __host__ __device__ constexpr bool exp_family_m(int m) {
@@ -111,11 +112,16 @@ __host__ __device__ constexpr bool uses_deltaA() {
   return kMethod != LRNNX_S7 && kMethod != LRNNX_RGLRU;
 }
 
-// Launch geometry shared by forward and backward.
+// Launch geometry shared by forward and backward.  d_state > 64 runs in
+// state blocks: nsb workgroups per (channel block, b) along grid z, each with
+// nW * kS state slots (the last block's tail is padding).  Their sums over
+// states (y; the du / ddelta terms) are fp32 partials in a workspace, added in
+// block order by a combine kernel.
 struct SSGeom {
   int CB;        // channels per workgroup (<= 64, divides D/G when G > 1)
   int n_cb;      // channel blocks
   int kS, nW;    // states per wave, waves per workgroup
+  int nsb;       // state blocks (1 for d_state <= 64)
   int ck;        // checkpoint interval (steps)
   int64_t n_ck;  // checkpoints per (b, d)
 };
@@ -132,10 +138,18 @@ inline SSGeom ss_geom(const lrnnx_selective_scan_args& a) {
   }
   g.n_cb = (int)((a.dim + g.CB - 1) / g.CB);
   g.kS = pick_kS(a.dstate);
-  g.nW = (int)((a.dstate + g.kS - 1) / g.kS);
+  g.nsb = (int)((a.dstate + 63) / 64);
+  const int64_t per_blk = (a.dstate + g.nsb - 1) / g.nsb;   // states per block, balanced
+  g.nW = (int)((per_blk + g.kS - 1) / g.kS);
   g.ck = ck_for(g.kS);
   g.n_ck = (a.seqlen + g.ck - 1) / g.ck;
   return g;
+}
+
+// Bytes of forward workspace for the state blocks' partial y (0: one block).
+inline int64_t ss_fwd_blocks_ws_bytes(const lrnnx_selective_scan_args& a) {
+  const SSGeom g = ss_geom(a);
+  return g.nsb > 1 ? (int64_t)g.nsb * a.batch * a.dim * a.seqlen * (int64_t)sizeof(float) : 0;
 }
 
 }  // namespace lrnnx

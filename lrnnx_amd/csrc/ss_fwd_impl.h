@@ -39,9 +39,12 @@ __host__ __device__ constexpr int fwd_tile() {
 // most waves a workgroup can have for a given kS (ceil(256 / kS) capped at 8)
 __host__ __device__ constexpr int fwd_nw_max(int kS) { return (kS == 8 || kS == 32) ? 8 : 4; }
 
+// ypart: with state blocks (grid z > 1) and outputs, the block's partial y
+// (sum over its states of C h, fp32, [block][b][d][L]) instead of out / out_z.
 template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
 __global__ void __launch_bounds__(512)
-ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_ck, const int flags) {
+ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_ck, const int flags,
+              float* __restrict__ ypart) {
   constexpr int kCk = ck_for(kS);
   constexpr int kT = fwd_tile<IT, kS>();
   constexpr int kEl = 16 / sizeof(IT);   // elements per 16-byte block
@@ -74,7 +77,7 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int64_t b = blockIdx.y;
   const int64_t D = a.dim, L = a.seqlen;
-  const int N = (int)a.dstate;
+  const int N = (int)a.dstate;                 // all states (layout of x and the checkpoints)
   const int64_t d0 = (int64_t)blockIdx.x * CB;
   const int rows = (int)((D - d0) < CB ? (D - d0) : CB);   // valid channels of this block
   const int64_t d = d0 + lane;
@@ -82,6 +85,8 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   const int64_t grp = (a.var_B || a.var_C) ? d0 / (D / a.n_groups) : 0;
   const int n0 = w * kS;
   const int NP = nW * kS;
+  const int nb = (int)blockIdx.z * NP;               // first state of this state block
+  const int Nb = N - nb < NP ? N - nb : NP;          // its real states
   constexpr bool has_dA = kDA;  // deltaA drives A_bar (never for s7 / rglru)
   const bool has_bias = a.delta_bias.ptr != nullptr;
   const bool has_D = a.D.ptr != nullptr;
@@ -94,10 +99,11 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   const IT* gd = static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d0 * a.delta.s1;
   const IT* gz = has_z ? static_cast<const IT*>(a.z.ptr) + b * a.z.s0 + d0 * a.z.s1 : nullptr;
   const IT* gdA = has_dA ? static_cast<const IT*>(a.deltaA.ptr) + b * a.deltaA.s0 + d0 * a.deltaA.s1 : nullptr;
-  const IT* gB = kVarB ? static_cast<const IT*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1 : nullptr;
-  const IT* gC = kVarC ? static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1 : nullptr;
-  IT* go = a.out.ptr ? static_cast<IT*>(a.out.ptr) + b * a.out.s0 + d0 * a.out.s1 : nullptr;
-  IT* goz = a.out_z.ptr ? static_cast<IT*>(a.out_z.ptr) + b * a.out_z.s0 + d0 * a.out_z.s1 : nullptr;
+  const IT* gB = kVarB ? static_cast<const IT*>(a.B.ptr) + b * a.B.s0 + grp * a.B.s1 + nb * a.B.s2 : nullptr;
+  const IT* gC = kVarC ? static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1 + nb * a.C.s2 : nullptr;
+  IT* go = (a.out.ptr && !ypart) ? static_cast<IT*>(a.out.ptr) + b * a.out.s0 + d0 * a.out.s1 : nullptr;
+  IT* goz = (a.out_z.ptr && !ypart) ? static_cast<IT*>(a.out_z.ptr) + b * a.out_z.s0 + d0 * a.out_z.s1 : nullptr;
+  float* gyp = ypart ? ypart + (((int64_t)blockIdx.z * a.batch + b) * D + d0) * L : nullptr;
   const uint32_t su = (uint32_t)a.u.s1, sd = (uint32_t)a.delta.s1, sz = (uint32_t)a.z.s1;
   const uint32_t sdA = (uint32_t)a.deltaA.s1, sBn = (uint32_t)a.B.s2, sCn = (uint32_t)a.C.s2;
   const uint32_t so = (uint32_t)a.out.s1, soz = (uint32_t)a.out_z.s1;
@@ -111,13 +117,14 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
 #pragma unroll
     for (int k = 0; k < kS; ++k) {
       const int n = n0 + k;
-      const bool ok = lane_ok && n < N;
-      const float Av = ok ? Ap[d * a.A.s0 + n * a.A.s1] : (kMethod == LRNNX_RGLRU ? 0.5f : -1.f);
+      const bool ok = lane_ok && n < Nb;
+      const int64_t ng = nb + n;
+      const float Av = ok ? Ap[d * a.A.s0 + ng * a.A.s1] : (kMethod == LRNNX_RGLRU ? 0.5f : -1.f);
       Araw[k] = Av;
       invA[k] = 1.f / Av;
       a2[k] = prep_a2<kMethod>(Av);
-      const float bc = (!kVarB && ok) ? Bp[d * a.B.s0 + n * a.B.s1] : 1.f;
-      const float cc = (!kVarC && ok) ? Cp[d * a.C.s0 + n * a.C.s1] : 1.f;
+      const float bc = (!kVarB && ok) ? Bp[d * a.B.s0 + ng * a.B.s1] : 1.f;
+      const float cc = (!kVarC && ok) ? Cp[d * a.C.s0 + ng * a.C.s1] : 1.f;
       cout_c[k] = ok ? (kVarB ? 1.f : bc) * (kVarC ? 1.f : cc) : 0.f;
       h[k] = 0.f;
       prodA[k] = 1.f;
@@ -151,8 +158,8 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
     tile_fetch_async<IT, kQ>(gu + t0, su, CB, s_raw_u[buf], w, nW, lane);
     tile_fetch_async<IT, kQ>(gd + t0, sd, CB, s_raw_d, w, nW, lane);
     if (has_z) tile_fetch_async<IT, kQ>(gz + t0, sz, CB, s_raw_z[buf], w, nW, lane);
-    if constexpr (kVarB) tile_fetch_async<IT, kQ>(gB + t0, sBn, N, s_raw_bc, w, nW, lane);
-    if constexpr (kVarC) tile_fetch_async<IT, kQ>(gC + t0, sCn, N, s_raw_bc + kRawBC, w, nW, lane);
+    if constexpr (kVarB) tile_fetch_async<IT, kQ>(gB + t0, sBn, Nb, s_raw_bc, w, nW, lane);
+    if constexpr (kVarC) tile_fetch_async<IT, kQ>(gC + t0, sCn, Nb, s_raw_bc + kRawBC, w, nW, lane);
     if constexpr (kDA) tile_fetch_async<IT, kQ>(gdA + t0, sdA, CB, s_raw_dA, w, nW, lane);
   };
   auto fetch_sync = [&](int64_t tile, int buf) __attribute__((always_inline)) {
@@ -161,8 +168,8 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
     tile_fetch_sync<IT, kQ>(gu + t0, su, kWave, rows, nt, s_raw_u[buf], tid, blockDim.x);
     tile_fetch_sync<IT, kQ>(gd + t0, sd, kWave, rows, nt, s_raw_d, tid, blockDim.x);
     if (has_z) tile_fetch_sync<IT, kQ>(gz + t0, sz, kWave, rows, nt, s_raw_z[buf], tid, blockDim.x);
-    if constexpr (kVarB) tile_fetch_sync<IT, kQ>(gB + t0, sBn, NP, N, nt, s_raw_bc, tid, blockDim.x);
-    if constexpr (kVarC) tile_fetch_sync<IT, kQ>(gC + t0, sCn, NP, N, nt, s_raw_bc + kRawBC, tid, blockDim.x);
+    if constexpr (kVarB) tile_fetch_sync<IT, kQ>(gB + t0, sBn, NP, Nb, nt, s_raw_bc, tid, blockDim.x);
+    if constexpr (kVarC) tile_fetch_sync<IT, kQ>(gC + t0, sCn, NP, Nb, nt, s_raw_bc + kRawBC, tid, blockDim.x);
     if constexpr (kDA) tile_fetch_sync<IT, kQ>(gdA + t0, sdA, kWave, rows, nt, s_raw_dA, tid, blockDim.x);
   };
 
@@ -208,7 +215,7 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
     if constexpr (kVarB || kVarC) {
       const char* rbc = s_raw_bc;
       for (int j = tid; j < NP * kQ; j += blockDim.x) {
-        const bool st_ok = j / kQ < N;  // padded states read B = C = 0
+        const bool st_ok = j / kQ < Nb;  // padded states read B = C = 0
         float v[kEl];
         if constexpr (kVarB) {
           raw_to_f32<IT>(*reinterpret_cast<const uint4*>(rbc + 16 * j), v);
@@ -232,6 +239,28 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
     for (int j = tid; j < kWave * kQ; j += blockDim.x) {
       const int r = j / kQ, q = j % kQ;
       if (!kFull && r >= rows) continue;
+      if (gyp) {  // state block: its partial y, fp32 (D u and the gate come in the combine)
+        float y[kEl];
+#pragma unroll
+        for (int i = 0; i < kEl; i += 4) {
+          const int g = (q * kEl + i) / 4;
+          float4 acc = *reinterpret_cast<const float4*>(sY + (g * kWave + r) * 4);
+          for (int ww = 1; ww < nW; ++ww) {
+            const float4 p = *reinterpret_cast<const float4*>(sY + ((ww * kG + g) * kWave + r) * 4);
+            acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
+          }
+          y[i] = acc.x; y[i + 1] = acc.y; y[i + 2] = acc.z; y[i + 3] = acc.w;
+        }
+        float* p = gyp + r * L + t0 + q * kEl;
+        const int n_ = kFull ? kEl : nt - q * kEl;
+        if (n_ >= kEl && (L & 3) == 0) {
+#pragma unroll
+          for (int i = 0; i < kEl; i += 4) *reinterpret_cast<float4*>(p + i) = make_float4(y[i], y[i + 1], y[i + 2], y[i + 3]);
+        } else {
+          for (int i = 0; i < (n_ < kEl ? n_ : kEl); ++i) p[i] = y[i];
+        }
+        continue;
+      }
       const float Dv = s_Dv[r];
       float vu[kEl], y[kEl];
       raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_u[buf] + 16 * j), vu);
@@ -290,21 +319,21 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
     const int64_t kk = tg / kCk;
 #pragma unroll
     for (int k = 0; k < kS; ++k)
-      if (lane_ok && n0 + k < N) ckp[((b * n_ck + kk) * N + n0 + k) * D + d] = h[k];
+      if (lane_ok && n0 + k < Nb) ckp[((b * n_ck + kk) * N + nb + n0 + k) * D + d] = h[k];
   };
   auto store_x = [&](int64_t tg) __attribute__((always_inline)) {  // reference chunk carry at step tg
     const int64_t c = tg / kXChunk;
 #pragma unroll
     for (int k = 0; k < kS; ++k) {
-      if (lane_ok && n0 + k < N) {
+      if (lane_ok && n0 + k < Nb) {
         float ac;
         if constexpr (exp_family<kMethod>())
           ac = fast_exp2(a2[k] * sumdt);
         else
           ac = prodA[k];
         float* xr = xp + ((b * D + d) * n_xc + c) * 2 * N;
-        xr[2 * (n0 + k)] = ac;
-        xr[2 * (n0 + k) + 1] = h[k];
+        xr[2 * (nb + n0 + k)] = ac;
+        xr[2 * (nb + n0 + k) + 1] = h[k];
       }
     }
   };
@@ -401,9 +430,34 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   }
 }
 
+// State blocks: out = sum over the blocks' partial y in block order + D u,
+// out_z = out silu(z).  One thread per (b, d, t), consecutive threads along t.
+template <typename IT>
+__global__ void __launch_bounds__(256)
+ss_fwd_combine_kernel(const lrnnx_selective_scan_args a, const float* __restrict__ ypart, const int nsb) {
+  const int64_t L = a.seqlen, D = a.dim, BD = a.batch * a.dim;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= BD * L) return;
+  const int64_t t = i % L, r = i / L, b = r / D, d = r % D;
+  float y = 0.f;
+  for (int z = 0; z < nsb; ++z) y += ypart[(z * BD + r) * L + t];
+  if (a.D.ptr) {
+    const float u = to_f32(static_cast<const IT*>(a.u.ptr)[b * a.u.s0 + d * a.u.s1 + t]);
+    y = fmaf(static_cast<const float*>(a.D.ptr)[d * a.D.s0], u, y);
+  }
+  if (a.out.ptr) static_cast<IT*>(a.out.ptr)[b * a.out.s0 + d * a.out.s1 + t] = from_f32<IT>(y);
+  if (a.z.ptr && a.out_z.ptr) {
+    const float z = to_f32(static_cast<const IT*>(a.z.ptr)[b * a.z.s0 + d * a.z.s1 + t]);
+    static_cast<IT*>(a.out_z.ptr)[b * a.out_z.s0 + d * a.out_z.s1 + t] = from_f32<IT>(y * (z * sigmoid_fast(z)));
+  }
+}
+
 template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
 static hipError_t launch_fwd_t(const lrnnx_selective_scan_args& a, const SSGeom& g, hipStream_t st) {
-  dim3 grid(g.n_cb, (unsigned)a.batch);
+  // state blocks write partial y to the workspace when there are outputs (ss_fwd_blocks_ws_bytes;
+  // launch_fwd_s falls back to one block when the workspace is missing)
+  float* ypart = (g.nsb > 1 && (a.out.ptr || a.out_z.ptr)) ? static_cast<float*>(a.workspace) : nullptr;
+  dim3 grid(g.n_cb, (unsigned)a.batch, (unsigned)g.nsb);
   dim3 block(g.nW * kWave);
   if (g.nW > fwd_nw_max(kS)) return hipErrorInvalidConfiguration;
   // async LDS fetches need 16-byte aligned row starts for every fetched tensor
@@ -418,7 +472,12 @@ static hipError_t launch_fwd_t(const lrnnx_selective_scan_args& a, const SSGeom&
   const bool out_ok = al(a.out.ptr, a.out.s0, a.out.s1) && al(a.out_z.ptr, a.out_z.s0, a.out_z.s1);
   const int flags = (in_ok ? kFlagAsyncIn : 0) | (out_ok ? kFlagAlignedOut : 0);
   hipLaunchKernelGGL((ss_fwd_kernel<IT, kS, kMethod, kVarB, kVarC, kDA>), grid, block, 0, st, a, g.CB, g.n_ck,
-                     flags);
+                     flags, ypart);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || ypart == nullptr) return e;
+  const int64_t n = a.batch * a.dim * a.seqlen;
+  hipLaunchKernelGGL(ss_fwd_combine_kernel<IT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a,
+                     static_cast<const float*>(ypart), g.nsb);
   return hipGetLastError();
 }
 
@@ -440,6 +499,17 @@ static hipError_t launch_fwd_bc(const lrnnx_selective_scan_args& a, const SSGeom
 
 template <typename IT, int kMethod>
 static hipError_t launch_fwd_s(const lrnnx_selective_scan_args& a, const SSGeom& g, hipStream_t st) {
+  if (g.nsb > 1 && (a.out.ptr || a.out_z.ptr) &&
+      (a.workspace == nullptr || a.workspace_bytes < ss_fwd_blocks_ws_bytes(a) ||
+       (reinterpret_cast<uintptr_t>(a.workspace) & 15u) != 0)) {
+    // no room for the blocks' partial y: every state in one workgroup, 32 per
+    // wave (slower: it spills), with the checkpoint interval of the blocks
+    SSGeom g1 = g;
+    g1.kS = 32;
+    g1.nW = (int)((a.dstate + 31) / 32);
+    g1.nsb = 1;
+    return launch_fwd_bc<IT, 32, kMethod>(a, g1, st);
+  }
   switch (g.kS) {
     case 1: return launch_fwd_bc<IT, 1, kMethod>(a, g, st);
     case 4: return launch_fwd_bc<IT, 4, kMethod>(a, g, st);

@@ -350,3 +350,85 @@ def test_dirac_binding_fwd_then_bwd(dev, monkeypatch, save, no_split):
     for i, k in enumerate(("u", "delta", "A", "B", "C", "D", "delta_bias")):
         close(f"d{k}", g[i], rg[k], 1e-4, 1e-4 if k in ("A", "D", "delta_bias") else 1e-5)
     close("dz", g[7], rg["z"], 1e-4, 1e-5)
+
+
+# d_state > 64 (real weights): blocks of at most 64 states along the grid's z
+# dimension, on the 8-states-per-wave kernels; their sums over states (y, and
+# the du / ddelta / ddeltaA terms) are fp32 partials combined in block order.
+@pytest.mark.parametrize("method,N,extra", [
+    ("mamba", 100, {}),                                  # blocks of 56 + 44 states
+    ("mamba", 128, dict(groups=2)),
+    ("mamba", 128, dict(varB=False, varC=False)),
+    ("mamba", 96, dict(with_deltaA=True)),
+    ("mamba", 200, dict(has_z=False, softplus=False)),   # four blocks of 56, 56, 56, 32
+    ("zoh", 80, {}),
+    ("zoh", 96, dict(with_deltaA=True)),
+    ("bilinear", 72, {}),
+    ("dirac", 128, dict(varB=True, varC=False)),
+], ids=lambda v: str(v) if not isinstance(v, dict) else "-".join(f"{k}={x}" for k, x in v.items()) or "default")
+def test_state_blocks_vs_oracle(dev, method, N, extra):
+    print(f"state blocks: {method} N={N} {extra}", flush=True)
+    _run(dev, 2, 64, 200, N, method=method, seed=61 + N, **extra)
+
+
+def test_state_blocks_one_state_methods(dev):
+    """s7 and rglru with 80 states (constant B / C), on the state blocks."""
+    _run(dev, 2, 64, 96, 80, method="s7", varB=False, varC=False, has_z=False, has_D=True, has_bias=False,
+         softplus=False, seed=63)
+    A = torch.rand(64, 80, generator=torch.Generator().manual_seed(64)) * 0.5 + 0.45
+    _run(dev, 2, 64, 96, 80, method="rglru", varB=False, varC=False, has_z=False, has_D=False, has_bias=False,
+         softplus=False, A_override=A, seed=64)
+
+
+def test_state_blocks_long_chunks_bf16(dev):
+    # the 2048-step chunk carries of every block (last_state) across a chunk end
+    _run(dev, 1, 64, 2100, 128, itype=torch.bfloat16, seed=65)
+
+
+def test_state_blocks_without_workspace(dev):
+    """d_state > 64 without a forward workspace: every state in one workgroup
+    (the fallback), with the checkpoint interval of the blocks.  out, out_z, x
+    and the checkpoints match the state-block forward; the allocation-free
+    forward takes the same path; the backward (state blocks) from the
+    fallback's checkpoints matches the fp64 oracle."""
+    from lrnnx_amd import _lib
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    Bt, D, L, N = 2, 64, 160, 128
+    inp = R.make_selective_inputs(Bt, D, L, N, seed=66)
+    dout = torch.randn(Bt, D, L, generator=torch.Generator().manual_seed(67))
+    ro, rl, rg = oracle_selective(inp, "mamba", True, None, True, dout)
+    d = to_dev(inp, dev)
+    d["B"], d["C"] = d["B"].unsqueeze(1).contiguous(), d["C"].unsqueeze(1).contiguous()
+
+    def args():
+        return ssc.build_args(d["u"], d["delta"], d["A"], d["B"], d["C"], d["D"], d["z"], d["delta_bias"], None,
+                              True, "mamba")
+
+    a = args()
+    assert _lib.lib().lrnnx_selective_scan_workspace_size(a, 0) == 2 * Bt * D * L * 4   # two blocks of 64
+    res = {"blocks": ssc.run_fwd(a, d["u"], d["delta"], d["A"], d["z"], want_ckpt=True)}
+    for entry in ("lrnnx_selective_scan_fwd", "lrnnx_selective_scan_fwd_noalloc"):
+        a = args()
+        out, out_z = torch.empty_like(d["u"]), torch.empty_like(d["z"])
+        x = torch.empty((Bt, D, 1, 2 * N), dtype=torch.float32, device=dev)
+        ckpt = torch.empty(_lib.lib().lrnnx_selective_scan_ckpt_size(a) // 4, dtype=torch.float32, device=dev)
+        a.out, a.out_z = _lib.view(out, 2), _lib.view(out_z, 2)
+        a.x, a.ckpt = x.data_ptr(), ckpt.data_ptr()
+        a.workspace, a.workspace_bytes = None, 0
+        _lib.check(getattr(_lib.lib(), entry)(a, _lib.stream_of(d["u"])), entry)
+        torch.cuda.synchronize()
+        res[entry] = (out, x, out_z, ckpt)
+    ref = res["blocks"]
+    for entry in ("lrnnx_selective_scan_fwd", "lrnnx_selective_scan_fwd_noalloc"):
+        for name, g_, r_ in zip(("out", "x", "out_z", "ckpt"), res[entry], ref):
+            close(f"{name} ({entry})", g_, r_.cpu().double(), 1e-5, 1e-5)
+    out, x, out_z, ckpt = res["lrnnx_selective_scan_fwd"]
+    close("out_z vs oracle", out_z, ro, 1e-4, 1e-5)
+    g = ssc.run_bwd(args(), d["u"], d["delta"], d["A"], d["B"], d["C"], d["D"], d["z"], d["delta_bias"], None,
+                    dout.to(dev), out, ckpt)
+    torch.cuda.synchronize()
+    for i, k in enumerate(("u", "delta", "A", "B", "C", "D", "delta_bias")):
+        gk = g[i].squeeze(1) if k in ("B", "C") else g[i]
+        close(f"d{k}", gk, rg[k], 1e-4, 1e-4 if k in ("A", "D", "delta_bias") else 1e-5)
+    close("dz", g[7], rg["z"], 1e-4, 1e-5)
