@@ -244,7 +244,7 @@ class ConvStep:
         self.L_.check(self.L_.lib().lrnnx_causal_conv1d_bwd(self.a, self.stream.cuda_stream), "conv bwd")
 
 
-def decode_cfg4(torch, dev, n_layer=24, reps=50):
+def decode_cfg4(torch, dev, n_layer=24, reps=50, N=16):
     """Config 4's decode step on the scan side: ``selective_state_update`` at the
     Mamba-130m decode shape (batch 64, d_inner 1536, d_state 16, bf16 state,
     z gate, dt_bias + softplus) for each of 24 layers, run eagerly and as one
@@ -253,7 +253,7 @@ def decode_cfg4(torch, dev, n_layer=24, reps=50):
     (4 x 64 x 1536 x 2) plus B, C (2 x 64 x 16 x 2)."""
     from lrnnx_amd import selective_state_update
     g = torch.Generator(device=dev).manual_seed(4)
-    Bt, D, N = 64, 1536, 16
+    Bt, D = 64, 1536
     bf = torch.bfloat16
     layers = []
     for _ in range(n_layer):
@@ -533,7 +533,9 @@ def dstate_sweep(torch, dev, ss, L_):
     config-2 shape (B=8, D=1536, L=2048, bf16, mamba, variable B/C, z) for
     d_state 1 .. 256: the fast kernels up to 16, the general kernels above
     (state blocks past 64).  Event-timed medians of 10 after 3 warm-ups; the
-    general kernels also at 16 (LRNNX_SCAN_GENERIC=1) for comparison."""
+    general kernels also at 16 (LRNNX_SCAN_GENERIC=1) for comparison.  Then
+    the decode update (decode_cfg4, one captured 24-layer graph) at d_state
+    16, 64, 128 and 256."""
     import statistics
 
     Bt, D, L = 8, 1536, 2048
@@ -572,6 +574,11 @@ def dstate_sweep(torch, dev, ss, L_):
         _log(f"d_state sweep {key}: {res[key]}")
         del st, inp
         torch.cuda.empty_cache()
+    for N in (16, 64, 128, 256):   # the decode update at config 4's decode shape, one 24-layer graph
+        r = decode_cfg4(torch, dev, N=N)
+        res[f"decode_n{N}"] = {"graph_us_per_layer": round(r["graph_us_per_token"] / r["layers"], 2),
+                               "graph_GB_s": r["graph_GB_s"]}
+        _log(f"d_state sweep decode_n{N}: {res[f'decode_n{N}']}")
     return res
 
 
@@ -905,7 +912,8 @@ def main():
                     help="time only the other discretisations / one-state path / complex weights (for a kernel "
                          "trace of those kernels), print their JSON, then exit")
     ap.add_argument("--dstate-sweep", action="store_true",
-                    help="time fwd / bwd at the config-2 shape for d_state 1 .. 256, print the JSON, then exit")
+                    help="time fwd / bwd at the config-2 shape for d_state 1 .. 256 and the decode update "
+                         "at d_state 16 .. 256, print the JSON, then exit")
     ap.add_argument("--summarize-counters", nargs="+", metavar="COUNTER_CSV",
                     help="print a markdown table of rocprofv3 --pmc counter_collection.csv files, then exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",

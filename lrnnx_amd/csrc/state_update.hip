@@ -10,9 +10,10 @@
 //   state <- state * A_bar + B_bar * x   (stored in the state dtype, in place)
 //   out = sum_n state_n C_n (+ D x), times silu(z).
 // General kernel: one thread owns one (batch, head, channel) row of `state`;
-// consecutive threads own consecutive channels.  At d_state 16, 32 or 64 with
-// unit-stride aligned rows a row is split over 2 to 16 adjacent lanes, each
-// reading and writing 16 bytes after all its operands are loaded.
+// consecutive threads own consecutive channels.  At d_state 16, 32, 64, 128 or
+// 256 with unit-stride aligned rows a row is split over 2 to 16 adjacent
+// lanes, each reading and writing 16 to 64 bytes after all its operands are
+// loaded.
 #include "common.h"
 
 namespace lrnnx {
@@ -53,15 +54,17 @@ __device__ __forceinline__ void discretize1(float An, float Bn, float dt, float 
 // Row-at-once update for d_state == kN with unit-stride, 16-byte aligned state
 // / A rows and unit-stride B / C (checked on the host).  A row is split over
 // kSplit = kN / kV adjacent lanes (2 to 16, an aligned group inside one 16-lane
-// DPP row), each owning kV entries = 16 bytes of state, so every state access
-// of a wave is one contiguous 1 KiB; the lanes' partial outputs are summed with
+// DPP row), each owning kV entries: 16 bytes of state, or kN / 16 entries when
+// that is more (d_state 128 and 256 keep 16 lanes per row), so every state
+// access of a wave is contiguous; the lanes' partial outputs are summed with
 // DPP (quad xor 1, xor 2, then half-row and row mirrors).  All types are compile-time (ST: state;
 // XT: x, dt, z, deltaA, B, C and out), and a lane loads all its operands
 // before it computes and stores, so a row costs one round trip to memory.
 template <typename ST, typename XT, int kMethod, int kN>
 __global__ void __launch_bounds__(256) state_update_rows(const lrnnx_state_update_args a) {
-  constexpr int kV = 16 / sizeof(ST);   // state entries per lane (one 16-byte access)
-  constexpr int kSplit = kN / kV;       // lanes per row: 2 (16-bit state) or 4 (fp32)
+  constexpr int kVB = 16 / (int)sizeof(ST);        // state entries per 16-byte access
+  constexpr int kV = kN / 16 > kVB ? kN / 16 : kVB;   // state entries per lane
+  constexpr int kSplit = kN / kV;                     // lanes per row
   static_assert(kSplit == 2 || kSplit == 4 || kSplit == 8 || kSplit == 16, "a row spans 2 to 16 lanes");
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t d = t / kSplit;
@@ -76,11 +79,12 @@ __global__ void __launch_bounds__(256) state_update_rows(const lrnnx_state_updat
   const XT* __restrict__ Bp = static_cast<const XT*>(a.B) + b * a.B_s0 + g * a.B_s1 + part * kV;
   const XT* __restrict__ Cp = static_cast<const XT*>(a.C) + b * a.C_s0 + g * a.C_s1 + part * kV;
   float sv[kV], Av[kV], Bv[kV], Cv[kV];
-  {
-    const uint4 raw = *reinterpret_cast<const uint4*>(state);
+#pragma unroll
+  for (int c = 0; c < kV / kVB; ++c) {
+    const uint4 raw = reinterpret_cast<const uint4*>(state)[c];
     const ST* e = reinterpret_cast<const ST*>(&raw);
 #pragma unroll
-    for (int v = 0; v < kV; ++v) sv[v] = to_f32(e[v]);
+    for (int v = 0; v < kVB; ++v) sv[c * kVB + v] = to_f32(e[v]);
   }
 #pragma unroll
   for (int q = 0; q < kV / 4; ++q) {
@@ -107,17 +111,19 @@ __global__ void __launch_bounds__(256) state_update_rows(const lrnnx_state_updat
   if (a.dt_softplus) dt = softplus20(dt);
   const float dAv = a.deltaA ? dAraw : dt;
   float acc = 0.f;
-  {
+#pragma unroll
+  for (int c = 0; c < kV / kVB; ++c) {
     uint4 raw;
     ST* e = reinterpret_cast<ST*>(&raw);
 #pragma unroll
-    for (int v = 0; v < kV; ++v) {
+    for (int v = 0; v < kVB; ++v) {
+      const int i = c * kVB + v;
       float Ab, Bb;
-      discretize1<kMethod>(Av[v], Bv[v], dt, dAv, Ab, Bb);
-      e[v] = from_f32<ST>(fmaf(sv[v], Ab, Bb * x));
-      acc = fmaf(to_f32(e[v]), Cv[v], acc);
+      discretize1<kMethod>(Av[i], Bv[i], dt, dAv, Ab, Bb);
+      e[v] = from_f32<ST>(fmaf(sv[i], Ab, Bb * x));
+      acc = fmaf(to_f32(e[v]), Cv[i], acc);
     }
-    *reinterpret_cast<uint4*>(state) = raw;
+    reinterpret_cast<uint4*>(state)[c] = raw;
   }
   // every lane of the group ends with the group's sum: xor 1 and xor 2 sum a
   // quad, the half-row mirror pairs quads 0 / 1, the row mirror halves 0 / 1
@@ -179,12 +185,13 @@ __global__ void __launch_bounds__(256) state_update_kernel(const lrnnx_state_upd
   }
 }
 
-// the row-at-once kernel's layout requirements (d_state 16, 32 or 64)
+// the row-at-once kernel's layout requirements (d_state 16, 32, 64, 128 or 256)
 template <typename ST>
 static bool su_rows_ok(const lrnnx_state_update_args& a) {
   const int64_t es = sizeof(ST);
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  return (a.dstate == 16 || a.dstate == 32 || a.dstate == 64) && a.state_s3 == 1 && a.A_s2 == 1 && a.B_s2 == 1 && a.C_s2 == 1 && al16(a.state) &&
+  return (a.dstate == 16 || a.dstate == 32 || a.dstate == 64 || a.dstate == 128 || a.dstate == 256) &&
+         a.state_s3 == 1 && a.A_s2 == 1 && a.B_s2 == 1 && a.C_s2 == 1 && al16(a.state) &&
          al16(a.A) && (a.state_s0 * es) % 16 == 0 && (a.state_s1 * es) % 16 == 0 && (a.state_s2 * es) % 16 == 0 &&
          (a.A_s0 * 4) % 16 == 0 && (a.A_s1 * 4) % 16 == 0;
 }
@@ -193,8 +200,9 @@ static bool su_rows_ok(const lrnnx_state_update_args& a) {
 // instantiation (x / B / C of the state's own type, or 16-bit with an fp32 state).
 template <typename ST, int kMethod, int kN>
 static bool su_rows_launch(const lrnnx_state_update_args& a, dim3 grid, hipStream_t st) {
-  // kSplit lanes per row (kN entries, 16 / sizeof(ST) per lane)
-  constexpr int64_t kSplit = kN / (16 / sizeof(ST));
+  // kSplit lanes per row (as in state_update_rows)
+  constexpr int64_t kVB = 16 / sizeof(ST);
+  constexpr int64_t kSplit = kN / (kN / 16 > kVB ? kN / 16 : kVB);
   const dim3 rg((unsigned)((a.dim * kSplit + 255) / 256), grid.y, grid.z);
   if (a.x_type == a.state_type) {
     hipLaunchKernelGGL((state_update_rows<ST, ST, kMethod, kN>), rg, dim3(256), 0, st, a);
@@ -216,9 +224,11 @@ static bool su_rows_launch(const lrnnx_state_update_args& a, dim3 grid, hipStrea
 template <typename ST, int kMethod>
 static void su_launch(const lrnnx_state_update_args& a, dim3 grid, hipStream_t st) {
   if (su_rows_ok<ST>(a) && a.bc_type == a.x_type) {
-    const bool done = a.dstate == 16   ? su_rows_launch<ST, kMethod, 16>(a, grid, st)
-                      : a.dstate == 32 ? su_rows_launch<ST, kMethod, 32>(a, grid, st)
-                                       : su_rows_launch<ST, kMethod, 64>(a, grid, st);
+    const bool done = a.dstate == 16    ? su_rows_launch<ST, kMethod, 16>(a, grid, st)
+                      : a.dstate == 32  ? su_rows_launch<ST, kMethod, 32>(a, grid, st)
+                      : a.dstate == 64  ? su_rows_launch<ST, kMethod, 64>(a, grid, st)
+                      : a.dstate == 128 ? su_rows_launch<ST, kMethod, 128>(a, grid, st)
+                                        : su_rows_launch<ST, kMethod, 256>(a, grid, st);
     if (done) return;
   }
   hipLaunchKernelGGL((state_update_kernel<ST, kMethod>), grid, dim3(256), 0, st, a);

@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("method", ["mamba", "zoh", "bilinear", "dirac", "s7", "rglru"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("heads", [False, True])
-@pytest.mark.parametrize("n", [16, 64])
+@pytest.mark.parametrize("n", [16, 64, 128, 256])
 def test_state_update(dev, method, dtype, heads, n):
     g = torch.Generator().manual_seed(3)
     b, h, d, grp = 3, (2 if heads else 1), 96, (2 if heads else 1)
@@ -68,21 +68,24 @@ def test_state_update_batch_indices(dev):
     close("out", out, out_ref, 1e-4, 1e-5)
 
 
-_LAYOUT_DSTATE = {"dstate32": 32, "dstate64": 64, "f32_state_dstate32": 32, "f32_state_dstate64": 64, "dstate24": 24}
+_LAYOUT_DSTATE = {"dstate32": 32, "dstate64": 64, "f32_state_dstate32": 32, "f32_state_dstate64": 64, "dstate24": 24,
+                  "dstate128": 128, "dstate256": 256, "f32_state_dstate128": 128, "f32_state_dstate256": 256}
 
 
 @pytest.mark.parametrize("layout", ["rows16_batch_indices", "strided_state16", "dstate32", "dstate64",
-                                    "f32_state_dstate32", "f32_state_dstate64", "dstate24", "f16_state"])
+                                    "f32_state_dstate32", "f32_state_dstate64", "dstate24", "f16_state",
+                                    "dstate128", "dstate256", "f32_state_dstate128", "f32_state_dstate256"])
 def test_state_update_layouts(dev, layout):
-    """Both kernels of the update: the row-at-once path (d_state 16 / 32 / 64,
-    unit-stride aligned rows: 2 to 16 lanes per row with bf16 / fp16 / fp32
-    states; here also with state_batch_indices) and the entry-by-entry path (a
-    state view with stride 2 along d_state; d_state 24)."""
+    """Both kernels of the update: the row-at-once path (d_state 16 / 32 / 64 /
+    128 / 256, unit-stride aligned rows: 2 to 16 lanes per row, 16 to 64 bytes
+    of state per lane, with bf16 / fp16 / fp32 states; here also with
+    state_batch_indices) and the entry-by-entry path (a state view with stride
+    2 along d_state; d_state 24)."""
     g = torch.Generator().manual_seed(5)
     b, d = 4, 200
     n = _LAYOUT_DSTATE.get(layout, 16)
-    sdt = {"f16_state": torch.float16, "f32_state_dstate32": torch.float32,
-           "f32_state_dstate64": torch.float32}.get(layout, torch.bfloat16)
+    sdt = {"f16_state": torch.float16, "f32_state_dstate32": torch.float32, "f32_state_dstate64": torch.float32,
+           "f32_state_dstate128": torch.float32, "f32_state_dstate256": torch.float32}.get(layout, torch.bfloat16)
     pool = 6 if layout == "rows16_batch_indices" else b
     if layout == "strided_state16":
         big = torch.randn(pool, d, 2 * n, generator=g).to(sdt)
