@@ -432,3 +432,11 @@ def test_state_blocks_without_workspace(dev):
         gk = g[i].squeeze(1) if k in ("B", "C") else g[i]
         close(f"d{k}", gk, rg[k], 1e-4, 1e-4 if k in ("A", "D", "delta_bias") else 1e-5)
     close("dz", g[7], rg["z"], 1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+def test_state_blocks_ragged_shapes(dev, itype):
+    """State blocks on ragged shapes: D = 200 in two groups (50-channel
+    workgroups: partial channel blocks, synchronous tile fetches) and L = 203
+    (a partial last tile; the partial sums' rows are not 16-byte multiples)."""
+    _run(dev, 2, 200, 203, 100, itype=itype, groups=2, seed=68)
