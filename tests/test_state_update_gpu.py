@@ -122,14 +122,14 @@ def test_state_update_layouts(dev, layout):
 
 
 @pytest.mark.parametrize("method", ["mamba", "zoh", "rglru"])
-@pytest.mark.parametrize("n", [16, 24, 64])
+@pytest.mark.parametrize("n", [16, 24, 64, 128, 256])
 @pytest.mark.parametrize("form", ["deltaA", "bare"])
 def test_state_update_deltaA_and_bare(dev, method, n, form):
     """The operand forms the reference callers use besides the full one:
     deltaA given (the event-mode Mamba step, lrnnx/models/ltv/mamba.py:441-455)
     and the bare call without D, z, dt_bias and softplus (the RG-LRU step,
-    lrnnx/models/ltv/rglru.py:315-325), on the row kernel (d_state 16, 64)
-    and the entry-by-entry kernel (d_state 24)."""
+    lrnnx/models/ltv/rglru.py:315-325), on the row kernel (d_state 16, 64,
+    128, 256) and the entry-by-entry kernel (d_state 24)."""
     g = torch.Generator().manual_seed(6 + n)
     b, d = 3, 160
     dtype = torch.bfloat16
