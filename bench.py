@@ -587,6 +587,7 @@ def method_configs(torch, dev):
     weight types at B=8, D=1536, L=2048 (fp32, event-timed medians of 10): the
     general kernels (zoh / bilinear, N=16, variable B/C), dirac on the fast
     kernels and, for comparison, on the general ones (LRNNX_SCAN_GENERIC=1),
+    Mamba's event mode (deltaA; forward alone and fwd+bwd, fast and general),
     the one-state fast path (rglru N=1; the s7 binding call with 256 S7 states)
     and the complex-weight kernels (N=16)."""
     import lrnnx_amd as lx
@@ -617,12 +618,28 @@ def method_configs(torch, dev):
         def fb(m=m):
             lx.selective_scan_fn(u, dl, A, B, C, None, None, None, None, True, discretization=m).backward(dout)
         res[f"{m}_n16_fwd_bwd_ms"] = med(fb)
+    # Mamba's event mode (lrnnx/models/ltv/mamba.py:303-330): delta without softplus or bias,
+    # deltaA the step of A_bar, z and D; the forward on the fast kernels, the backward general
+    dpos = (0.2 * torch.rand(Bt, D, L, device=dev, generator=g) + 1e-3).requires_grad_()
+    dA_ev = (0.5 * torch.rand(Bt, D, L, device=dev, generator=g)).requires_grad_()
+    z_ev, D_ev = rn(Bt, D, L).requires_grad_(), torch.ones(D, device=dev, requires_grad=True)
+
+    def event(bwd):
+        with torch.set_grad_enabled(bwd):
+            y = lx.selective_scan_fn(u, dpos, A, B, C, D_ev, z_ev, None, dA_ev, False, discretization="mamba")
+        if bwd:
+            y.backward(dout)
+
+    res["mamba_event_deltaA_n16_fwd_ms"] = med(lambda: event(False))
+    res["mamba_event_deltaA_n16_fwd_bwd_ms"] = med(lambda: event(True))
     prev = os.environ.get("LRNNX_SCAN_GENERIC")
     os.environ["LRNNX_SCAN_GENERIC"] = "1"
     try:
         res["dirac_n16_generic_fwd_bwd_ms"] = med(
             lambda: lx.selective_scan_fn(u, dl, A, B, C, None, None, None, None, True,
                                          discretization="dirac").backward(dout))
+        res["mamba_event_deltaA_n16_generic_fwd_ms"] = med(lambda: event(False))
+        res["mamba_event_deltaA_n16_generic_fwd_bwd_ms"] = med(lambda: event(True))
     finally:
         if prev is None:
             del os.environ["LRNNX_SCAN_GENERIC"]

@@ -1,9 +1,12 @@
 // Selective scan backward, fast path of the headline case (gfx950).
 //
-// Same coverage as the fast forward (ssf_fwd_eligible): method "mamba" (f32 /
-// bf16 / f16 I/O) and "dirac" (f32 I/O), variable B and C, no deltaA,
-// d_state <= 16, 64 channels per group block, L a multiple of 16,
-// 16-byte aligned rows.
+// The fast forward's coverage (ssf_fwd_eligible) without deltaA: method
+// "mamba" (f32 / bf16 / f16 I/O) and "dirac" (f32 I/O), variable B and C,
+// d_state <= 16, 64 channels per group block, L a multiple of 16, 16-byte
+// aligned rows.  (deltaA would need one more raw tile and fp32 operand tile,
+// LDS this kernel does not have below the 80 KB of two workgroups per CU; a
+// deltaA forward on the fast path writes the checkpoint layout the general
+// backward reads.)
 // Gradients of the reference kernel
 // csrc/selective_scan/selective_scan_backward.cuh:86-845 for this method:
 //   dh_t  = A_bar_{t+1} dh_{t+1} + C_t dy_t      (dy = dout silu(z))

@@ -15,7 +15,7 @@ bool ssf_fwd_bf16(const lrnnx_selective_scan_args& a, hipStream_t st, hipError_t
 // not cover the call.
 bool ssf_ckpt_rebuild_bf16(const lrnnx_selective_scan_args& a, float* ckpt, float* fws, int64_t fws_bytes,
                         const float* x, hipStream_t st, hipError_t* err) {
-  if (!ssf::shape_ok<bf16>(a, ssf::tile_steps<bf16>())) return false;
+  if (!ssf::shape_ok<bf16>(a, ssf::tile_steps<bf16>(), true)) return false;
   lrnnx_selective_scan_args f = a;
   f.ckpt = ckpt;
   f.out.ptr = nullptr;

@@ -24,7 +24,7 @@ int64_t ssf_fwd_workspace_bytes(const lrnnx_selective_scan_args& a) {
 // not cover the call.
 bool ssf_ckpt_rebuild_f32(const lrnnx_selective_scan_args& a, float* ckpt, float* fws, int64_t fws_bytes,
                         const float* x, hipStream_t st, hipError_t* err) {
-  if (!ssf::shape_ok<float>(a, ssf::tile_steps<float>())) return false;
+  if (!ssf::shape_ok<float>(a, ssf::tile_steps<float>(), true)) return false;
   lrnnx_selective_scan_args f = a;
   f.ckpt = ckpt;
   f.out.ptr = nullptr;

@@ -1,8 +1,9 @@
 // Selective scan forward, fast path of the headline case (gfx950).
 //
-// Covers: method "mamba" (f32 / bf16 / f16 I/O) and "dirac" (f32 I/O; the
-// input term B u without delta'), variable B and C of any group count, no
-// deltaA, d_state <= 16, real fp32 A, d_model a multiple
+// Covers: method "mamba" (f32 / bf16 / f16 I/O; with or without deltaA, the
+// step of A_bar in Mamba's event mode) and "dirac" (f32 I/O; the input term
+// B u without delta'), variable B and C of any group count, d_state <= 16,
+// real fp32 A, d_model a multiple
 // of 64 per group, L a multiple of the tile length, 16-byte aligned rows
 // (ssf_fwd_eligible).  Everything else runs the generic kernel of
 // ss_fwd_impl.h.  Semantics are those of the reference kernel
@@ -100,13 +101,17 @@ struct SsfSeg {
 // that a grid too small to give every CU two 64-channel workgroups (at most
 // 256 of them) runs twice as many workgroups, two per CU.  The 32-channel
 // form walks 32-step tiles whatever the element size.
-template <typename IT, bool kSP, bool kZ, bool kOut = true, int kCh = kWave, bool kDi = false>
+// kDA: deltaA given (mamba): A_bar = exp(deltaA A), the chunk carries' sums
+// run over deltaA, and delta' enters the input term only.  Its raw tile takes
+// the LDS of the D u partial, which stays in registers (no faster, no slower).
+template <typename IT, bool kSP, bool kZ, bool kOut = true, int kCh = kWave, bool kDi = false, bool kDA = false>
 __global__ void __launch_bounds__(ssf::kNT)
 ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf::SsfSeg sg) {
   using namespace ssf;
   static_assert(kOut || !kZ, "the checkpoint rebuild reads no z");
   static_assert(kCh == kWave || kCh == kWave / 2, "64 or 32 channels per workgroup");
   static_assert(!kDi || sizeof(IT) == 4, "the dirac method takes fp32 input only");
+  static_assert(!(kDi && kDA), "deltaA on the fast path: mamba only");
   constexpr int kH = kWave / kCh;                                 // lane halves per wave
   constexpr int kS = 16 / kNW / kH;                               // states per lane
   constexpr int kT = kCh == kWave ? tile_steps<IT>() : 32;        // steps per tile
@@ -132,11 +137,13 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   __shared__ __attribute__((aligned(16))) char s_raw_z[kZ ? 2 * kRaw : 16];
   __shared__ __attribute__((aligned(16))) char s_raw_b[kRawS];
   __shared__ __attribute__((aligned(16))) char s_raw_c[kOut ? kRawS : 16];
-  __shared__ __attribute__((aligned(16))) float s_dl[kOp];                  // [g][ch][4] delta'
+  __shared__ __attribute__((aligned(16))) char s_raw_a[kDA ? kRaw : 16];       // deltaA
+  __shared__ __attribute__((aligned(16))) float s_dl[kOp];                  // [g][ch][4] delta' (deltaA: deltaA)
   __shared__ __attribute__((aligned(16))) float s_x[kOp];                   // [g][ch][4] delta' u (dirac: u)
   __shared__ __attribute__((aligned(16))) float s_B[16 * kT];               // [n][t]
   __shared__ __attribute__((aligned(16))) float s_C[kOut ? 16 * kT : 4];
-  __shared__ __attribute__((aligned(16))) float s_Y[kOut ? (kNP + 1) * kOp : 4];  // [partial][g][ch][4]; kNP: D u
+  constexpr int kYSlots = kNP + (kDA ? 0 : 1);   // wave partials (+ D u)
+  __shared__ __attribute__((aligned(16))) float s_Y[kOut ? kYSlots * kOp : 4];  // [partial][g][ch][4]; kNP: D u
   __shared__ __attribute__((aligned(16))) float s_dsum[kNT];                // [ch][kP] chunk sums of delta'
 
   const int tid = threadIdx.x;
@@ -160,6 +167,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   const IT* gC = static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1;
   IT* go = a.out.ptr ? static_cast<IT*>(a.out.ptr) + b * a.out.s0 + (d0 + er) * a.out.s1 + eq * kEt : nullptr;
   IT* goz = kZ ? static_cast<IT*>(a.out_z.ptr) + b * a.out_z.s0 + (d0 + er) * a.out_z.s1 + eq * kEt : nullptr;
+  const IT* gA = kDA ? static_cast<const IT*>(a.deltaA.ptr) + b * a.deltaA.s0 + d0 * a.deltaA.s1 : nullptr;
   const uint32_t su = (uint32_t)a.u.s1, sd = (uint32_t)a.delta.s1, sz = (uint32_t)a.z.s1;
   const uint32_t sBn = (uint32_t)a.B.s2, sCn = (uint32_t)a.C.s2;
   float* ckp = static_cast<float*>(a.ckpt);
@@ -183,6 +191,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   // that starts inside a chunk takes the chunk's earlier sum on one thread)
   float e_dsum = (sg.dsum_pre && eq == 0) ? sg.dsum_pre[(blockIdx.z * a.batch + b) * D + d0 + er] : 0.f;
   float e_seg = 0.f;  // sum of this thread's delta' over the segment (summary pass)
+  float e_du[kDA ? kEt : 1];  // deltaA: this thread's D u of the converted tile
 
   const int64_t n_tiles = L / kT;
   const int64_t tb = (int64_t)blockIdx.z * sg.tiles;                     // this segment's tiles
@@ -198,12 +207,14 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   const uint32_t off_u = dma_lane_offset<IT, kQ>(su, w, lane);
   const uint32_t off_d = dma_lane_offset<IT, kQ>(sd, w, lane);
   const uint32_t off_z = kZ ? dma_lane_offset<IT, kQ>(sz, w, lane) : 0u;
+  const uint32_t off_a = kDA ? dma_lane_offset<IT, kQ>((uint32_t)a.deltaA.s1, w, lane) : 0u;
   const uint32_t off_bc = dma_lane_offset<IT, kQ>(bc_b ? sBn : sCn, bc_i, lane);
   auto fetch = [&](int64_t tile) __attribute__((always_inline)) {
     const int64_t t0 = tile * kT;
     tile_fetch_async_s<kQ>(gu + t0, off_u, kCh, s_raw_u, w, lane);
     tile_fetch_async_s<kQ>(gd + t0, off_d, kCh, s_raw_d, w, lane);
     if constexpr (kZ) tile_fetch_async_s<kQ>(gz + t0, off_z, kCh, s_raw_z + (tile & 1) * kRaw, w, lane);
+    if constexpr (kDA) tile_fetch_async_s<kQ>(gA + t0, off_a, kCh, s_raw_a, w, lane);
     if (bc_b) tile_fetch_async_s<kQ>(gB + t0, off_bc, N, s_raw_b, bc_i, lane);
     else if (kOut && w < 2 * kInS) tile_fetch_async_s<kQ>(gC + t0, off_bc, N, s_raw_c, bc_i, lane);
   };
@@ -220,15 +231,16 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
 
   // raw tile -> fp32 operands; thread tid owns row er, steps eq*kEt .. +kEt
   auto convert = [&]() __attribute__((always_inline)) {
-    float vu[kEt], vd[kEt];
+    float vu[kEt], vd[kEt], va[kEt];
     load_el(s_raw_u, vu);
     load_el(s_raw_d, vd);
+    if constexpr (kDA) load_el(s_raw_a, va);
     float dsum = 0.f;
 #pragma unroll
     for (int i = 0; i < kEt; ++i) {
       const float x = vd[i] + e_bias;
       const float dl = kSP ? softplus20_fast(x) : x;
-      dsum += dl;
+      dsum += kDA ? va[i] : dl;
       vd[i] = dl;
     }
     e_dsum += dsum;
@@ -236,15 +248,22 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
 #pragma unroll
     for (int i = 0; i < kEt; i += 4) {
       const int o = op_off<kSh, kCh>((eq * kEt + i) >> 2, er);
-      *reinterpret_cast<float4*>(s_dl + o) = make_float4(vd[i], vd[i + 1], vd[i + 2], vd[i + 3]);
+      if constexpr (kDA)
+        *reinterpret_cast<float4*>(s_dl + o) = make_float4(va[i], va[i + 1], va[i + 2], va[i + 3]);
+      else
+        *reinterpret_cast<float4*>(s_dl + o) = make_float4(vd[i], vd[i + 1], vd[i + 2], vd[i + 3]);
       if constexpr (kDi)
         *reinterpret_cast<float4*>(s_x + o) = make_float4(vu[i], vu[i + 1], vu[i + 2], vu[i + 3]);
       else
         *reinterpret_cast<float4*>(s_x + o) =
             make_float4(vd[i] * vu[i], vd[i + 1] * vu[i + 1], vd[i + 2] * vu[i + 2], vd[i + 3] * vu[i + 3]);
-      if constexpr (kOut)
+      if constexpr (kOut && kDA) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) e_du[i + m] = e_D * vu[i + m];
+      } else if constexpr (kOut) {
         *reinterpret_cast<float4*>(s_Y + kNP * kOp + o) =
             make_float4(e_D * vu[i], e_D * vu[i + 1], e_D * vu[i + 2], e_D * vu[i + 3]);
+      }
     }
     // B / C rows: threads [0, 16 kQ) convert B, [16 kQ, 32 kQ) C, one 16-byte
     // block each; rows >= N are zero
@@ -267,7 +286,9 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
 #pragma unroll
     for (int i = 0; i < kEt; i += 4) {
       const int o = op_off<kSh, kCh>((eq * kEt + i) >> 2, er);
-      float4 acc = *reinterpret_cast<const float4*>(s_Y + kNP * kOp + o);
+      float4 acc;
+      if constexpr (kDA) acc = make_float4(e_du[i], e_du[i + 1], e_du[i + 2], e_du[i + 3]);
+      else acc = *reinterpret_cast<const float4*>(s_Y + kNP * kOp + o);
 #pragma unroll
       for (int p = 0; p < kNP; ++p) {
         const float4 q = *reinterpret_cast<const float4*>(s_Y + p * kOp + o);
@@ -443,11 +464,14 @@ inline bool fetch_fits(const lrnnx_view& v, bool states, int64_t row_bytes) {
 }
 
 // Shape / option part of the fast-path coverage (both directions).
+// with_dA: the fast kernel may take deltaA (the forward, method mamba).
 template <typename IT>
-inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile) {
+inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile, bool with_dA = false) {
   // "mamba" (B u delta') at every input type, "dirac" (B u) at fp32 input
   const bool di = a.method == LRNNX_DIRAC && sizeof(IT) == 4;
-  if ((a.method != LRNNX_MAMBA && !di) || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C || a.deltaA.ptr) return false;
+  if ((a.method != LRNNX_MAMBA && !di) || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C) return false;
+  if (a.deltaA.ptr && (!with_dA || a.method != LRNNX_MAMBA)) return false;
+  if (a.deltaA.ptr && (!fetch_fits<IT>(a.deltaA, false, 64) || !rows_aligned<IT>(a.deltaA, false))) return false;
   if (a.dstate < 1 || a.dstate > 16 || a.seqlen <= 0 || a.seqlen % tile != 0) return false;
   if (a.n_groups <= 0 || a.dim % a.n_groups != 0 || (a.dim / a.n_groups) % kWave != 0) return false;
   // the checkpoint rows (d_state rows of 64 fp32, D apart) of the backward's fetch
@@ -465,7 +489,7 @@ inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile) {
 // Whether the fast forward covers this call (see the header comment).
 template <typename IT>
 inline bool ssf_fwd_eligible(const lrnnx_selective_scan_args& a) {
-  if (!ssf::shape_ok<IT>(a, ssf::tile_steps<IT>())) return false;
+  if (!ssf::shape_ok<IT>(a, ssf::tile_steps<IT>(), true)) return false;
   if ((a.z.ptr != nullptr) != (a.out_z.ptr != nullptr)) return false;
   return ssf::rows_aligned<IT>(a.out, false) && ssf::rows_aligned<IT>(a.out_z, false);
 }
@@ -512,7 +536,7 @@ inline int64_t split_ws_floats(const lrnnx_selective_scan_args& a, int64_t S) {
 // Depends on shapes and options only (the output pointers need not be set).
 template <typename IT>
 inline int64_t ssf_fwd_ws_bytes(const lrnnx_selective_scan_args& a) {
-  if (!ssf::shape_ok<IT>(a, ssf::tile_steps<IT>())) return 0;
+  if (!ssf::shape_ok<IT>(a, ssf::tile_steps<IT>(), true)) return 0;
   const int64_t steps = ssf::seg_steps(a);
   return steps ? ssf::split_ws_floats(a, ssf::n_segs(a, steps)) * (int64_t)sizeof(float) : 0;
 }
@@ -523,7 +547,7 @@ enum class FwdKind { kOutZ, kOut, kStates };  // with z gate / without / states 
 
 // chans: 64 or 32 for the output kinds (ssf::chans_for); the states-only
 // kind (split summaries, checkpoint rebuild) always runs 64.
-template <typename IT, bool kSP, bool kDi>
+template <typename IT, bool kSP, bool kDi, bool kDA = false>
 inline void ssf_fwd_launch_t(const lrnnx_selective_scan_args& a, int64_t n_ck, const ssf::SsfSeg& sg, unsigned nz,
                              ssf::FwdKind kind, int chans, hipStream_t st) {
   const dim3 grid64((unsigned)(a.dim / kWave), (unsigned)a.batch, nz);
@@ -531,15 +555,15 @@ inline void ssf_fwd_launch_t(const lrnnx_selective_scan_args& a, int64_t n_ck, c
   const dim3 blk(ssf::kNT);
   switch (kind) {
     case ssf::FwdKind::kOutZ:
-      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 32, kDi>), grid32, blk, 0, st, a, n_ck, sg);
-      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 64, kDi>), grid64, blk, 0, st, a, n_ck, sg);
+      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 32, kDi, kDA>), grid32, blk, 0, st, a, n_ck, sg);
+      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 64, kDi, kDA>), grid64, blk, 0, st, a, n_ck, sg);
       break;
     case ssf::FwdKind::kOut:
-      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 32, kDi>), grid32, blk, 0, st, a, n_ck, sg);
-      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 64, kDi>), grid64, blk, 0, st, a, n_ck, sg);
+      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 32, kDi, kDA>), grid32, blk, 0, st, a, n_ck, sg);
+      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 64, kDi, kDA>), grid64, blk, 0, st, a, n_ck, sg);
       break;
     case ssf::FwdKind::kStates:
-      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false, 64, kDi>), grid64, blk, 0, st, a, n_ck, sg);
+      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false, 64, kDi, kDA>), grid64, blk, 0, st, a, n_ck, sg);
       break;
   }
 }
@@ -560,6 +584,11 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
                                                     : ssf::FwdKind::kOut;
   auto launch = [&](const lrnnx_selective_scan_args& x, const ssf::SsfSeg& sg, unsigned nz, ssf::FwdKind k,
                     int chans) {
+    if (x.deltaA.ptr) {   // mamba only (shape_ok)
+      if (x.delta_softplus) ssf_fwd_launch_t<IT, true, false, true>(x, n_ck, sg, nz, k, chans, st);
+      else ssf_fwd_launch_t<IT, false, false, true>(x, n_ck, sg, nz, k, chans, st);
+      return;
+    }
     if constexpr (sizeof(IT) == 4) {   // dirac: fp32 input only (shape_ok)
       if (x.method == LRNNX_DIRAC) {
         if (x.delta_softplus) ssf_fwd_launch_t<IT, true, true>(x, n_ck, sg, nz, k, chans, st);

@@ -440,3 +440,83 @@ def test_state_blocks_ragged_shapes(dev, itype):
     workgroups: partial channel blocks, synchronous tile fetches) and L = 203
     (a partial last tile; the partial sums' rows are not 16-byte multiples)."""
     _run(dev, 2, 200, 203, 100, itype=itype, groups=2, seed=68)
+
+
+# deltaA (Mamba's event mode, lrnnx/models/ltv/mamba.py:303-330: delta without
+# softplus or bias, deltaA the step of A_bar) on the fast forward; the
+# backward runs the general kernels from the fast forward's checkpoints.
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("schedule", ["split", "unsplit64", "unsplit32"])
+def test_deltaA_fast_forward_vs_oracle(dev, monkeypatch, itype, schedule):
+    if schedule != "split":
+        monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", "1")
+        monkeypatch.setenv("LRNNX_SCAN_CHANNELS", schedule[-2:])
+    print(f"deltaA fast forward, {schedule}, {itype}", flush=True)
+    _run(dev, 2, 128, 512, 16, itype=itype, has_bias=False, softplus=False, with_deltaA=True, seed=71)
+
+
+def test_deltaA_fast_forward_softplus_long(dev):
+    # with softplus and bias too; two chunk ends and a ragged last chunk (x carries over deltaA)
+    _run(dev, 1, 64, 4160, 13, itype=torch.bfloat16, with_deltaA=True, seed=72)
+
+
+@pytest.mark.parametrize("save", ["checkpoints", "x"])
+def test_deltaA_binding_fwd_then_bwd(dev, monkeypatch, save):
+    """selective_scan_cuda.fwd -> bwd(x, out) with deltaA: the backward gets
+    the forward's checkpoints, or rebuilds them on the fast states-only
+    forward from the x carries (unsplit grid: one 2048-step chunk per slice)."""
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", "1")
+    prev = ssc.save_mode()
+    ssc.set_save_mode(save)
+    try:
+        Bt, D, L = 1, 64, 4160
+        inp = R.make_selective_inputs(Bt, D, L, 16, seed=73, has_bias=False)
+        inp["delta"] = inp["delta"].abs() * 0.2 + 1e-3
+        g = torch.Generator().manual_seed(74)
+        dA = 0.5 * torch.rand(Bt, D, L, generator=g)
+        dout = torch.randn(Bt, D, L, generator=g)
+        ro, rl, rg = oracle_selective(inp, "mamba", False, dA, True, dout)
+        d = to_dev(inp, dev)
+        u, dl, A, B, C, Dv, z = (d[k] for k in ("u", "delta", "A", "B", "C", "D", "z"))
+        B, C = B.unsqueeze(1).contiguous(), C.unsqueeze(1).contiguous()
+        dA_dev = dA.to(dev)
+        out, x, out_z = ssc.fwd(u, dl, A, B, C, Dv, z, None, dA_dev, False, "mamba")[:3]
+        res = ssc.bwd(u, dl, A, B, C, Dv, z, None, dA_dev, dout.to(dev), x, out, None, False, False, "mamba")
+        torch.cuda.synchronize()
+    finally:
+        ssc.set_save_mode(prev)
+    close("out", out_z, ro, 1e-4, 1e-5)
+    close("last_state", x[:, :, -1, 1::2], rl, 1e-4, 1e-5)
+    # du, ddelta, dA, dB, dC, dD, ddelta_bias (None), ddeltaA, dz
+    for i, k in ((0, "u"), (1, "delta"), (2, "A"), (3, "B"), (4, "C"), (5, "D")):
+        gk = res[i].squeeze(1) if k in ("B", "C") else res[i]
+        close(f"d{k}", gk, rg[k], 1e-4, 1e-4 if k in ("A", "D") else 1e-5)
+    close("ddeltaA", res[7], rg["deltaA"], 1e-4, 1e-5)
+    close("dz", res[8], rg["z"], 1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+def test_deltaA_fast_forward_matches_generic(dev, monkeypatch, itype):
+    """The deltaA forward on the fast and on the general kernels: out, x
+    carries and checkpoints agree (fp32 state; sums in another order)."""
+    from lrnnx_amd import _lib
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    inp = R.make_selective_inputs(2, 128, 512, 16, seed=75, itype=itype, has_bias=False)
+    inp["delta"] = (inp["delta"].float().abs() * 0.2 + 1e-3).to(itype)
+    dA = (0.5 * torch.rand(2, 128, 512, generator=torch.Generator().manual_seed(76))).to(itype)
+    d = to_dev(inp, dev)
+    d["B"], d["C"] = d["B"].unsqueeze(1).contiguous(), d["C"].unsqueeze(1).contiguous()
+    res = []
+    for generic in ("0", "1"):
+        monkeypatch.setenv("LRNNX_SCAN_GENERIC", generic)
+        a = ssc.build_args(d["u"], d["delta"], d["A"], d["B"], d["C"], d["D"], d["z"], None, dA.to(dev), False,
+                           "mamba")
+        res.append(ssc.run_fwd(a, d["u"], d["delta"], d["A"], d["z"], want_ckpt=True))
+        torch.cuda.synchronize()
+    tol = 1e-5 if itype == torch.float32 else 1e-2
+    for name, f_, g_ in zip(("out", "x", "out_z", "ckpt"), res[0], res[1]):
+        t = tol if name in ("out", "out_z") else 1e-5
+        close(f"{name} fast vs general", f_.float(), g_.float().cpu().double(), t, t)
