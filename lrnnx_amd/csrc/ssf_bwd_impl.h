@@ -1,12 +1,11 @@
 // Selective scan backward, fast path of the headline case (gfx950).
 //
-// The fast forward's coverage (ssf_fwd_eligible) without deltaA: method
-// "mamba" (f32 / bf16 / f16 I/O) and "dirac" (f32 I/O), variable B and C,
-// d_state <= 16, 64 channels per group block, L a multiple of 16, 16-byte
-// aligned rows.  (deltaA would need one more raw tile and fp32 operand tile,
-// LDS this kernel does not have below the 80 KB of two workgroups per CU; a
-// deltaA forward on the fast path writes the checkpoint layout the general
-// backward reads.)
+// The fast forward's coverage (ssf_fwd_eligible): method "mamba" (f32 / bf16
+// / f16 I/O) and "dirac" (f32 I/O), variable B and C, d_state <= 16, 64
+// channels per group block, L a multiple of 16, 16-byte aligned rows; deltaA
+// (mamba) without softplus, as Mamba's event mode passes it (with softplus
+// the extra raw tile would take the LDS past the 80 KB of two workgroups per
+// CU; such calls run the general kernels, which read the same checkpoints).
 // Gradients of the reference kernel
 // csrc/selective_scan/selective_scan_backward.cuh:86-845 for this method:
 //   dh_t  = A_bar_{t+1} dh_{t+1} + C_t dy_t      (dy = dout silu(z))
@@ -15,6 +14,8 @@
 //   dA    = sum_t delta' A_bar h_{t-1} dh,  dB_t = sum_d dh delta' u,
 //   dC_t  = sum_d dy h_t,  dD = sum dy u,  ddelta_bias = sum ddelta,
 //   dz    = dout out sigma(z) (1 + z (1 - sigma(z)))      (:218-219)
+// With deltaA, A_bar = exp(deltaA A): the A term goes to ddeltaA instead of
+// ddelta', and dA sums deltaA A_bar h_{t-1} dh.
 // For "dirac" (input term B u) delta' drops out of du and dB, and ddelta'
 // keeps the A term only.
 //
@@ -77,7 +78,11 @@ __device__ __forceinline__ float softplus20_sig(float x, float& sg) {
 // per CU.  The channel reductions lose their cross-half stage (the halves
 // hold different states), and the per-element phases take 2 elements per
 // thread.
-template <typename IT, bool kSP, bool kZ, int kRT, int kCh = kWave, bool kDi = false>
+// kDA: deltaA given (mamba, no softplus).  The operand tile s_x then holds
+// deltaA (the step of A_bar) and the compute phases form delta' u from s_dl
+// and s_u; the raw deltaA tile takes the LDS that sigmoid(delta + bias) has
+// with softplus.
+template <typename IT, bool kSP, bool kZ, int kRT, int kCh = kWave, bool kDi = false, bool kDA = false>
 __global__ void __launch_bounds__(ssf::kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __restrict__ ws, const SSBwdWs wo,
                const float* __restrict__ ckp, const int64_t seg_tiles) {
@@ -87,6 +92,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   static_assert(kRT == kT || kRT == 2 * kT, "a raw fetch covers one or two tiles");
   static_assert(kCh == kWave || kCh == kWave / 2, "64 or 32 channels per workgroup");
   static_assert(!kDi || sizeof(IT) == 4, "the dirac method takes fp32 input only");
+  static_assert(!kDA || (!kSP && !kDi), "deltaA on the fast backward: mamba without softplus");
   constexpr int kH = kWave / kCh;         // lane halves per wave
   constexpr int kS = 4 / kH;              // states per lane
   constexpr int kPair = kRT / kT;         // tiles per raw fetch
@@ -110,10 +116,11 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   __shared__ __attribute__((aligned(16))) char s_raw_o[kZ ? kRaw : 16];
   __shared__ __attribute__((aligned(16))) char s_raw_b[kRawS];
   __shared__ __attribute__((aligned(16))) char s_raw_c[kRawS];
+  __shared__ __attribute__((aligned(16))) char s_raw_a[kDA ? kRaw : 16];  // deltaA
   __shared__ __attribute__((aligned(16))) float s_ck[16 * kCh];        // [n][ch] h at the tile start
   __shared__ __attribute__((aligned(16))) float s_dl[kOp];             // [g][ch][4] delta'
   __shared__ __attribute__((aligned(16))) float s_u[kOp];              // u (epilogue)
-  __shared__ __attribute__((aligned(16))) float s_x[kOp];              // delta' u (compute phases)
+  __shared__ __attribute__((aligned(16))) float s_x[kOp];              // delta' u (compute phases; deltaA: deltaA)
   __shared__ __attribute__((aligned(16))) float s_dy[kOp];             // dout silu(z)
   __shared__ __attribute__((aligned(16))) float s_sg[kSP ? kOp : 4];   // sigmoid(delta + bias)
   __shared__ __attribute__((aligned(16))) float s_B[kT * 16];          // [t][n]
@@ -160,6 +167,8 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   IT* gdu = static_cast<IT*>(a.du.ptr) + b * a.du.s0 + (d0 + er) * a.du.s1 + kEt * eq;
   IT* gddl = static_cast<IT*>(a.ddelta.ptr) + b * a.ddelta.s0 + (d0 + er) * a.ddelta.s1 + kEt * eq;
   IT* gdz = kZ ? static_cast<IT*>(a.dz.ptr) + b * a.dz.s0 + (d0 + er) * a.dz.s1 + kEt * eq : nullptr;
+  const IT* gA = kDA ? static_cast<const IT*>(a.deltaA.ptr) + b * a.deltaA.s0 + d0 * a.deltaA.s1 : nullptr;
+  IT* gddA = kDA ? static_cast<IT*>(a.ddeltaA.ptr) + b * a.ddeltaA.s0 + (d0 + er) * a.ddeltaA.s1 + kEt * eq : nullptr;
   const uint32_t su = (uint32_t)a.u.s1, sd = (uint32_t)a.delta.s1, sdo = (uint32_t)a.dout.s1;
   const uint32_t sz = (uint32_t)a.z.s1, sos = (uint32_t)a.out_saved.s1;
   const uint32_t sBn = (uint32_t)a.B.s2, sCn = (uint32_t)a.C.s2;
@@ -202,6 +211,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   const uint32_t off_do = dma_lane_offset<IT, kQ>(sdo, w, lane);
   const uint32_t off_z = kZ ? dma_lane_offset<IT, kQ>(sz, w, lane) : 0u;
   const uint32_t off_os = kZ ? dma_lane_offset<IT, kQ>(sos, w, lane) : 0u;
+  const uint32_t off_a = kDA ? dma_lane_offset<IT, kQ>((uint32_t)a.deltaA.s1, w, lane) : 0u;
   const uint32_t off_bc = dma_lane_offset<IT, kQ>(w == 2 ? sBn : sCn, 0, lane);
   const int ck_row = n0w + lane / kQck;                       // state row of this lane's checkpoint block
   const bool ck_on = lane < 4 * kQck && ck_row < N;
@@ -216,6 +226,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       tile_fetch_async_s<kQ>(gz + t0, off_z, kCh, s_raw_z, w, lane);
       tile_fetch_async_s<kQ>(gos + t0, off_os, kCh, s_raw_o, w, lane);
     }
+    if constexpr (kDA) tile_fetch_async_s<kQ>(gA + t0, off_a, kCh, s_raw_a, w, lane);
     if (w == 2) tile_fetch_async_s<kQ>(gB + t0, off_bc, N, s_raw_b, 0, lane);
     if (w == 3) tile_fetch_async_s<kQ>(gC + t0, off_bc, N, s_raw_c, 0, lane);
   };
@@ -256,7 +267,13 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     }
     lds_stv<kEt>(&s_dl[eo], vd);
     lds_stv<kEt>(&s_u[eo], vu);
-    lds_stv<kEt>(&s_x[eo], xu);
+    if constexpr (kDA) {
+      float va[kEt];
+      rawn_to_f32<IT, kEt>(s_raw_a + ro, va);
+      lds_stv<kEt>(&s_x[eo], va);
+    } else {
+      lds_stv<kEt>(&s_x[eo], xu);
+    }
     lds_stv<kEt>(&s_dy[eo], dy);
     // read back by this thread only, in the epilogue
     if constexpr (kSP) lds_stv<kEt>(&s_sg[eo], sg);
@@ -295,17 +312,19 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     lds_ldv<kEt>(&s_u[eo], uu);
     lds_ldv<kEt>(&s_dy[eo], dy);
     if constexpr (kSP) lds_ldv<kEt>(&s_sg[eo], sg);
-    float du[kEt], dd[kEt];
+    float du[kEt], dd[kEt], dda[kEt];
 #pragma unroll
     for (int i = 0; i < kEt; ++i) {
       du[i] = kDi ? fmaf(e_D, dy[i], p1[i]) : fmaf(dl[i], p1[i], e_D * dy[i]);
-      const float ddl = kDi ? kLn2 * p2[i] : fmaf(uu[i], p1[i], kLn2 * p2[i]);
+      const float ddl = kDi ? kLn2 * p2[i] : kDA ? uu[i] * p1[i] : fmaf(uu[i], p1[i], kLn2 * p2[i]);
+      dda[i] = kLn2 * p2[i];
       dd[i] = kSP ? ddl * sg[i] : ddl;
       e_dD = fmaf(dy[i], uu[i], e_dD);
       e_dbias += dd[i];
     }
     storen<IT, kEt>(gdu + tile * kT, du);
     storen<IT, kEt>(gddl + tile * kT, dd);
+    if constexpr (kDA) storen<IT, kEt>(gddA + tile * kT, dda);
   };
 
   // ---- prologue: the segment's last tile (segment bounds are multiples of kPair tiles)
@@ -376,6 +395,19 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     auto rs_b0 = [&](float lo, float hi) __attribute__((always_inline)) {
       return rs_pair(lo, hi, lane & 1, std::integral_constant<int, kDppQuadXor1>{});
     };
+    // operands of 4 steps: the step of A_bar (delta', or deltaA) and the input factor x (delta' u)
+    auto step_ops = [&](int og, float (&dt)[4], float (&xx)[4]) __attribute__((always_inline)) {
+      const float4 d4 = *reinterpret_cast<const float4*>(&s_dl[og]);
+      const float4 x4 = *reinterpret_cast<const float4*>(&s_x[og]);
+      if constexpr (kDA) {
+        const float4 u4 = *reinterpret_cast<const float4*>(&s_u[og]);
+        dt[0] = x4.x; dt[1] = x4.y; dt[2] = x4.z; dt[3] = x4.w;
+        xx[0] = d4.x * u4.x; xx[1] = d4.y * u4.y; xx[2] = d4.z * u4.z; xx[3] = d4.w * u4.w;
+      } else {
+        dt[0] = d4.x; dt[1] = d4.y; dt[2] = d4.z; dt[3] = d4.w;
+        xx[0] = x4.x; xx[1] = x4.y; xx[2] = x4.z; xx[3] = x4.w;
+      }
+    };
     // recompute A_bar and h over the tile; dC_t = sum_d dy_t h_t is complete
     // here, so its reduce-scatter runs with it (steps in increasing order)
     float AB[kT][kS], H[kT][kS];
@@ -403,10 +435,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
         // hoisted above this group's arithmetic (that would exceed 256 VGPRs)
         __builtin_amdgcn_sched_barrier(0);
         const int og = op_off<0, kCh>(g, ch);
-        const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[og]);
-        const float4 x4 = *reinterpret_cast<const float4*>(&s_x[og]);
+        float dl[4], xx[4];
+        step_ops(og, dl, xx);
         const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[og]);
-        const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, xx[4] = {x4.x, x4.y, x4.z, x4.w};
         const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -447,11 +478,10 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     for (int g = kG - 1; g >= 0; --g) {
       __builtin_amdgcn_sched_barrier(0);
       const int og = op_off<0, kCh>(g, ch);
-      const float4 dl4 = *reinterpret_cast<const float4*>(&s_dl[og]);
-      const float4 x4 = *reinterpret_cast<const float4*>(&s_x[og]);
+      float dl[4], xx[4];
+      step_ops(og, dl, xx);
       const float4 dy4 = *reinterpret_cast<const float4*>(&s_dy[og]);
-      const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w}, dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
-      const float xx[4] = {x4.x, x4.y, x4.z, x4.w};
+      const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
       float p1v[4], p2v[4];
 #pragma unroll
       for (int i = 3; i >= 0; --i) {
@@ -532,7 +562,7 @@ __device__ __forceinline__ void ld8_f32(const IT* p, float* o) {
   }
 }
 
-template <typename IT, bool kSP, bool kZ>
+template <typename IT, bool kSP, bool kZ, bool kDA>
 __global__ void __launch_bounds__(256)
 ssf_bwd_adj_summary_kernel(const lrnnx_selective_scan_args a, const int64_t seg_steps, const int n_seg, float* ws,
                            const SSBwdWs wo) {
@@ -547,7 +577,9 @@ ssf_bwd_adj_summary_kernel(const lrnnx_selective_scan_args a, const int64_t seg_
   const int64_t t0 = s * seg_steps, t1 = t0 + seg_steps < L ? t0 + seg_steps : L;  // multiples of 8
   const float a2 = on ? static_cast<const float*>(a.A.ptr)[d * a.A.s0 + n * a.A.s1] * kLog2e : 0.f;
   const float bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[d * a.delta_bias.s0] : 0.f;
-  const IT* pd = static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d * a.delta.s1;
+  // the step of A_bar: delta' (or deltaA)
+  const IT* pd = kDA ? static_cast<const IT*>(a.deltaA.ptr) + b * a.deltaA.s0 + d * a.deltaA.s1
+                     : static_cast<const IT*>(a.delta.ptr) + b * a.delta.s0 + d * a.delta.s1;
   const IT* pdo = static_cast<const IT*>(a.dout.ptr) + b * a.dout.s0 + d * a.dout.s1;
   const IT* pz = kZ ? static_cast<const IT*>(a.z.ptr) + b * a.z.s0 + d * a.z.s1 : nullptr;
   const IT* pc = static_cast<const IT*>(a.C.ptr) + b * a.C.s0 + grp * a.C.s1 + (on ? n : 0) * a.C.s2;
@@ -560,8 +592,8 @@ ssf_bwd_adj_summary_kernel(const lrnnx_selective_scan_args a, const int64_t seg_
     ld8_f32<IT>(pc + tb, vc);
 #pragma unroll
     for (int j = 7; j >= 0; --j) {
-      float dl = vd[j] + bias;
-      if constexpr (kSP) dl = ssf::softplus20_fast(dl);
+      float dl = kDA ? vd[j] : vd[j] + bias;
+      if constexpr (kSP && !kDA) dl = ssf::softplus20_fast(dl);
       float dy = vdo[j];
       if constexpr (kZ) dy *= vz[j] * ssf::sigmoidf_fast(vz[j]);
       ssum += dl;
@@ -592,11 +624,19 @@ ssf_bwd_adj_chain_kernel(const lrnnx_selective_scan_args a, const int n_seg, flo
   }
 }
 
+// Shape / option coverage of the fast backward: the forward's, deltaA
+// without softplus only.
+template <typename IT>
+inline bool ssf_bwd_shape_ok(const lrnnx_selective_scan_args& a) {
+  return ssf::shape_ok<IT>(a, ssf::kCk, !a.delta_softplus);
+}
+
 // Whether the fast backward covers this call.
 template <typename IT>
 inline bool ssf_bwd_eligible(const lrnnx_selective_scan_args& a) {
   using ssf::rows_aligned;
-  if (!ssf::shape_ok<IT>(a, ssf::kCk)) return false;
+  if (!ssf_bwd_shape_ok<IT>(a)) return false;
+  if (a.deltaA.ptr && (!a.ddeltaA.ptr || !rows_aligned<IT>(a.ddeltaA, false))) return false;
   if (a.z.ptr && (!a.out_saved.ptr || !a.dz.ptr)) return false;
   return rows_aligned<IT>(a.dout, false) && rows_aligned<IT>(a.out_saved, false) && rows_aligned<IT>(a.du, false) &&
          rows_aligned<IT>(a.ddelta, false) && rows_aligned<IT>(a.dz, false);
@@ -606,7 +646,7 @@ inline bool ssf_bwd_eligible(const lrnnx_selective_scan_args& a) {
 // from shapes and options only, so that the workspace size and the launch agree.
 template <typename IT>
 inline int64_t ssf_bwd_segs(const lrnnx_selective_scan_args& a) {
-  if (!ssf::shape_ok<IT>(a, ssf::kCk)) return 1;
+  if (!ssf_bwd_shape_ok<IT>(a)) return 1;
   const int64_t steps = ssf::seg_steps(a);
   return steps ? ssf::n_segs(a, steps) : 1;
 }
@@ -618,7 +658,7 @@ inline int64_t ssf_bwd_segs(const lrnnx_selective_scan_args& a) {
 // LRNNX_SCAN_CHANNELS forces either where 32 is possible.
 template <typename IT>
 inline int ssf_bwd_chans(const lrnnx_selective_scan_args& a) {
-  if (!ssf::shape_ok<IT>(a, ssf::kCk) || ssf_bwd_segs<IT>(a) > 1) return kWave;
+  if (!ssf_bwd_shape_ok<IT>(a) || ssf_bwd_segs<IT>(a) > 1) return kWave;
   if (sizeof(IT) == 2 && a.seqlen % (2 * ssf::kCk) != 0) return kWave;
   const int o = scan_channels_override();
   if (o) return o;
@@ -637,7 +677,7 @@ inline SSGeom ssf_bwd_geom(const lrnnx_selective_scan_args& a) {
   return g;
 }
 
-template <typename IT, bool kSP, bool kZ, bool kDi>
+template <typename IT, bool kSP, bool kZ, bool kDi, bool kDA = false>
 inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                              const float* ckp, int64_t seg_steps, hipStream_t st) {
   // Two-tile raw fetches for 16-bit I/O when every segment holds an even
@@ -649,7 +689,7 @@ inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g
   const int64_t seg_tiles = S > 1 ? seg_steps / ssf::kCk : a.seqlen / ssf::kCk;
   if (S > 1) {
     const int64_t nsum = (S - 1) * B * D * 16, nch = B * N * D;
-    hipLaunchKernelGGL((ssf_bwd_adj_summary_kernel<IT, kSP, kZ>), dim3((unsigned)((nsum + 255) / 256)), dim3(256), 0,
+    hipLaunchKernelGGL((ssf_bwd_adj_summary_kernel<IT, kSP, kZ, kDA>), dim3((unsigned)((nsum + 255) / 256)), dim3(256), 0,
                        st, a, seg_steps, (int)S, ws, wo);
     hipLaunchKernelGGL(ssf_bwd_adj_chain_kernel<IT>, dim3((unsigned)((nch + 255) / 256)), dim3(256), 0, st, a, (int)S,
                        ws, wo);
@@ -659,22 +699,22 @@ inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g
   if constexpr (kTwo) {
     if (a.seqlen % (2 * ssf::kCk) == 0) {
       if (c32)
-        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave / 2, kDi>), grid, blk, 0, st, a, g.n_ck, ws,
+        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave / 2, kDi, kDA>), grid, blk, 0, st, a, g.n_ck, ws,
                            wo, ckp, seg_tiles);
       else
-        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave, kDi>), grid, blk, 0, st, a, g.n_ck, ws, wo,
+        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave, kDi, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo,
                            ckp, seg_tiles);
       return;
     }
     // (the 32-channel form comes with two-tile fetches only: ssf_bwd_chans)
-    hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave, kDi>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+    hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave, kDi, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
                        seg_tiles);
   } else {
     if (c32)
-      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave / 2, kDi>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave / 2, kDi, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
                          seg_tiles);
     else
-      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave, kDi>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave, kDi, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
                          seg_tiles);
   }
 }
@@ -688,7 +728,10 @@ inline hipError_t ssf_bwd_launch(const lrnnx_selective_scan_args& a, float* ws, 
   const bool z = a.z.ptr != nullptr;
   bool di = false;
   if constexpr (sizeof(IT) == 4) di = a.method == LRNNX_DIRAC;   // dirac: fp32 input only (shape_ok)
-  if (di) {
+  if (a.deltaA.ptr) {   // mamba without softplus (ssf_bwd_shape_ok)
+    if (z) ssf_bwd_launch_t<IT, false, true, false, true>(a, g, ws, wo, ckp, steps, st);
+    else ssf_bwd_launch_t<IT, false, false, false, true>(a, g, ws, wo, ckp, steps, st);
+  } else if (di) {
     if constexpr (sizeof(IT) == 4) {
       if (a.delta_softplus) {
         if (z) ssf_bwd_launch_t<IT, true, true, true>(a, g, ws, wo, ckp, steps, st);

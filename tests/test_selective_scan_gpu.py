@@ -443,15 +443,16 @@ def test_state_blocks_ragged_shapes(dev, itype):
 
 
 # deltaA (Mamba's event mode, lrnnx/models/ltv/mamba.py:303-330: delta without
-# softplus or bias, deltaA the step of A_bar) on the fast forward; the
-# backward runs the general kernels from the fast forward's checkpoints.
+# softplus or bias, deltaA the step of A_bar) on the fast kernels, both
+# directions; with softplus the backward runs the general kernels from the
+# fast forward's checkpoints.
 @pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("schedule", ["split", "unsplit64", "unsplit32"])
-def test_deltaA_fast_forward_vs_oracle(dev, monkeypatch, itype, schedule):
+def test_deltaA_fast_path_vs_oracle(dev, monkeypatch, itype, schedule):
     if schedule != "split":
         monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", "1")
         monkeypatch.setenv("LRNNX_SCAN_CHANNELS", schedule[-2:])
-    print(f"deltaA fast forward, {schedule}, {itype}", flush=True)
+    print(f"deltaA fast path, {schedule}, {itype}", flush=True)
     _run(dev, 2, 128, 512, 16, itype=itype, has_bias=False, softplus=False, with_deltaA=True, seed=71)
 
 
@@ -520,3 +521,32 @@ def test_deltaA_fast_forward_matches_generic(dev, monkeypatch, itype):
     for name, f_, g_ in zip(("out", "x", "out_z", "ckpt"), res[0], res[1]):
         t = tol if name in ("out", "out_z") else 1e-5
         close(f"{name} fast vs general", f_.float(), g_.float().cpu().double(), t, t)
+
+
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("with_z", [True, False])
+def test_deltaA_fast_path_matches_generic(dev, monkeypatch, itype, with_z):
+    """Event-mode fwd + bwd on the fast and on the general kernels: every
+    output and gradient, ddeltaA included (fp32 state; sums in another order)."""
+    inp = R.make_selective_inputs(2, 128, 512, 16, seed=77, itype=itype, has_bias=False, has_z=with_z)
+    inp["delta"] = (inp["delta"].float().abs() * 0.2 + 1e-3).to(itype)
+    g = torch.Generator().manual_seed(78)
+    dA = (0.5 * torch.rand(2, 128, 512, generator=g)).to(itype)
+    dout = torch.randn(2, 128, 512, generator=g).to(itype).to(dev)
+    d = to_dev(inp, dev)
+    res = []
+    for generic in ("0", "1"):
+        monkeypatch.setenv("LRNNX_SCAN_GENERIC", generic)
+        lv = {k: d[k].clone().requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D")}
+        z = d["z"].clone().requires_grad_(True) if with_z else None
+        dA_dev = dA.to(dev).requires_grad_(True)
+        out, last = selective_scan_fn(lv["u"], lv["delta"], lv["A"], lv["B"], lv["C"], lv["D"], z, None, dA_dev,
+                                      False, True, "mamba")
+        out.backward(dout)
+        torch.cuda.synchronize()
+        res.append([out.detach().float(), last.detach()] + [lv[k].grad.float() for k in lv] +
+                   [dA_dev.grad.float()] + ([z.grad.float()] if with_z else []))
+    names = ["out", "last_state", "du", "ddelta", "dA", "dB", "dC", "dD", "ddeltaA"] + (["dz"] if with_z else [])
+    rt = 1e-5 if itype == torch.float32 else 1e-2
+    for n, a_, b_ in zip(names, res[0], res[1]):
+        close(f"{n} fast vs general", a_, b_.cpu().double(), rt, rt)
