@@ -24,10 +24,11 @@
 //               the fp32 operands delta', delta' u, D u and B, C rows.
 // The per-element work of both phases is done by a fixed thread -> (channel,
 // 16-byte block) map, so a thread rewrites its own D u slot right after the
-// epilogue has read it.  The chunk carries x need the sum of delta' over a
-// 2048-step chunk; each thread accumulates the sum of its own block across
-// the tiles of a chunk and the four block sums of a channel are added when
-// the chunk ends.
+// epilogue has read it.  The chunk carries x hold, at each 2048-step chunk
+// end, the product of A_bar since the sequence start (the reference's running
+// prefix, selective_scan.cuh:316-333), exp(A sum delta'); each thread
+// accumulates the sum of its own block over the tiles and the block sums of a
+// channel are added when a chunk ends.
 #pragma once
 #include <type_traits>
 
@@ -75,7 +76,7 @@ __device__ __forceinline__ float sigmoidf_fast(float z) {
 // Summary pass: h_end != nullptr; the segment runs from h = 0 and writes its
 // final state and its sum of delta' (no other outputs).  Main pass: h_init !=
 // nullptr; the segment starts from h_init and from dsum_pre, the sum of delta'
-// from its 2048-step chunk's start to the segment start (for the x carries).
+// from the sequence start to the segment start (for the x carries).
 // Buffers: states [seg][b][n][d], sums [seg][b][d].  Checkpoint rebuild
 // (kOut = false, below): x_seed != nullptr; segments are the 2048-step chunks
 // of the x carries and segment s > 0 starts from the state x holds at the end
@@ -187,8 +188,8 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   // per-thread constants of the per-element phases (channel d0 + er)
   const float e_bias = a.delta_bias.ptr ? static_cast<const float*>(a.delta_bias.ptr)[(d0 + er) * a.delta_bias.s0] : 0.f;
   const float e_D = a.D.ptr ? static_cast<const float*>(a.D.ptr)[(d0 + er) * a.D.s0] : 0.f;
-  // sum of this thread's delta' over the current 2048-step chunk (a segment
-  // that starts inside a chunk takes the chunk's earlier sum on one thread)
+  // sum of this thread's delta' since the sequence start (a segment takes the
+  // sum before its start on one thread of each channel)
   float e_dsum = (sg.dsum_pre && eq == 0) ? sg.dsum_pre[(blockIdx.z * a.batch + b) * D + d0 + er] : 0.f;
   float e_seg = 0.f;  // sum of this thread's delta' over the segment (summary pass)
   float e_du[kDA ? kEt : 1];  // deltaA: this thread's D u of the converted tile
@@ -399,7 +400,6 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
     if constexpr (kOut) epilogue(tile);
     if (chunk_end(tile)) {
       s_dsum[tid] = e_dsum;
-      e_dsum = 0.f;
     }
     if (tile + 1 < te) convert();
     __syncthreads();
@@ -419,10 +419,10 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
 
 // Chains the segments' carries, in segment order, per (b, n, d):
 // h_init[0] = 0, h_init[s + 1] = exp(A dsum_seg[s]) h_init[s] + h_end[s];
-// and per (b, d) the sum of delta' from each segment's chunk start.
+// and per (b, d) the sum of delta' before each segment's start.
 template <typename IT>  // one instantiation per unit that launches it
 __global__ void __launch_bounds__(256)
-ssf_seg_chain_kernel(const lrnnx_selective_scan_args a, const ssf::SsfSeg sg, const int n_seg, const int seg_steps,
+ssf_seg_chain_kernel(const lrnnx_selective_scan_args a, const ssf::SsfSeg sg, const int n_seg,
                      float* __restrict__ h_init, float* __restrict__ dsum_pre) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (b, n, d)
   const int64_t B = a.batch, D = a.dim, N = a.dstate;
@@ -433,8 +433,6 @@ ssf_seg_chain_kernel(const lrnnx_selective_scan_args a, const ssf::SsfSeg sg, co
   for (int s = 0; s < n_seg; ++s) {
     const int64_t o = ((s * B + b) * N + n) * D + d;
     h_init[o] = carry;
-    const int64_t t_start = (int64_t)s * seg_steps;
-    if (t_start % kXChunk == 0) pre = 0.f;
     if (n == 0) dsum_pre[(s * B + b) * D + d] = pre;
     if (s + 1 < n_seg) {
       const float ds = sg.dsum_seg[(s * B + b) * D + d];
@@ -635,7 +633,7 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
   const ssf::SsfSeg chain{tiles, nullptr, nullptr, h_end, dsum_seg, nullptr};
   const int64_t nt = a.batch * a.dstate * a.dim;
   hipLaunchKernelGGL(ssf_seg_chain_kernel<IT>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st, a, chain, (int)S,
-                     (int)steps, h_init, dsum_pre);
+                     h_init, dsum_pre);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch(a, ssf::SsfSeg{tiles, h_init, dsum_pre, nullptr, nullptr, nullptr}, (unsigned)S, kind, kWave);

@@ -550,3 +550,34 @@ def test_deltaA_fast_path_matches_generic(dev, monkeypatch, itype, with_z):
     rt = 1e-5 if itype == torch.float32 else 1e-2
     for n, a_, b_ in zip(names, res[0], res[1]):
         close(f"{n} fast vs general", a_, b_.cpu().double(), rt, rt)
+
+
+@pytest.mark.parametrize("path", ["fast_split", "fast_unsplit64", "fast_unsplit32", "general", "state_blocks"])
+@pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
+def test_x_carries_vs_oracle(dev, monkeypatch, path, itype):
+    """Both halves of every chunk carry of ``selective_scan_cuda.fwd``'s x over
+    three 2048-step chunks: the product of A_bar since the sequence start (the
+    reference's running prefix, selective_scan.cuh:316-333) and the state,
+    against oracle.selective_scan_fwd_ref."""
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    N = 80 if path == "state_blocks" else 16
+    if path.startswith("fast_unsplit"):
+        monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", "1")
+        monkeypatch.setenv("LRNNX_SCAN_CHANNELS", path[-2:])
+    if path == "general":
+        monkeypatch.setenv("LRNNX_SCAN_GENERIC", "1")
+    Bt, D, L = 1, 64, 4160
+    inp = R.make_selective_inputs(Bt, D, L, N, seed=79, itype=itype)
+    inp["delta"] = (inp["delta"].float() * 0.1).to(itype)   # keep the products above underflow for a while
+    ro, rx, roz = R.selective_scan_fwd_ref(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                                           inp["delta_bias"], None, True, compute_dtype=torch.float64)
+    d = to_dev(inp, dev)
+    B, C = d["B"].unsqueeze(1).contiguous(), d["C"].unsqueeze(1).contiguous()
+    out, x = ssc.fwd(d["u"], d["delta"], d["A"], B, C, d["D"], d["z"], d["delta_bias"], None, True, "mamba")[:2]
+    torch.cuda.synchronize()
+    assert x.shape == rx.shape
+    # a product over up to 4160 steps (an exp of an fp32 sum of as many delta') carries up to
+    # ~4160 * 2^-24 relative rounding, as the reference's own fp32 running product does
+    close(f"x products ({path})", x[..., 0::2], rx[..., 0::2], 2e-3, 1e-6)
+    close(f"x states ({path})", x[..., 1::2], rx[..., 1::2], 1e-4, 1e-5)
