@@ -73,3 +73,25 @@ def test_complex_groups_deltaA_options(dev):
     _run(dev, 2, 128, 48, 4, groups=2)
     _run(dev, 2, 64, 48, 4, with_deltaA=True)
     _run(dev, 1, 64, 48, 4, has_z=False, has_D=False, has_bias=False, softplus=False)
+
+
+@pytest.mark.parametrize("method", ["mamba", "zoh", "bilinear"])
+def test_complex_x_carries_vs_oracle(dev, method):
+    """Both halves of the complex chunk carries of ``selective_scan_cuda.fwd``
+    over three 2048-step chunks: the product of A_bar since the sequence start
+    (the reference's running prefix, selective_scan.cuh:316-333) and the
+    state, against oracle.selective_scan_fwd_ref."""
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    inp = R.make_selective_inputs(1, 64, 4200, 4, seed=81, complex_A=True)
+    inp["delta"] = inp["delta"] * 0.1   # keep the products above underflow for a while
+    ro, rx, roz = R.selective_scan_fwd_ref(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                                           inp["delta_bias"], None, True, method, compute_dtype=torch.float64)
+    d = to_dev(inp, dev)
+    B, C = d["B"].unsqueeze(1).contiguous(), d["C"].unsqueeze(1).contiguous()
+    out, x = ssc.fwd(d["u"], d["delta"], d["A"], B, C, d["D"], d["z"], d["delta_bias"], None, True, method)[:2]
+    torch.cuda.synchronize()
+    assert x.shape == rx.shape and x.is_complex()
+    # products over up to 4200 steps carry up to ~4200 * 2^-24 relative rounding (see the real-weight test)
+    close(f"x products ({method})", x[..., 0::2], rx[..., 0::2], 2e-3, 1e-6)
+    close(f"x states ({method})", x[..., 1::2], rx[..., 1::2], 1e-4, 1e-5)
