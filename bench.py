@@ -585,7 +585,8 @@ def dstate_sweep(torch, dev, ss, L_):
 def method_configs(torch, dev):
     """fwd+bwd through the autograd wrappers for the other discretisations and
     weight types at B=8, D=1536, L=2048 (fp32, event-timed medians of 10): the
-    general kernels (zoh / bilinear, N=16, variable B/C), dirac on the fast
+    zoh / bilinear (N=16, variable B/C; the forward on the fast kernels, also
+    alone and, for comparison, on the general ones), dirac on the fast
     kernels and, for comparison, on the general ones (LRNNX_SCAN_GENERIC=1),
     Mamba's event mode (deltaA; forward alone and fwd+bwd, fast and general),
     the one-state fast path (rglru N=1; the s7 binding call with 256 S7 states)
@@ -617,6 +618,11 @@ def method_configs(torch, dev):
     for m in ("zoh", "bilinear", "dirac"):
         def fb(m=m):
             lx.selective_scan_fn(u, dl, A, B, C, None, None, None, None, True, discretization=m).backward(dout)
+
+        def fo(m=m):
+            with torch.no_grad():
+                lx.selective_scan_fn(u, dl, A, B, C, None, None, None, None, True, discretization=m)
+        res[f"{m}_n16_fwd_ms"] = med(fo)
         res[f"{m}_n16_fwd_bwd_ms"] = med(fb)
     # Mamba's event mode (lrnnx/models/ltv/mamba.py:303-330): delta without softplus or bias,
     # deltaA the step of A_bar, z and D; the forward on the fast kernels, the backward general
@@ -638,6 +644,11 @@ def method_configs(torch, dev):
         res["dirac_n16_generic_fwd_bwd_ms"] = med(
             lambda: lx.selective_scan_fn(u, dl, A, B, C, None, None, None, None, True,
                                          discretization="dirac").backward(dout))
+        for m in ("zoh", "bilinear"):
+            def fo(m=m):
+                with torch.no_grad():
+                    lx.selective_scan_fn(u, dl, A, B, C, None, None, None, None, True, discretization=m)
+            res[f"{m}_n16_generic_fwd_ms"] = med(fo)
         res["mamba_event_deltaA_n16_generic_fwd_ms"] = med(lambda: event(False))
         res["mamba_event_deltaA_n16_generic_fwd_bwd_ms"] = med(lambda: event(True))
     finally:

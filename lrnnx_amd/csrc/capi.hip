@@ -112,9 +112,11 @@ const char* method_name(int m) {
 }
 
 
-// Methods with a fast path: "mamba" at every input type, "dirac" (whose
-// input is fp32).
-bool has_fast_path(int method) { return method == LRNNX_MAMBA || method == LRNNX_DIRAC; }
+// Methods with a fast forward: "mamba" at every input type; "dirac", "zoh"
+// and "bilinear", whose input is fp32 (the fast backward: mamba and dirac).
+bool has_fast_path(int method) {
+  return method == LRNNX_MAMBA || method == LRNNX_DIRAC || method == LRNNX_ZOH || method == LRNNX_BILINEAR;
+}
 
 // Forward workspace of the fast path's split of L (0: the call does not split).
 int64_t fwd_split_ws_bytes(const lrnnx_selective_scan_args& a) {
@@ -156,11 +158,12 @@ hipError_t bwd_mamba(const lrnnx_selective_scan_args& a, float* ws, const float*
   }
 }
 
-// Forward / backward of the other real methods (fp32 input): the fast path
-// for "dirac" when it covers the call, else the generic kernels.
+// Forward / backward of the other real methods (fp32 input): the fast
+// forward for "dirac", "zoh" and "bilinear", the fast backward for "dirac",
+// when they cover the call; else the generic kernels.
 hipError_t fwd_other(const lrnnx_selective_scan_args& a, hipStream_t st) {
   hipError_t e = hipSuccess;
-  if (a.method == LRNNX_DIRAC && fast_paths_enabled() && ssf_fwd_f32(a, st, &e)) return e;
+  if (has_fast_path(a.method) && fast_paths_enabled() && ssf_fwd_f32(a, st, &e)) return e;
   return ss_fwd_other_f32(a, st);
 }
 hipError_t bwd_other(const lrnnx_selective_scan_args& a, float* ws, const float* ckp, hipStream_t st) {
@@ -309,8 +312,8 @@ int lrnnx_selective_scan_bwd(const lrnnx_selective_scan_args* a, void* stream) {
                                              "selective_scan_bwd (complex)");
   const float* ckp = static_cast<const float*>(a->ckpt);
   if (!ckp) {
-    // rebuild the fine checkpoints into the workspace.  The fast path (mamba,
-    // dirac) has a states-only forward: split like the forward on small grids, or
+    // rebuild the fine checkpoints into the workspace.  The fast forward
+    // (has_fast_path) has a states-only form: split like the forward on small grids, or
     // with the caller's x carries (the reference's seeds,
     // selective_scan_backward.cuh:330) one 2048-step chunk per grid slice.
     char* wsb = reinterpret_cast<char*>(a->workspace);

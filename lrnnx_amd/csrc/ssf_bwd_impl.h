@@ -628,7 +628,7 @@ ssf_bwd_adj_chain_kernel(const lrnnx_selective_scan_args a, const int n_seg, flo
 // without softplus only.
 template <typename IT>
 inline bool ssf_bwd_shape_ok(const lrnnx_selective_scan_args& a) {
-  return ssf::shape_ok<IT>(a, ssf::kCk, !a.delta_softplus);
+  return ssf::shape_ok<IT>(a, ssf::kCk, false, !a.delta_softplus);
 }
 
 // Whether the fast backward covers this call.

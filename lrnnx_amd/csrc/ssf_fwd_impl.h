@@ -1,9 +1,11 @@
 // Selective scan forward, fast path of the headline case (gfx950).
 //
 // Covers: method "mamba" (f32 / bf16 / f16 I/O; with or without deltaA, the
-// step of A_bar in Mamba's event mode) and "dirac" (f32 I/O; the input term
-// B u without delta'), variable B and C of any group count, d_state <= 16,
-// real fp32 A, d_model a multiple
+// step of A_bar in Mamba's event mode), and at f32 I/O "dirac" (input term
+// B u), "zoh" (A_bar = exp(delta' A), input factor expm1(delta' A) / A) and
+// "bilinear" (A_bar = (1 + delta' A / 2) / (1 - delta' A / 2), input factor
+// delta' / (1 - delta' A / 2)), variable B and C of any group count,
+// d_state <= 16, real fp32 A, d_model a multiple
 // of 64 per group, L a multiple of the tile length, 16-byte aligned rows
 // (ssf_fwd_eligible).  Everything else runs the generic kernel of
 // ss_fwd_impl.h.  Semantics are those of the reference kernel
@@ -105,14 +107,18 @@ struct SsfSeg {
 // kDA: deltaA given (mamba): A_bar = exp(deltaA A), the chunk carries' sums
 // run over deltaA, and delta' enters the input term only.  Its raw tile takes
 // the LDS of the D u partial, which stays in registers (no faster, no slower).
-template <typename IT, bool kSP, bool kZ, bool kOut = true, int kCh = kWave, bool kDi = false, bool kDA = false>
+// kM: the method (LRNNX_MAMBA, DIRAC, ZOH or BILINEAR), compile-time.
+template <typename IT, bool kSP, bool kZ, bool kOut = true, int kCh = kWave, int kM = LRNNX_MAMBA, bool kDA = false>
 __global__ void __launch_bounds__(ssf::kNT)
 ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf::SsfSeg sg) {
   using namespace ssf;
   static_assert(kOut || !kZ, "the checkpoint rebuild reads no z");
   static_assert(kCh == kWave || kCh == kWave / 2, "64 or 32 channels per workgroup");
-  static_assert(!kDi || sizeof(IT) == 4, "the dirac method takes fp32 input only");
-  static_assert(!(kDi && kDA), "deltaA on the fast path: mamba only");
+  static_assert(kM == LRNNX_MAMBA || kM == LRNNX_DIRAC || kM == LRNNX_ZOH || kM == LRNNX_BILINEAR, "method");
+  static_assert(kM == LRNNX_MAMBA || sizeof(IT) == 4, "methods other than mamba take fp32 input only");
+  static_assert(kM == LRNNX_MAMBA || !kDA, "deltaA on the fast path: mamba only");
+  constexpr bool kUx = kM != LRNNX_MAMBA;        // the operand x is u (the input factor is per state)
+  constexpr bool kProd = kM == LRNNX_BILINEAR;   // chunk carries from a running product of A_bar
   constexpr int kH = kWave / kCh;                                 // lane halves per wave
   constexpr int kS = 16 / kNW / kH;                               // states per lane
   constexpr int kT = kCh == kWave ? tile_steps<IT>() : 32;        // steps per tile
@@ -140,7 +146,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
   __shared__ __attribute__((aligned(16))) char s_raw_c[kOut ? kRawS : 16];
   __shared__ __attribute__((aligned(16))) char s_raw_a[kDA ? kRaw : 16];       // deltaA
   __shared__ __attribute__((aligned(16))) float s_dl[kOp];                  // [g][ch][4] delta' (deltaA: deltaA)
-  __shared__ __attribute__((aligned(16))) float s_x[kOp];                   // [g][ch][4] delta' u (dirac: u)
+  __shared__ __attribute__((aligned(16))) float s_x[kOp];                   // [g][ch][4] delta' u (other methods: u)
   __shared__ __attribute__((aligned(16))) float s_B[16 * kT];               // [n][t]
   __shared__ __attribute__((aligned(16))) float s_C[kOut ? 16 * kT : 4];
   constexpr int kYSlots = kNP + (kDA ? 0 : 1);   // wave partials (+ D u)
@@ -176,11 +182,15 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
 
   // per-lane constants of the recurrence (channel d0 + ch, states n0 .. n0 + kS - 1)
   float a2[kS], h[kS];
+  float Ar[kM == LRNNX_ZOH || kProd ? kS : 1], iA[kM == LRNNX_ZOH ? kS : 1], pA[kProd ? kS : 1];
 #pragma unroll
   for (int k = 0; k < kS; ++k) {
     const int n = n0 + k;
     const float Av = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + ch) * a.A.s0 + n * a.A.s1] : -1.f;
     a2[k] = Av * kLog2e;
+    if constexpr (kM == LRNNX_ZOH || kProd) Ar[k] = Av;
+    if constexpr (kM == LRNNX_ZOH) iA[k] = 1.f / Av;
+    if constexpr (kProd) pA[k] = 1.f;   // product of A_bar since the sequence start
     h[k] = (sg.h_init && n < N) ? sg.h_init[((blockIdx.z * a.batch + b) * N + n) * D + d0 + ch] : 0.f;
     if (!kOut && sg.x_seed && blockIdx.z > 0 && n < N)   // the state at the end of chunk z - 1
       h[k] = sg.x_seed[((b * D + d0 + ch) * ((L + kXChunk - 1) / kXChunk) + blockIdx.z - 1) * 2 * N + 2 * n + 1];
@@ -253,7 +263,7 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
         *reinterpret_cast<float4*>(s_dl + o) = make_float4(va[i], va[i + 1], va[i + 2], va[i + 3]);
       else
         *reinterpret_cast<float4*>(s_dl + o) = make_float4(vd[i], vd[i + 1], vd[i + 2], vd[i + 3]);
-      if constexpr (kDi)
+      if constexpr (kUx)
         *reinterpret_cast<float4*>(s_x + o) = make_float4(vu[i], vu[i + 1], vu[i + 2], vu[i + 3]);
       else
         *reinterpret_cast<float4*>(s_x + o) =
@@ -308,7 +318,8 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
     }
   };
 
-  // chunk carry after the last step of `tile`: (exp(A sum delta'), h) per state
+  // chunk carry after the last step of `tile`: (exp(A sum delta'), h) per
+  // state; bilinear: (the running product of A_bar, h)
   auto store_x = [&](int64_t tile) __attribute__((always_inline)) {
     float S = 0.f;
 #pragma unroll
@@ -321,7 +332,8 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
 #pragma unroll
     for (int k = 0; k < kS; ++k) {
       if (n0 + k < N) {
-        xr[2 * (n0 + k)] = __builtin_amdgcn_exp2f(a2[k] * S);
+        if constexpr (kProd) xr[2 * (n0 + k)] = pA[k];
+        else xr[2 * (n0 + k)] = __builtin_amdgcn_exp2f(a2[k] * S);
         xr[2 * (n0 + k) + 1] = h[k];
       }
     }
@@ -372,8 +384,18 @@ ssf_fwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, const ssf:
         float acc = 0.f;
 #pragma unroll
         for (int k = 0; k < kS; ++k) {
-          const float ab = __builtin_amdgcn_exp2f(dlv[i] * a2[k]);
-          h[k] = fmaf(ab, h[k], xv[i] * (&b4[k].x)[i]);
+          float ab, xk = xv[i];   // A_bar and the input factor times u
+          if constexpr (kM == LRNNX_BILINEAR) {
+            const float v = 0.5f * dlv[i] * Ar[k];
+            const float r = __builtin_amdgcn_rcpf(1.f - v);
+            ab = (1.f + v) * r;
+            xk = dlv[i] * r * xv[i];
+            pA[k] *= ab;
+          } else {
+            ab = __builtin_amdgcn_exp2f(dlv[i] * a2[k]);
+            if constexpr (kM == LRNNX_ZOH) xk = expm1_from(dlv[i] * Ar[k], ab) * iA[k] * xv[i];
+          }
+          h[k] = fmaf(ab, h[k], xk * (&b4[k].x)[i]);
           if constexpr (kOut) acc = fmaf((&c4[k].x)[i], h[k], acc);
         }
         y[i] = acc;
@@ -462,13 +484,17 @@ inline bool fetch_fits(const lrnnx_view& v, bool states, int64_t row_bytes) {
 }
 
 // Shape / option part of the fast-path coverage (both directions).
-// with_dA: the fast kernel may take deltaA (the forward, method mamba).
+// fwd: the coverage of the forward (deltaA with mamba; zoh and bilinear),
+// else of the backward (ssf_bwd_shape_ok adds deltaA without softplus).
 template <typename IT>
-inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile, bool with_dA = false) {
-  // "mamba" (B u delta') at every input type, "dirac" (B u) at fp32 input
-  const bool di = a.method == LRNNX_DIRAC && sizeof(IT) == 4;
-  if ((a.method != LRNNX_MAMBA && !di) || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C) return false;
-  if (a.deltaA.ptr && (!with_dA || a.method != LRNNX_MAMBA)) return false;
+inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile, bool fwd = false, bool bwd_dA = false) {
+  // "mamba" at every input type; "dirac" (both directions), "zoh" and
+  // "bilinear" (forward) at fp32 input
+  const bool f32 = sizeof(IT) == 4;
+  const bool m_ok = a.method == LRNNX_MAMBA || (f32 && a.method == LRNNX_DIRAC) ||
+                    (f32 && fwd && (a.method == LRNNX_ZOH || a.method == LRNNX_BILINEAR));
+  if (!m_ok || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C) return false;
+  if (a.deltaA.ptr && (!(fwd || bwd_dA) || a.method != LRNNX_MAMBA)) return false;
   if (a.deltaA.ptr && (!fetch_fits<IT>(a.deltaA, false, 64) || !rows_aligned<IT>(a.deltaA, false))) return false;
   if (a.dstate < 1 || a.dstate > 16 || a.seqlen <= 0 || a.seqlen % tile != 0) return false;
   if (a.n_groups <= 0 || a.dim % a.n_groups != 0 || (a.dim / a.n_groups) % kWave != 0) return false;
@@ -487,7 +513,7 @@ inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile, bool with
 // Whether the fast forward covers this call (see the header comment).
 template <typename IT>
 inline bool ssf_fwd_eligible(const lrnnx_selective_scan_args& a) {
-  if (!ssf::shape_ok<IT>(a, ssf::tile_steps<IT>(), true)) return false;
+  if (!ssf::shape_ok<IT>(a, ssf::tile_steps<IT>(), true)) return false;   // (forward coverage)
   if ((a.z.ptr != nullptr) != (a.out_z.ptr != nullptr)) return false;
   return ssf::rows_aligned<IT>(a.out, false) && ssf::rows_aligned<IT>(a.out_z, false);
 }
@@ -507,7 +533,8 @@ namespace ssf {
 // segment boundary and are multiples of every tile length.
 inline int64_t seg_steps(const lrnnx_selective_scan_args& a) {
   const int64_t wgs = (a.dim / kWave) * a.batch;
-  if (wgs > 64 || !l_split_enabled()) return 0;
+  // (the carry chain is exp(A sum delta') h: not bilinear's A_bar)
+  if (wgs > 64 || !l_split_enabled() || a.method == LRNNX_BILINEAR) return 0;
   int64_t steps = 128;
   while (steps < a.seqlen && wgs * ((a.seqlen + steps - 1) / steps) > 512) steps *= 2;
   return steps < a.seqlen ? steps : 0;
@@ -545,7 +572,7 @@ enum class FwdKind { kOutZ, kOut, kStates };  // with z gate / without / states 
 
 // chans: 64 or 32 for the output kinds (ssf::chans_for); the states-only
 // kind (split summaries, checkpoint rebuild) always runs 64.
-template <typename IT, bool kSP, bool kDi, bool kDA = false>
+template <typename IT, bool kSP, int kM, bool kDA = false>
 inline void ssf_fwd_launch_t(const lrnnx_selective_scan_args& a, int64_t n_ck, const ssf::SsfSeg& sg, unsigned nz,
                              ssf::FwdKind kind, int chans, hipStream_t st) {
   const dim3 grid64((unsigned)(a.dim / kWave), (unsigned)a.batch, nz);
@@ -553,15 +580,15 @@ inline void ssf_fwd_launch_t(const lrnnx_selective_scan_args& a, int64_t n_ck, c
   const dim3 blk(ssf::kNT);
   switch (kind) {
     case ssf::FwdKind::kOutZ:
-      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 32, kDi, kDA>), grid32, blk, 0, st, a, n_ck, sg);
-      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 64, kDi, kDA>), grid64, blk, 0, st, a, n_ck, sg);
+      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 32, kM, kDA>), grid32, blk, 0, st, a, n_ck, sg);
+      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, true, true, 64, kM, kDA>), grid64, blk, 0, st, a, n_ck, sg);
       break;
     case ssf::FwdKind::kOut:
-      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 32, kDi, kDA>), grid32, blk, 0, st, a, n_ck, sg);
-      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 64, kDi, kDA>), grid64, blk, 0, st, a, n_ck, sg);
+      if (chans == 32) hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 32, kM, kDA>), grid32, blk, 0, st, a, n_ck, sg);
+      else hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, true, 64, kM, kDA>), grid64, blk, 0, st, a, n_ck, sg);
       break;
     case ssf::FwdKind::kStates:
-      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false, 64, kDi, kDA>), grid64, blk, 0, st, a, n_ck, sg);
+      hipLaunchKernelGGL((ssf_fwd_kernel<IT, kSP, false, false, 64, kM, kDA>), grid64, blk, 0, st, a, n_ck, sg);
       break;
   }
 }
@@ -583,19 +610,24 @@ inline hipError_t ssf_fwd_launch(const lrnnx_selective_scan_args& a, int64_t n_c
   auto launch = [&](const lrnnx_selective_scan_args& x, const ssf::SsfSeg& sg, unsigned nz, ssf::FwdKind k,
                     int chans) {
     if (x.deltaA.ptr) {   // mamba only (shape_ok)
-      if (x.delta_softplus) ssf_fwd_launch_t<IT, true, false, true>(x, n_ck, sg, nz, k, chans, st);
-      else ssf_fwd_launch_t<IT, false, false, true>(x, n_ck, sg, nz, k, chans, st);
+      if (x.delta_softplus) ssf_fwd_launch_t<IT, true, LRNNX_MAMBA, true>(x, n_ck, sg, nz, k, chans, st);
+      else ssf_fwd_launch_t<IT, false, LRNNX_MAMBA, true>(x, n_ck, sg, nz, k, chans, st);
       return;
     }
-    if constexpr (sizeof(IT) == 4) {   // dirac: fp32 input only (shape_ok)
-      if (x.method == LRNNX_DIRAC) {
-        if (x.delta_softplus) ssf_fwd_launch_t<IT, true, true>(x, n_ck, sg, nz, k, chans, st);
-        else ssf_fwd_launch_t<IT, false, true>(x, n_ck, sg, nz, k, chans, st);
-        return;
+    auto by_sp = [&](auto m) __attribute__((always_inline)) {
+      constexpr int kM = decltype(m)::value;
+      if (x.delta_softplus) ssf_fwd_launch_t<IT, true, kM>(x, n_ck, sg, nz, k, chans, st);
+      else ssf_fwd_launch_t<IT, false, kM>(x, n_ck, sg, nz, k, chans, st);
+    };
+    if constexpr (sizeof(IT) == 4) {   // the other methods: fp32 input only (shape_ok)
+      switch (x.method) {
+        case LRNNX_DIRAC: by_sp(std::integral_constant<int, LRNNX_DIRAC>{}); return;
+        case LRNNX_ZOH: by_sp(std::integral_constant<int, LRNNX_ZOH>{}); return;
+        case LRNNX_BILINEAR: by_sp(std::integral_constant<int, LRNNX_BILINEAR>{}); return;
+        default: break;
       }
     }
-    if (x.delta_softplus) ssf_fwd_launch_t<IT, true, false>(x, n_ck, sg, nz, k, chans, st);
-    else ssf_fwd_launch_t<IT, false, false>(x, n_ck, sg, nz, k, chans, st);
+    by_sp(std::integral_constant<int, LRNNX_MAMBA>{});
   };
   const int64_t steps = ssf::seg_steps(a);
   const int64_t need = ssf_fwd_ws_bytes<IT>(a);

@@ -581,3 +581,57 @@ def test_x_carries_vs_oracle(dev, monkeypatch, path, itype):
     # ~4160 * 2^-24 relative rounding, as the reference's own fp32 running product does
     close(f"x products ({path})", x[..., 0::2], rx[..., 0::2], 2e-3, 1e-6)
     close(f"x states ({path})", x[..., 1::2], rx[..., 1::2], 1e-4, 1e-5)
+
+
+# zoh and bilinear (fp32) on the fast forward; the backward runs the general
+# kernels from its checkpoints.  bilinear never splits L (its A_bar is not
+# exp-form), zoh does on small grids.
+@pytest.mark.parametrize("method", ["zoh", "bilinear"])
+@pytest.mark.parametrize("schedule", ["default", "unsplit64", "unsplit32"])
+def test_zoh_bilinear_fast_forward_vs_oracle(dev, monkeypatch, method, schedule):
+    if schedule != "default":
+        monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", "1")
+        monkeypatch.setenv("LRNNX_SCAN_CHANNELS", schedule[-2:])
+    print(f"{method} fast forward, {schedule}", flush=True)
+    _run(dev, 2, 128, 512, 16, method=method, seed=83)
+    _run(dev, 2, 128, 512, 11, method=method, has_z=False, softplus=False, seed=84)
+
+
+@pytest.mark.parametrize("method", ["zoh", "bilinear"])
+@pytest.mark.parametrize("no_split", ["0", "1"])
+def test_zoh_bilinear_x_carries_vs_oracle(dev, monkeypatch, method, no_split):
+    """out, out_z and both halves of x over three chunks (bilinear's products
+    from a running product of A_bar, zoh's from exp(A sum delta'))."""
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", no_split)
+    Bt, D, L = 1, 64, 4160
+    inp = R.make_selective_inputs(Bt, D, L, 16, seed=85)
+    inp["delta"] = inp["delta"] * 0.1
+    ro, rx, roz = R.selective_scan_fwd_ref(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                                           inp["delta_bias"], None, True, method, compute_dtype=torch.float64)
+    d = to_dev(inp, dev)
+    B, C = d["B"].unsqueeze(1).contiguous(), d["C"].unsqueeze(1).contiguous()
+    out, x, out_z = ssc.fwd(d["u"], d["delta"], d["A"], B, C, d["D"], d["z"], d["delta_bias"], None, True, method)[:3]
+    torch.cuda.synchronize()
+    close(f"out ({method})", out, ro, 1e-4, 1e-5)
+    close(f"out_z ({method})", out_z, roz, 1e-4, 1e-5)
+    close(f"x products ({method})", x[..., 0::2], rx[..., 0::2], 2e-3, 1e-6)
+    close(f"x states ({method})", x[..., 1::2], rx[..., 1::2], 1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("method", ["zoh", "bilinear"])
+def test_zoh_bilinear_fast_forward_matches_generic(dev, monkeypatch, method):
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    inp = R.make_selective_inputs(2, 128, 512, 16, seed=86, groups=2)   # B / C (b, g, n, l)
+    d = to_dev(inp, dev)
+    res = []
+    for generic in ("0", "1"):
+        monkeypatch.setenv("LRNNX_SCAN_GENERIC", generic)
+        a = ssc.build_args(d["u"], d["delta"], d["A"], d["B"], d["C"], d["D"], d["z"], d["delta_bias"], None, True,
+                           method)
+        res.append(ssc.run_fwd(a, d["u"], d["delta"], d["A"], d["z"], want_ckpt=True))
+        torch.cuda.synchronize()
+    for name, f_, g_ in zip(("out", "x", "out_z", "ckpt"), res[0], res[1]):
+        close(f"{name} fast vs general ({method})", f_, g_.cpu().double(), 1e-5, 1e-5)
