@@ -112,8 +112,8 @@ const char* method_name(int m) {
 }
 
 
-// Methods with a fast forward: "mamba" at every input type; "dirac", "zoh"
-// and "bilinear", whose input is fp32 (the fast backward: mamba and dirac).
+// Methods with a fast path (forward and backward): "mamba" at every input
+// type; "dirac", "zoh" and "bilinear", whose input is fp32.
 bool has_fast_path(int method) {
   return method == LRNNX_MAMBA || method == LRNNX_DIRAC || method == LRNNX_ZOH || method == LRNNX_BILINEAR;
 }
@@ -158,9 +158,9 @@ hipError_t bwd_mamba(const lrnnx_selective_scan_args& a, float* ws, const float*
   }
 }
 
-// Forward / backward of the other real methods (fp32 input): the fast
-// forward for "dirac", "zoh" and "bilinear", the fast backward for "dirac",
-// when they cover the call; else the generic kernels.
+// Forward / backward of the other real methods (fp32 input): the fast path
+// for "dirac", "zoh" and "bilinear" when it covers the call; else the
+// generic kernels.
 hipError_t fwd_other(const lrnnx_selective_scan_args& a, hipStream_t st) {
   hipError_t e = hipSuccess;
   if (has_fast_path(a.method) && fast_paths_enabled() && ssf_fwd_f32(a, st, &e)) return e;
@@ -168,7 +168,7 @@ hipError_t fwd_other(const lrnnx_selective_scan_args& a, hipStream_t st) {
 }
 hipError_t bwd_other(const lrnnx_selective_scan_args& a, float* ws, const float* ckp, hipStream_t st) {
   hipError_t e = hipSuccess;
-  if (a.method == LRNNX_DIRAC && fast_paths_enabled() && ssf_bwd_f32(a, ws, ckp, st, &e)) return e;
+  if (has_fast_path(a.method) && fast_paths_enabled() && ssf_bwd_f32(a, ws, ckp, st, &e)) return e;
   return ss_bwd_other_f32(a, ws, ckp, st);
 }
 

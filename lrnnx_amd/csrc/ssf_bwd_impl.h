@@ -1,7 +1,8 @@
 // Selective scan backward, fast path of the headline case (gfx950).
 //
 // The fast forward's coverage (ssf_fwd_eligible): method "mamba" (f32 / bf16
-// / f16 I/O) and "dirac" (f32 I/O), variable B and C, d_state <= 16, 64
+// / f16 I/O), "dirac", "zoh" and "bilinear" (f32 I/O; zoh and bilinear in
+// 32-channel workgroups, unsplit), variable B and C, d_state <= 16, 64
 // channels per group block, L a multiple of 16, 16-byte aligned rows; deltaA
 // (mamba) without softplus, as Mamba's event mode passes it (with softplus
 // the extra raw tile would take the LDS past the 80 KB of two workgroups per
@@ -17,7 +18,12 @@
 // With deltaA, A_bar = exp(deltaA A): the A term goes to ddeltaA instead of
 // ddelta', and dA sums deltaA A_bar h_{t-1} dh.
 // For "dirac" (input term B u) delta' drops out of du and dB, and ddelta'
-// keeps the A term only.
+// keeps the A term only.  For "zoh" and "bilinear" (input factor beta per
+// state) du = sum_n dh beta B, dB_t = sum_d dh beta u, and
+//   ddelta' = sum_n dh dA_bar/ddelta' (A h_{t-1} + u B),
+// since dbeta/ddelta' = dA_bar/ddelta' / A: A_bar for zoh, r^2 for bilinear
+// (r = 1 / (1 - delta' A / 2) = (A_bar + 1) / 2); dA adds the input term
+// dh u B dbeta/dA: (delta' A_bar - beta) / A (zoh), delta'^2 r^2 / 2 (bilinear).
 //
 // Decomposition as in the forward (ssf_fwd_impl.h): one workgroup = one batch
 // row and 64 channels, wave w owns states 4w..4w+3, lane = channel.  The
@@ -82,7 +88,10 @@ __device__ __forceinline__ float softplus20_sig(float x, float& sg) {
 // deltaA (the step of A_bar) and the compute phases form delta' u from s_dl
 // and s_u; the raw deltaA tile takes the LDS that sigmoid(delta + bias) has
 // with softplus.
-template <typename IT, bool kSP, bool kZ, int kRT, int kCh = kWave, bool kDi = false, bool kDA = false>
+// kM: the method (LRNNX_MAMBA, DIRAC, ZOH or BILINEAR), compile-time; zoh and
+// bilinear re-derive their input factor beta from A_bar in the reverse walk,
+// whose extra terms fit the registers of the 32-channel form only.
+template <typename IT, bool kSP, bool kZ, int kRT, int kCh = kWave, int kM = LRNNX_MAMBA, bool kDA = false>
 __global__ void __launch_bounds__(ssf::kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __restrict__ ws, const SSBwdWs wo,
                const float* __restrict__ ckp, const int64_t seg_tiles) {
@@ -91,8 +100,12 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   static_assert(kT == kCk, "one checkpoint interval per tile");
   static_assert(kRT == kT || kRT == 2 * kT, "a raw fetch covers one or two tiles");
   static_assert(kCh == kWave || kCh == kWave / 2, "64 or 32 channels per workgroup");
-  static_assert(!kDi || sizeof(IT) == 4, "the dirac method takes fp32 input only");
-  static_assert(!kDA || (!kSP && !kDi), "deltaA on the fast backward: mamba without softplus");
+  constexpr bool kDi = kM == LRNNX_DIRAC;
+  constexpr bool kBeta = kM == LRNNX_ZOH || kM == LRNNX_BILINEAR;   // input factor per state
+  static_assert(kM == LRNNX_MAMBA || kDi || kBeta, "method");
+  static_assert(kM == LRNNX_MAMBA || sizeof(IT) == 4, "methods other than mamba take fp32 input only");
+  static_assert(!kDA || (!kSP && kM == LRNNX_MAMBA), "deltaA on the fast backward: mamba without softplus");
+  static_assert(!kBeta || kCh == kWave / 2, "zoh / bilinear: 32-channel workgroups");
   constexpr int kH = kWave / kCh;         // lane halves per wave
   constexpr int kS = 4 / kH;              // states per lane
   constexpr int kPair = kRT / kT;         // tiles per raw fetch
@@ -183,11 +196,19 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   const bool wr_bc = rs_n < N;
 
   float a2[kS], gn[kS], dA_acc[kS];
+  float Ar[kBeta ? kS : 1], iA[kM == LRNNX_ZOH ? kS : 1];   // A, 1 / A (zoh / bilinear)
+  // zoh: the input term of dA, sum dh u B (delta' A_bar - beta), times 1 / A at the end
+  float dAz[kM == LRNNX_ZOH ? kS : 1];
 #pragma unroll
   for (int k = 0; k < kS; ++k) {
     const int n = ns[k];
     const float A_ = n < N ? static_cast<const float*>(a.A.ptr)[(d0 + ch) * a.A.s0 + n * a.A.s1] : -1.f;
     a2[k] = A_ * kLog2e;
+    if constexpr (kBeta) Ar[k] = A_;
+    if constexpr (kM == LRNNX_ZOH) {
+      iA[k] = 1.f / A_;
+      dAz[k] = 0.f;
+    }
     // split of L: the adjoint entering this segment from the right
     gn[k] = (wo.S > 1 && n < N) ? ws[wo.g_init + ((blockIdx.z * a.batch + b) * N + n) * D + d0 + ch] : 0.f;
     dA_acc[k] = 0.f;
@@ -250,7 +271,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
       const float x = vd[i] + e_bias;
       vd[i] = kSP ? softplus20_sig(x, sg[i]) : x;
       dy[i] = vdo[i];
-      xu[i] = kDi ? vu[i] : vd[i] * vu[i];
+      xu[i] = (kDi || kBeta) ? vu[i] : vd[i] * vu[i];
     }
     if constexpr (kZ) {
       float vz[kEt], vo[kEt], dz[kEt];
@@ -315,8 +336,8 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     float du[kEt], dd[kEt], dda[kEt];
 #pragma unroll
     for (int i = 0; i < kEt; ++i) {
-      du[i] = kDi ? fmaf(e_D, dy[i], p1[i]) : fmaf(dl[i], p1[i], e_D * dy[i]);
-      const float ddl = kDi ? kLn2 * p2[i] : kDA ? uu[i] * p1[i] : fmaf(uu[i], p1[i], kLn2 * p2[i]);
+      du[i] = (kDi || kBeta) ? fmaf(e_D, dy[i], p1[i]) : fmaf(dl[i], p1[i], e_D * dy[i]);
+      const float ddl = kBeta ? p2[i] : kDi ? kLn2 * p2[i] : kDA ? uu[i] * p1[i] : fmaf(uu[i], p1[i], kLn2 * p2[i]);
       dda[i] = kLn2 * p2[i];
       dd[i] = kSP ? ddl * sg[i] : ddl;
       e_dD = fmaf(dy[i], uu[i], e_dD);
@@ -411,6 +432,12 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     // recompute A_bar and h over the tile; dC_t = sum_d dy_t h_t is complete
     // here, so its reduce-scatter runs with it (steps in increasing order)
     float AB[kT][kS], H[kT][kS];
+    // the input factor beta of zoh / bilinear from A_bar: expm1(delta' A) / A
+    // (zoh; A_bar = exp(delta' A)), delta' r with r = (A_bar + 1) / 2 (bilinear)
+    auto beta_of = [&](float ab, float dlt, int k) __attribute__((always_inline)) {
+      if constexpr (kM == LRNNX_ZOH) return expm1_from(dlt * Ar[k], ab) * iA[k];
+      else return dlt * (0.5f * (ab + 1.f));
+    };
     float c8[8], c4[4], c2[2], c1 = 0.f, dC_part = 0.f;
     auto stream_dC = [&](int t, float v) __attribute__((always_inline)) {
       if (t < 8) { c8[t] = v; return; }
@@ -449,8 +476,17 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
           float vC[kS];
 #pragma unroll
           for (int k = 0; k < kS; ++k) {
-            const float ab = __builtin_amdgcn_exp2f(dl[i] * a2[k]);
-            hc[k] = fmaf(ab, hc[k], x * bv[k]);
+            float ab, xk = x;   // A_bar and the input factor times u
+            if constexpr (kM == LRNNX_BILINEAR) {
+              const float v = 0.5f * dl[i] * Ar[k];
+              const float r = __builtin_amdgcn_rcpf(1.f - v);
+              ab = (1.f + v) * r;
+              xk = dl[i] * r * x;
+            } else {
+              ab = __builtin_amdgcn_exp2f(dl[i] * a2[k]);
+              if constexpr (kM == LRNNX_ZOH) xk = beta_of(ab, dl[i], k) * x;
+            }
+            hc[k] = fmaf(ab, hc[k], xk * bv[k]);
             AB[t][k] = ab;
             H[t][k] = hc[k];
             vC[k] = dy[i] * hc[k];
@@ -499,11 +535,35 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
           const float dh = fmaf(dy[i], cv[k], gn[k]);
           const float gk = AB[t][k] * dh;
           gn[k] = gk;
-          const float wv = gk * (t > 0 ? H[t - 1][k] : h0[k]);
-          p2 = fmaf(wv, a2[k], p2);   // A log2(e) units; the epilogue multiplies by ln 2
-          dA_acc[k] = fmaf(wv, dl[i], dA_acc[k]);
-          p1 = fmaf(dh, bv[k], p1);
-          vB[k] = dh * x;
+          const float hp = t > 0 ? H[t - 1][k] : h0[k];
+          if constexpr (kBeta) {
+            // natural units: the epilogue takes p2 as ddelta' unscaled
+            const float be = beta_of(AB[t][k], dl[i], k);
+            const float g2 = dh * bv[k];                 // dh B
+            const float q = fmaf(Ar[k], hp, x * bv[k]);  // A h_{t-1} + u B
+            p1 = fmaf(g2, be, p1);
+            if constexpr (kM == LRNNX_ZOH) {
+              p2 = fmaf(gk, q, p2);
+              dA_acc[k] = fmaf(gk * hp, dl[i], dA_acc[k]);
+              dAz[k] = fmaf(g2 * x, fmaf(dl[i], AB[t][k], -be), dAz[k]);
+              // accumulate at this step: sinking the chains to the end of the
+              // walk keeps every step's operands live (spills past 256 VGPRs)
+              pin_vgpr(dA_acc[k]);
+              pin_vgpr(dAz[k]);
+            } else {
+              const float rr = 0.5f * (AB[t][k] + 1.f);
+              const float dr = dh * (rr * rr);           // dh r^2
+              p2 = fmaf(dr, q, p2);
+              dA_acc[k] = fmaf(dr * dl[i], fmaf(0.5f * dl[i], x * bv[k], hp), dA_acc[k]);
+            }
+            vB[k] = dh * be * x;
+          } else {
+            const float wv = gk * hp;
+            p2 = fmaf(wv, a2[k], p2);   // A log2(e) units; the epilogue multiplies by ln 2
+            dA_acc[k] = fmaf(wv, dl[i], dA_acc[k]);
+            p1 = fmaf(dh, bv[k], p1);
+            vB[k] = dh * x;
+          }
         }
         p1v[i] = p1;
         p2v[i] = p2;
@@ -529,8 +589,10 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   // per-((segment, b), d, n) and per-((segment, b), d) partials, summed over
   // the rows by ss_reduce_batch_kernel
 #pragma unroll
-  for (int k = 0; k < kS; ++k)
+  for (int k = 0; k < kS; ++k) {
+    if constexpr (kM == LRNNX_ZOH) dA_acc[k] = fmaf(dAz[k], iA[k], dA_acc[k]);
     if (ns[k] < N) ws[wo.dA + (prow * D + d0 + ch) * N + ns[k]] = dA_acc[k];
+  }
   // dD / ddelta_bias: the kP threads of a channel are consecutive lanes
   e_dD += dpp_mov<kDppQuadXor1>(e_dD);
   e_dD += dpp_mov<kDppQuadXor2>(e_dD);
@@ -646,7 +708,8 @@ inline bool ssf_bwd_eligible(const lrnnx_selective_scan_args& a) {
 // from shapes and options only, so that the workspace size and the launch agree.
 template <typename IT>
 inline int64_t ssf_bwd_segs(const lrnnx_selective_scan_args& a) {
-  if (!ssf_bwd_shape_ok<IT>(a)) return 1;
+  // (zoh / bilinear run unsplit: their 32-channel grid is twice the 64-channel one)
+  if (!ssf_bwd_shape_ok<IT>(a) || a.method == LRNNX_ZOH || a.method == LRNNX_BILINEAR) return 1;
   const int64_t steps = ssf::seg_steps(a);
   return steps ? ssf::n_segs(a, steps) : 1;
 }
@@ -658,7 +721,9 @@ inline int64_t ssf_bwd_segs(const lrnnx_selective_scan_args& a) {
 // LRNNX_SCAN_CHANNELS forces either where 32 is possible.
 template <typename IT>
 inline int ssf_bwd_chans(const lrnnx_selective_scan_args& a) {
-  if (!ssf_bwd_shape_ok<IT>(a) || ssf_bwd_segs<IT>(a) > 1) return kWave;
+  if (!ssf_bwd_shape_ok<IT>(a)) return kWave;
+  if (a.method == LRNNX_ZOH || a.method == LRNNX_BILINEAR) return kWave / 2;   // (fp32: kRT = 16)
+  if (ssf_bwd_segs<IT>(a) > 1) return kWave;
   if (sizeof(IT) == 2 && a.seqlen % (2 * ssf::kCk) != 0) return kWave;
   const int o = scan_channels_override();
   if (o) return o;
@@ -677,7 +742,7 @@ inline SSGeom ssf_bwd_geom(const lrnnx_selective_scan_args& a) {
   return g;
 }
 
-template <typename IT, bool kSP, bool kZ, bool kDi, bool kDA = false>
+template <typename IT, bool kSP, bool kZ, int kM, bool kDA = false>
 inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                              const float* ckp, int64_t seg_steps, hipStream_t st) {
   // Two-tile raw fetches for 16-bit I/O when every segment holds an even
@@ -699,22 +764,25 @@ inline void ssf_bwd_launch_t(const lrnnx_selective_scan_args& a, const SSGeom& g
   if constexpr (kTwo) {
     if (a.seqlen % (2 * ssf::kCk) == 0) {
       if (c32)
-        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave / 2, kDi, kDA>), grid, blk, 0, st, a, g.n_ck, ws,
+        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave / 2, kM, kDA>), grid, blk, 0, st, a, g.n_ck, ws,
                            wo, ckp, seg_tiles);
       else
-        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave, kDi, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo,
+        hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, 2 * ssf::kCk, kWave, kM, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo,
                            ckp, seg_tiles);
       return;
     }
     // (the 32-channel form comes with two-tile fetches only: ssf_bwd_chans)
-    hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave, kDi, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+    hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave, kM, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
                        seg_tiles);
+  } else if constexpr (kM == LRNNX_ZOH || kM == LRNNX_BILINEAR) {   // 32 channels only (ssf_bwd_chans)
+    hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave / 2, kM, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo,
+                       ckp, seg_tiles);
   } else {
     if (c32)
-      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave / 2, kDi, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave / 2, kM, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
                          seg_tiles);
     else
-      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave, kDi, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
+      hipLaunchKernelGGL((ssf_bwd_kernel<IT, kSP, kZ, ssf::kCk, kWave, kM, kDA>), grid, blk, 0, st, a, g.n_ck, ws, wo, ckp,
                          seg_tiles);
   }
 }
@@ -726,28 +794,31 @@ inline hipError_t ssf_bwd_launch(const lrnnx_selective_scan_args& a, float* ws, 
   const SSBwdWs wo = ss_bwd_ws(a, g, a.ckpt == nullptr, S);
   const int64_t steps = S > 1 ? ssf::seg_steps(a) : 0;
   const bool z = a.z.ptr != nullptr;
-  bool di = false;
-  if constexpr (sizeof(IT) == 4) di = a.method == LRNNX_DIRAC;   // dirac: fp32 input only (shape_ok)
-  if (a.deltaA.ptr) {   // mamba without softplus (ssf_bwd_shape_ok)
-    if (z) ssf_bwd_launch_t<IT, false, true, false, true>(a, g, ws, wo, ckp, steps, st);
-    else ssf_bwd_launch_t<IT, false, false, false, true>(a, g, ws, wo, ckp, steps, st);
-  } else if (di) {
-    if constexpr (sizeof(IT) == 4) {
-      if (a.delta_softplus) {
-        if (z) ssf_bwd_launch_t<IT, true, true, true>(a, g, ws, wo, ckp, steps, st);
-        else ssf_bwd_launch_t<IT, true, false, true>(a, g, ws, wo, ckp, steps, st);
-      } else {
-        if (z) ssf_bwd_launch_t<IT, false, true, true>(a, g, ws, wo, ckp, steps, st);
-        else ssf_bwd_launch_t<IT, false, false, true>(a, g, ws, wo, ckp, steps, st);
-      }
+  auto by_opts = [&](auto m) __attribute__((always_inline)) {
+    constexpr int kM = decltype(m)::value;
+    if (a.delta_softplus) {
+      if (z) ssf_bwd_launch_t<IT, true, true, kM>(a, g, ws, wo, ckp, steps, st);
+      else ssf_bwd_launch_t<IT, true, false, kM>(a, g, ws, wo, ckp, steps, st);
+    } else {
+      if (z) ssf_bwd_launch_t<IT, false, true, kM>(a, g, ws, wo, ckp, steps, st);
+      else ssf_bwd_launch_t<IT, false, false, kM>(a, g, ws, wo, ckp, steps, st);
     }
-  } else if (a.delta_softplus) {
-    if (z) ssf_bwd_launch_t<IT, true, true, false>(a, g, ws, wo, ckp, steps, st);
-    else ssf_bwd_launch_t<IT, true, false, false>(a, g, ws, wo, ckp, steps, st);
-  } else {
-    if (z) ssf_bwd_launch_t<IT, false, true, false>(a, g, ws, wo, ckp, steps, st);
-    else ssf_bwd_launch_t<IT, false, false, false>(a, g, ws, wo, ckp, steps, st);
+  };
+  bool done = false;
+  if (a.deltaA.ptr) {   // mamba without softplus (ssf_bwd_shape_ok)
+    if (z) ssf_bwd_launch_t<IT, false, true, LRNNX_MAMBA, true>(a, g, ws, wo, ckp, steps, st);
+    else ssf_bwd_launch_t<IT, false, false, LRNNX_MAMBA, true>(a, g, ws, wo, ckp, steps, st);
+    done = true;
+  } else if constexpr (sizeof(IT) == 4) {   // the other methods: fp32 input only (shape_ok)
+    done = true;
+    switch (a.method) {
+      case LRNNX_DIRAC: by_opts(std::integral_constant<int, LRNNX_DIRAC>{}); break;
+      case LRNNX_ZOH: by_opts(std::integral_constant<int, LRNNX_ZOH>{}); break;
+      case LRNNX_BILINEAR: by_opts(std::integral_constant<int, LRNNX_BILINEAR>{}); break;
+      default: done = false;
+    }
   }
+  if (!done) by_opts(std::integral_constant<int, LRNNX_MAMBA>{});
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return ss_bwd_reductions<IT, true, true>(a, g, ws, wo, st);

@@ -484,15 +484,14 @@ inline bool fetch_fits(const lrnnx_view& v, bool states, int64_t row_bytes) {
 }
 
 // Shape / option part of the fast-path coverage (both directions).
-// fwd: the coverage of the forward (deltaA with mamba; zoh and bilinear),
-// else of the backward (ssf_bwd_shape_ok adds deltaA without softplus).
+// fwd: the coverage of the forward (deltaA with mamba), else of the backward
+// (ssf_bwd_shape_ok adds deltaA without softplus).
 template <typename IT>
 inline bool shape_ok(const lrnnx_selective_scan_args& a, int64_t tile, bool fwd = false, bool bwd_dA = false) {
-  // "mamba" at every input type; "dirac" (both directions), "zoh" and
-  // "bilinear" (forward) at fp32 input
+  // "mamba" at every input type; "dirac", "zoh" and "bilinear" at fp32 input
   const bool f32 = sizeof(IT) == 4;
-  const bool m_ok = a.method == LRNNX_MAMBA || (f32 && a.method == LRNNX_DIRAC) ||
-                    (f32 && fwd && (a.method == LRNNX_ZOH || a.method == LRNNX_BILINEAR));
+  const bool m_ok = a.method == LRNNX_MAMBA ||
+                    (f32 && (a.method == LRNNX_DIRAC || a.method == LRNNX_ZOH || a.method == LRNNX_BILINEAR));
   if (!m_ok || a.wtype != LRNNX_F32 || !a.var_B || !a.var_C) return false;
   if (a.deltaA.ptr && (!(fwd || bwd_dA) || a.method != LRNNX_MAMBA)) return false;
   if (a.deltaA.ptr && (!fetch_fits<IT>(a.deltaA, false, 64) || !rows_aligned<IT>(a.deltaA, false))) return false;

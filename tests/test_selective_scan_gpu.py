@@ -583,16 +583,16 @@ def test_x_carries_vs_oracle(dev, monkeypatch, path, itype):
     close(f"x states ({path})", x[..., 1::2], rx[..., 1::2], 1e-4, 1e-5)
 
 
-# zoh and bilinear (fp32) on the fast forward; the backward runs the general
-# kernels from its checkpoints.  bilinear never splits L (its A_bar is not
-# exp-form), zoh does on small grids.
+# zoh and bilinear (fp32) on the fast kernels: the forward in either channel
+# form (bilinear never splits L: its A_bar is not exp-form; zoh does on small
+# grids), the backward in 32-channel workgroups, unsplit.
 @pytest.mark.parametrize("method", ["zoh", "bilinear"])
 @pytest.mark.parametrize("schedule", ["default", "unsplit64", "unsplit32"])
-def test_zoh_bilinear_fast_forward_vs_oracle(dev, monkeypatch, method, schedule):
+def test_zoh_bilinear_fast_path_vs_oracle(dev, monkeypatch, method, schedule):
     if schedule != "default":
         monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", "1")
         monkeypatch.setenv("LRNNX_SCAN_CHANNELS", schedule[-2:])
-    print(f"{method} fast forward, {schedule}", flush=True)
+    print(f"{method} fast path, {schedule}", flush=True)
     _run(dev, 2, 128, 512, 16, method=method, seed=83)
     _run(dev, 2, 128, 512, 11, method=method, has_z=False, softplus=False, seed=84)
 
@@ -635,3 +635,27 @@ def test_zoh_bilinear_fast_forward_matches_generic(dev, monkeypatch, method):
         torch.cuda.synchronize()
     for name, f_, g_ in zip(("out", "x", "out_z", "ckpt"), res[0], res[1]):
         close(f"{name} fast vs general ({method})", f_, g_.cpu().double(), 1e-5, 1e-5)
+
+
+@pytest.mark.parametrize("method", ["zoh", "bilinear"])
+@pytest.mark.parametrize("with_z", [True, False])
+def test_zoh_bilinear_fast_path_matches_generic(dev, monkeypatch, method, with_z):
+    """fwd + bwd of zoh / bilinear on the fast and on the general kernels:
+    every output and gradient (fp32 state; sums in another order)."""
+    inp = R.make_selective_inputs(2, 128, 512, 16, seed=87, groups=2, has_z=with_z)
+    dout = torch.randn(2, 128, 512, generator=torch.Generator().manual_seed(88)).to(dev)
+    d = to_dev(inp, dev)
+    keys = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias") if with_z else ("u", "delta", "A", "B", "C", "D",
+                                                                                  "delta_bias")
+    res = []
+    for generic in ("0", "1"):
+        monkeypatch.setenv("LRNNX_SCAN_GENERIC", generic)
+        lv = {k: d[k].clone().requires_grad_(True) for k in keys}
+        out, last = selective_scan_fn(lv["u"], lv["delta"], lv["A"], lv["B"], lv["C"], lv["D"], lv.get("z"),
+                                      lv["delta_bias"], None, True, True, method)
+        out.backward(dout)
+        torch.cuda.synchronize()
+        res.append([out.detach(), last.detach()] + [lv[k].grad for k in keys])
+    names = ["out", "last_state"] + ["d" + k for k in keys]
+    for n, a_, b_ in zip(names, res[0], res[1]):
+        close(f"{n} fast vs general ({method})", a_, b_.cpu().double(), 1e-5, 1e-5)
