@@ -200,5 +200,32 @@ def test_workspace_queries_are_host_only():
     # (seg, b, n, d) plus two (seg, b, d) sums of delta', fp32
     a.batch, a.dim, a.seqlen = 1, 64, 2048
     assert L.lrnnx_selective_scan_workspace_size(a, 0) == (2 * 16 * 16 * 64 + 2 * 16 * 64) * 4
-    a.method = 0  # zoh: the general kernels, never split
+    a.method = 0  # zoh at bf16: the general kernels (the reference takes zoh at fp32 only), unsplit
     assert L.lrnnx_selective_scan_workspace_size(a, 0) == 0
+    a.itype = _lib.F32  # zoh at fp32: the fast forward, split like mamba (exp-form A_bar)
+    assert L.lrnnx_selective_scan_workspace_size(a, 0) == (2 * 16 * 16 * 64 + 2 * 16 * 64) * 4
+    a.method = 1  # bilinear: the fast forward, never split (its A_bar is not exp-form)
+    assert L.lrnnx_selective_scan_workspace_size(a, 0) == 0
+
+
+def test_state_block_sizes_are_host_only():
+    """d_state > 64: blocks of at most 64 states with 8-step checkpoints; the
+    forward's optional workspace holds one fp32 partial y per block, the
+    backward's the blocks' du / ddelta term sums (two for mamba, three for zoh)."""
+    L = _lib.lib()
+    a = _lib.SelectiveScanArgs()
+    a.batch, a.dim, a.seqlen, a.n_groups = 2, 64, 160, 1
+    a.itype, a.wtype, a.method, a.var_B, a.var_C = _lib.F32, _lib.F32, 3, 1, 1
+    for n, nsb in ((64, 1), (65, 2), (128, 2), (200, 4), (256, 4)):
+        a.dstate = n
+        assert L.lrnnx_selective_scan_ckpt_size(a) == 2 * (160 // 8) * n * 64 * 4, n
+        fws = L.lrnnx_selective_scan_workspace_size(a, 0)
+        assert fws == (nsb * 2 * 64 * 160 * 4 if nsb > 1 else 0), (n, fws)
+    a.dstate = 128
+    bws_mamba = L.lrnnx_selective_scan_workspace_size(a, 1)
+    a.method = 0
+    bws_zoh = L.lrnnx_selective_scan_workspace_size(a, 1)
+    assert bws_mamba >= 2 * 2 * 2 * 64 * 160 * 4          # blocks x terms x B x D x L fp32
+    assert bws_zoh - bws_mamba == 2 * 2 * 64 * 160 * 4     # zoh's third term
+    a.dstate = 16   # d_state <= 16: 16-step checkpoints (the fast kernels' interval)
+    assert L.lrnnx_selective_scan_ckpt_size(a) == 2 * (160 // 16) * 16 * 64 * 4
