@@ -659,3 +659,35 @@ def test_zoh_bilinear_fast_path_matches_generic(dev, monkeypatch, method, with_z
     names = ["out", "last_state"] + ["d" + k for k in keys]
     for n, a_, b_ in zip(names, res[0], res[1]):
         close(f"{n} fast vs general ({method})", a_, b_.cpu().double(), 1e-5, 1e-5)
+
+
+@pytest.mark.parametrize("method", ["zoh", "bilinear"])
+@pytest.mark.parametrize("no_split", ["0", "1"])
+def test_zoh_bilinear_binding_bwd_from_x(dev, monkeypatch, method, no_split):
+    """selective_scan_cuda.fwd -> bwd(x, out) in save mode "x": the backward
+    rebuilds the checkpoints on the fast states-only forward (zoh: split on
+    this small grid or, unsplit, one 2048-step chunk per grid slice from the x
+    carries; bilinear never splits) and runs the fast backward."""
+    from lrnnx_amd import selective_scan_cuda as ssc
+
+    monkeypatch.setenv("LRNNX_SCAN_NO_SPLIT", no_split)
+    prev = ssc.save_mode()
+    ssc.set_save_mode("x")
+    try:
+        Bt, D, L = 1, 64, 4160
+        inp = R.make_selective_inputs(Bt, D, L, 16, seed=89)
+        dout = torch.randn(Bt, D, L, generator=torch.Generator().manual_seed(90))
+        ro, rl, rg = oracle_selective(inp, method, True, None, True, dout)
+        d = to_dev(inp, dev)
+        u, dl, A, B, C, Dv, z, db = (d[k] for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias"))
+        B, C = B.unsqueeze(1).contiguous(), C.unsqueeze(1).contiguous()
+        out, x, out_z = ssc.fwd(u, dl, A, B, C, Dv, z, db, None, True, method)[:3]
+        g = ssc.bwd(u, dl, A, B, C, Dv, z, db, None, dout.to(dev), x, out, None, True, False, method)
+        torch.cuda.synchronize()
+    finally:
+        ssc.set_save_mode(prev)
+    close("out", out_z, ro, 1e-4, 1e-5)
+    for i, k in enumerate(("u", "delta", "A", "B", "C", "D", "delta_bias")):
+        gk = g[i].squeeze(1) if k in ("B", "C") else g[i]
+        close(f"d{k}", gk, rg[k], 1e-4, 1e-4 if k in ("A", "D", "delta_bias") else 1e-5)
+    close("dz", g[7], rg["z"], 1e-4, 1e-5)
