@@ -540,7 +540,7 @@ def dstate_sweep(torch, dev, ss, L_):
 
     Bt, D, L = 8, 1536, 2048
     res = {}
-    for N, generic in ((1, "0"), (8, "0"), (16, "0"), (16, "1"), (32, "0"), (64, "0"), (65, "0"), (100, "0"),
+    for N, generic in ((1, "0"), (8, "0"), (16, "0"), (16, "1"), (24, "0"), (32, "0"), (64, "0"), (65, "0"), (100, "0"),
                        (128, "0"), (256, "0")):
         prev = os.environ.get("LRNNX_SCAN_GENERIC")
         os.environ["LRNNX_SCAN_GENERIC"] = generic

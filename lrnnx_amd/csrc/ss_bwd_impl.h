@@ -121,7 +121,8 @@ __device__ __forceinline__ void lds_states(const float* p, float* o) {
   }
 }
 
-template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
+// kNWm: most waves of a launch (as in the forward).
+template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA, int kNWm = fwd_nw_max(kS)>
 __global__ void __launch_bounds__(512)
 ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_ck, float* __restrict__ ws,
               const SSBwdWs wo, const float* __restrict__ ckp, const int flags, const int nsb) {
@@ -136,7 +137,7 @@ ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   // A_bar of the interval kept in VGPRs (s7's is one value per step; mamba
   // and dirac keep it up to kS = 4 and re-derive it, one exp, above)
   constexpr bool kAbLive = kMethod == LRNNX_S7 || (!kP3 && kS <= 4);
-  constexpr int kNWmax = fwd_nw_max(kS);
+  constexpr int kNWmax = kNWm;
   constexpr int kNPmax = kNWmax * kS;
   constexpr int kRawArr = kWave * kTB * (int)sizeof(IT);
   constexpr int kRawBC = kNPmax * kTB * (int)sizeof(IT);
@@ -904,12 +905,12 @@ ss_bwd_combine_kernel(const lrnnx_selective_scan_args a, float* __restrict__ ws,
   }
 }
 
-template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
+template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA, int kNWm>
 static hipError_t launch_bwd_t(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                                const float* ckp, hipStream_t st) {
   dim3 grid(g.n_cb, (unsigned)a.batch, (unsigned)g.nsb);
   dim3 block(g.nW * kWave);
-  if (g.nW > fwd_nw_max(kS)) return hipErrorInvalidConfiguration;
+  if (g.nW > kNWm) return hipErrorInvalidConfiguration;
   // async LDS fetches need 16-byte aligned row starts for every fetched tensor
   auto al = [](const void* p, int64_t s_batch, int64_t s_row) {
     return p == nullptr || ((reinterpret_cast<uintptr_t>(p) & 15u) == 0 && ((s_batch * sizeof(IT)) & 15) == 0 &&
@@ -926,7 +927,7 @@ static hipError_t launch_bwd_t(const lrnnx_selective_scan_args& a, const SSGeom&
   const bool out_ok = al(a.du.ptr, a.du.s0, a.du.s1) && al(a.ddelta.ptr, a.ddelta.s0, a.ddelta.s1) &&
                       al(a.ddeltaA.ptr, a.ddeltaA.s0, a.ddeltaA.s1) && (!has_z || al(a.dz.ptr, a.dz.s0, a.dz.s1));
   const int flags = (in_ok ? kFlagAsyncIn : 0) | (out_ok ? kFlagAlignedOut : 0);
-  hipLaunchKernelGGL((ss_bwd_kernel<IT, kS, kMethod, kVarB, kVarC, kDA>), grid, block, 0, st, a, g.CB, g.n_ck, ws,
+  hipLaunchKernelGGL((ss_bwd_kernel<IT, kS, kMethod, kVarB, kVarC, kDA, kNWm>), grid, block, 0, st, a, g.CB, g.n_ck, ws,
                      wo, ckp, flags, g.nsb);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -986,22 +987,22 @@ static hipError_t ss_bwd_reductions(const lrnnx_selective_scan_args& a, const SS
   return hipGetLastError();
 }
 
-template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC>
+template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, int kNWm>
 static hipError_t launch_bwd_da(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                                 const float* ckp, hipStream_t st) {
   if constexpr (uses_deltaA<kMethod>()) {
-    if (a.deltaA.ptr != nullptr) return launch_bwd_t<IT, kS, kMethod, kVarB, kVarC, true>(a, g, ws, wo, ckp, st);
+    if (a.deltaA.ptr != nullptr) return launch_bwd_t<IT, kS, kMethod, kVarB, kVarC, true, kNWm>(a, g, ws, wo, ckp, st);
   }
-  return launch_bwd_t<IT, kS, kMethod, kVarB, kVarC, false>(a, g, ws, wo, ckp, st);
+  return launch_bwd_t<IT, kS, kMethod, kVarB, kVarC, false, kNWm>(a, g, ws, wo, ckp, st);
 }
 
-template <typename IT, int kS, int kMethod>
+template <typename IT, int kS, int kMethod, int kNWm = fwd_nw_max(kS)>
 static hipError_t launch_bwd_bc(const lrnnx_selective_scan_args& a, const SSGeom& g, float* ws, const SSBwdWs& wo,
                                 const float* ckp, hipStream_t st) {
-  if (a.var_B && a.var_C) return launch_bwd_da<IT, kS, kMethod, true, true>(a, g, ws, wo, ckp, st);
-  if (a.var_B) return launch_bwd_da<IT, kS, kMethod, true, false>(a, g, ws, wo, ckp, st);
-  if (a.var_C) return launch_bwd_da<IT, kS, kMethod, false, true>(a, g, ws, wo, ckp, st);
-  return launch_bwd_da<IT, kS, kMethod, false, false>(a, g, ws, wo, ckp, st);
+  if (a.var_B && a.var_C) return launch_bwd_da<IT, kS, kMethod, true, true, kNWm>(a, g, ws, wo, ckp, st);
+  if (a.var_B) return launch_bwd_da<IT, kS, kMethod, true, false, kNWm>(a, g, ws, wo, ckp, st);
+  if (a.var_C) return launch_bwd_da<IT, kS, kMethod, false, true, kNWm>(a, g, ws, wo, ckp, st);
+  return launch_bwd_da<IT, kS, kMethod, false, false, kNWm>(a, g, ws, wo, ckp, st);
 }
 
 template <typename IT, int kMethod>
@@ -1010,7 +1011,9 @@ static hipError_t launch_bwd_s(const lrnnx_selective_scan_args& a, const SSGeom&
   switch (g.kS) {
     case 1: return launch_bwd_bc<IT, 1, kMethod>(a, g, ws, wo, ckp, st);
     case 4: return launch_bwd_bc<IT, 4, kMethod>(a, g, ws, wo, ckp, st);
-    case 8: return launch_bwd_bc<IT, 8, kMethod>(a, g, ws, wo, ckp, st);
+    case 8:   // d_state 17..32: at most 4 waves, half the LDS (as in the forward)
+      return g.nW <= 4 ? launch_bwd_bc<IT, 8, kMethod, 4>(a, g, ws, wo, ckp, st)
+                       : launch_bwd_bc<IT, 8, kMethod>(a, g, ws, wo, ckp, st);
   }
   return hipErrorInvalidValue;
 }

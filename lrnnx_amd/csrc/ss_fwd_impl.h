@@ -41,7 +41,9 @@ __host__ __device__ constexpr int fwd_nw_max(int kS) { return (kS == 8 || kS == 
 
 // ypart: with state blocks (grid z > 1) and outputs, the block's partial y
 // (sum over its states of C h, fp32, [block][b][d][L]) instead of out / out_z.
-template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
+// kNWm: most waves of a launch (LDS is sized for it; fewer waves than
+// fwd_nw_max(kS) halve it for d_state 17..32).
+template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA, int kNWm = fwd_nw_max(kS)>
 __global__ void __launch_bounds__(512)
 ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_ck, const int flags,
               float* __restrict__ ypart) {
@@ -51,7 +53,7 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   constexpr int kQ = kT / kEl;           // blocks per row
   constexpr int kG = kT / 4;             // groups of 4 steps
   static_assert(kT % kCk == 0 || kCk % kT == 0, "tile / checkpoint interval mismatch");
-  constexpr int kNWmax = fwd_nw_max(kS);
+  constexpr int kNWmax = kNWm;
   constexpr int kNPmax = kNWmax * kS;
   constexpr int kRawArr = kWave * kT * (int)sizeof(IT);   // one [64][kT] raw tile (bytes)
   constexpr int kRawBC = kNPmax * kT * (int)sizeof(IT);   // one [NP][kT] raw B or C tile
@@ -452,14 +454,14 @@ ss_fwd_combine_kernel(const lrnnx_selective_scan_args a, const float* __restrict
   }
 }
 
-template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA>
+template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, bool kDA, int kNWm>
 static hipError_t launch_fwd_t(const lrnnx_selective_scan_args& a, const SSGeom& g, hipStream_t st) {
   // state blocks write partial y to the workspace when there are outputs (ss_fwd_blocks_ws_bytes;
   // launch_fwd_s falls back to one block when the workspace is missing)
   float* ypart = (g.nsb > 1 && (a.out.ptr || a.out_z.ptr)) ? static_cast<float*>(a.workspace) : nullptr;
   dim3 grid(g.n_cb, (unsigned)a.batch, (unsigned)g.nsb);
   dim3 block(g.nW * kWave);
-  if (g.nW > fwd_nw_max(kS)) return hipErrorInvalidConfiguration;
+  if (g.nW > kNWm) return hipErrorInvalidConfiguration;
   // async LDS fetches need 16-byte aligned row starts for every fetched tensor
   auto al = [](const void* p, int64_t s_batch, int64_t s_row) {
     return p == nullptr || ((reinterpret_cast<uintptr_t>(p) & 15u) == 0 && ((s_batch * sizeof(IT)) & 15) == 0 &&
@@ -471,7 +473,7 @@ static hipError_t launch_fwd_t(const lrnnx_selective_scan_args& a, const SSGeom&
                      (!kVarC || (al(a.C.ptr, a.C.s0, a.C.s2) && ((a.C.s1 * sizeof(IT)) & 15) == 0));
   const bool out_ok = al(a.out.ptr, a.out.s0, a.out.s1) && al(a.out_z.ptr, a.out_z.s0, a.out_z.s1);
   const int flags = (in_ok ? kFlagAsyncIn : 0) | (out_ok ? kFlagAlignedOut : 0);
-  hipLaunchKernelGGL((ss_fwd_kernel<IT, kS, kMethod, kVarB, kVarC, kDA>), grid, block, 0, st, a, g.CB, g.n_ck,
+  hipLaunchKernelGGL((ss_fwd_kernel<IT, kS, kMethod, kVarB, kVarC, kDA, kNWm>), grid, block, 0, st, a, g.CB, g.n_ck,
                      flags, ypart);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || ypart == nullptr) return e;
@@ -481,20 +483,20 @@ static hipError_t launch_fwd_t(const lrnnx_selective_scan_args& a, const SSGeom&
   return hipGetLastError();
 }
 
-template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC>
+template <typename IT, int kS, int kMethod, bool kVarB, bool kVarC, int kNWm>
 static hipError_t launch_fwd_da(const lrnnx_selective_scan_args& a, const SSGeom& g, hipStream_t st) {
   if constexpr (uses_deltaA<kMethod>()) {
-    if (a.deltaA.ptr != nullptr) return launch_fwd_t<IT, kS, kMethod, kVarB, kVarC, true>(a, g, st);
+    if (a.deltaA.ptr != nullptr) return launch_fwd_t<IT, kS, kMethod, kVarB, kVarC, true, kNWm>(a, g, st);
   }
-  return launch_fwd_t<IT, kS, kMethod, kVarB, kVarC, false>(a, g, st);
+  return launch_fwd_t<IT, kS, kMethod, kVarB, kVarC, false, kNWm>(a, g, st);
 }
 
-template <typename IT, int kS, int kMethod>
+template <typename IT, int kS, int kMethod, int kNWm = fwd_nw_max(kS)>
 static hipError_t launch_fwd_bc(const lrnnx_selective_scan_args& a, const SSGeom& g, hipStream_t st) {
-  if (a.var_B && a.var_C) return launch_fwd_da<IT, kS, kMethod, true, true>(a, g, st);
-  if (a.var_B) return launch_fwd_da<IT, kS, kMethod, true, false>(a, g, st);
-  if (a.var_C) return launch_fwd_da<IT, kS, kMethod, false, true>(a, g, st);
-  return launch_fwd_da<IT, kS, kMethod, false, false>(a, g, st);
+  if (a.var_B && a.var_C) return launch_fwd_da<IT, kS, kMethod, true, true, kNWm>(a, g, st);
+  if (a.var_B) return launch_fwd_da<IT, kS, kMethod, true, false, kNWm>(a, g, st);
+  if (a.var_C) return launch_fwd_da<IT, kS, kMethod, false, true, kNWm>(a, g, st);
+  return launch_fwd_da<IT, kS, kMethod, false, false, kNWm>(a, g, st);
 }
 
 template <typename IT, int kMethod>
@@ -513,7 +515,8 @@ static hipError_t launch_fwd_s(const lrnnx_selective_scan_args& a, const SSGeom&
   switch (g.kS) {
     case 1: return launch_fwd_bc<IT, 1, kMethod>(a, g, st);
     case 4: return launch_fwd_bc<IT, 4, kMethod>(a, g, st);
-    case 8: return launch_fwd_bc<IT, 8, kMethod>(a, g, st);
+    case 8:   // d_state 17..32: at most 4 waves, half the LDS (two workgroups per CU)
+      return g.nW <= 4 ? launch_fwd_bc<IT, 8, kMethod, 4>(a, g, st) : launch_fwd_bc<IT, 8, kMethod>(a, g, st);
     case 32: return launch_fwd_bc<IT, 32, kMethod>(a, g, st);
   }
   return hipErrorInvalidValue;

@@ -70,7 +70,7 @@ def test_mamba_fp32_var_const(dev, varB, varC):
     _run(dev, 2, 70, 96, 16, varB=varB, varC=varC)
 
 
-@pytest.mark.parametrize("N", [1, 3, 8, 16, 33, 64, 100, 128, 256])
+@pytest.mark.parametrize("N", [1, 3, 8, 16, 20, 32, 33, 64, 100, 128, 256])
 def test_mamba_fp32_dstate(dev, N):
     # N > 64 runs the 32-states-per-wave instantiation (the reference accepts
     # N <= 256; its LM tests use d_state 128)
@@ -691,3 +691,17 @@ def test_zoh_bilinear_binding_bwd_from_x(dev, monkeypatch, method, no_split):
         gk = g[i].squeeze(1) if k in ("B", "C") else g[i]
         close(f"d{k}", gk, rg[k], 1e-4, 1e-4 if k in ("A", "D", "delta_bias") else 1e-5)
     close("dz", g[7], rg["z"], 1e-4, 1e-5)
+
+
+# d_state 17..32: 8 states per wave in at most 4 waves, with LDS (and, for the
+# 16-bit forward, 16-step tiles) sized for 4 waves
+@pytest.mark.parametrize("case", [
+    ("mamba_bf16", dict(itype=torch.bfloat16)),
+    ("mamba_const_bc", dict(varB=False, varC=False)),
+    ("mamba_deltaA", dict(with_deltaA=True)),
+    ("zoh", dict(method="zoh")),
+    ("bilinear_groups", dict(method="bilinear", groups=2)),
+], ids=lambda c: c[0])
+@pytest.mark.parametrize("N", [24, 32])
+def test_dstate_17_to_32_four_waves(dev, case, N):
+    _run(dev, 2, 128, 300, N, seed=90 + N, **case[1])
