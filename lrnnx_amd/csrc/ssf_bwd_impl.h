@@ -4,9 +4,7 @@
 // / f16 I/O), "dirac", "zoh" and "bilinear" (f32 I/O; zoh and bilinear in
 // 32-channel workgroups, unsplit), variable B and C, d_state <= 16, 64
 // channels per group block, L a multiple of 16, 16-byte aligned rows; deltaA
-// (mamba) without softplus, as Mamba's event mode passes it (with softplus
-// the extra raw tile would take the LDS past the 80 KB of two workgroups per
-// CU; such calls run the general kernels, which read the same checkpoints).
+// (mamba), as Mamba's event mode passes it.
 // Gradients of the reference kernel
 // csrc/selective_scan/selective_scan_backward.cuh:86-845 for this method:
 //   dh_t  = A_bar_{t+1} dh_{t+1} + C_t dy_t      (dy = dout silu(z))
@@ -84,10 +82,10 @@ __device__ __forceinline__ float softplus20_sig(float x, float& sg) {
 // per CU.  The channel reductions lose their cross-half stage (the halves
 // hold different states), and the per-element phases take 2 elements per
 // thread.
-// kDA: deltaA given (mamba, no softplus).  The operand tile s_x then holds
-// deltaA (the step of A_bar) and the compute phases form delta' u from s_dl
-// and s_u; the raw deltaA tile takes the LDS that sigmoid(delta + bias) has
-// with softplus.
+// kDA: deltaA given (mamba).  The operand tile s_x then holds deltaA (the
+// step of A_bar) and the compute phases form delta' u from s_dl and s_u; the
+// raw deltaA tile takes the LDS that sigmoid(delta + bias) has with softplus
+// (the epilogue re-derives it from delta').
 // kM: the method (LRNNX_MAMBA, DIRAC, ZOH or BILINEAR), compile-time; zoh and
 // bilinear re-derive their input factor beta from A_bar in the reverse walk,
 // whose extra terms fit the registers of the 32-channel form only.
@@ -104,7 +102,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   constexpr bool kBeta = kM == LRNNX_ZOH || kM == LRNNX_BILINEAR;   // input factor per state
   static_assert(kM == LRNNX_MAMBA || kDi || kBeta, "method");
   static_assert(kM == LRNNX_MAMBA || sizeof(IT) == 4, "methods other than mamba take fp32 input only");
-  static_assert(!kDA || (!kSP && kM == LRNNX_MAMBA), "deltaA on the fast backward: mamba without softplus");
+  static_assert(!kDA || kM == LRNNX_MAMBA, "deltaA on the fast backward: mamba only");
   static_assert(!kBeta || kCh == kWave / 2, "zoh / bilinear: 32-channel workgroups");
   constexpr int kH = kWave / kCh;         // lane halves per wave
   constexpr int kS = 4 / kH;              // states per lane
@@ -135,7 +133,9 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
   __shared__ __attribute__((aligned(16))) float s_u[kOp];              // u (epilogue)
   __shared__ __attribute__((aligned(16))) float s_x[kOp];              // delta' u (compute phases; deltaA: deltaA)
   __shared__ __attribute__((aligned(16))) float s_dy[kOp];             // dout silu(z)
-  __shared__ __attribute__((aligned(16))) float s_sg[kSP ? kOp : 4];   // sigmoid(delta + bias)
+  // sigmoid(delta + bias); with deltaA the epilogue re-derives it as 1 - exp(-delta'), and its
+  // 4 KB hold the raw deltaA tile
+  __shared__ __attribute__((aligned(16))) float s_sg[kSP && !kDA ? kOp : 4];
   __shared__ __attribute__((aligned(16))) float s_B[kT * 16];          // [t][n]
   __shared__ __attribute__((aligned(16))) float s_C[kT * 16];
   __shared__ __attribute__((aligned(16))) float s_P1[kNP * kOp];       // [w, half][g][ch][4] sum_k dh B
@@ -297,7 +297,7 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     }
     lds_stv<kEt>(&s_dy[eo], dy);
     // read back by this thread only, in the epilogue
-    if constexpr (kSP) lds_stv<kEt>(&s_sg[eo], sg);
+    if constexpr (kSP && !kDA) lds_stv<kEt>(&s_sg[eo], sg);
     // B / C rows, transposed to step-major: threads [0, 64) B, [64, 128) C,
     // 4 steps of one state each; states >= N are zero
     if (tid < 2 * 16 * 4) {
@@ -332,7 +332,11 @@ ssf_bwd_kernel(const lrnnx_selective_scan_args a, const int64_t n_ck, float* __r
     lds_ldv<kEt>(&s_dl[eo], dl);
     lds_ldv<kEt>(&s_u[eo], uu);
     lds_ldv<kEt>(&s_dy[eo], dy);
-    if constexpr (kSP) lds_ldv<kEt>(&s_sg[eo], sg);
+    if constexpr (kSP && !kDA) lds_ldv<kEt>(&s_sg[eo], sg);
+    if constexpr (kSP && kDA) {
+#pragma unroll
+      for (int i = 0; i < kEt; ++i) sg[i] = one_minus_exp_neg(dl[i]);   // sigmoid(delta + bias)
+    }
     float du[kEt], dd[kEt], dda[kEt];
 #pragma unroll
     for (int i = 0; i < kEt; ++i) {
@@ -686,11 +690,10 @@ ssf_bwd_adj_chain_kernel(const lrnnx_selective_scan_args a, const int n_seg, flo
   }
 }
 
-// Shape / option coverage of the fast backward: the forward's, deltaA
-// without softplus only.
+// Shape / option coverage of the fast backward: the forward's.
 template <typename IT>
 inline bool ssf_bwd_shape_ok(const lrnnx_selective_scan_args& a) {
-  return ssf::shape_ok<IT>(a, ssf::kCk, false, !a.delta_softplus);
+  return ssf::shape_ok<IT>(a, ssf::kCk, false, true);
 }
 
 // Whether the fast backward covers this call.
@@ -805,9 +808,14 @@ inline hipError_t ssf_bwd_launch(const lrnnx_selective_scan_args& a, float* ws, 
     }
   };
   bool done = false;
-  if (a.deltaA.ptr) {   // mamba without softplus (ssf_bwd_shape_ok)
-    if (z) ssf_bwd_launch_t<IT, false, true, LRNNX_MAMBA, true>(a, g, ws, wo, ckp, steps, st);
-    else ssf_bwd_launch_t<IT, false, false, LRNNX_MAMBA, true>(a, g, ws, wo, ckp, steps, st);
+  if (a.deltaA.ptr) {   // mamba only (ssf_bwd_shape_ok)
+    if (a.delta_softplus) {
+      if (z) ssf_bwd_launch_t<IT, true, true, LRNNX_MAMBA, true>(a, g, ws, wo, ckp, steps, st);
+      else ssf_bwd_launch_t<IT, true, false, LRNNX_MAMBA, true>(a, g, ws, wo, ckp, steps, st);
+    } else {
+      if (z) ssf_bwd_launch_t<IT, false, true, LRNNX_MAMBA, true>(a, g, ws, wo, ckp, steps, st);
+      else ssf_bwd_launch_t<IT, false, false, LRNNX_MAMBA, true>(a, g, ws, wo, ckp, steps, st);
+    }
     done = true;
   } else if constexpr (sizeof(IT) == 4) {   // the other methods: fp32 input only (shape_ok)
     done = true;

@@ -444,8 +444,7 @@ def test_state_blocks_ragged_shapes(dev, itype):
 
 # deltaA (Mamba's event mode, lrnnx/models/ltv/mamba.py:303-330: delta without
 # softplus or bias, deltaA the step of A_bar) on the fast kernels, both
-# directions; with softplus the backward runs the general kernels from the
-# fast forward's checkpoints.
+# directions, with and without softplus.
 @pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("schedule", ["split", "unsplit64", "unsplit32"])
 def test_deltaA_fast_path_vs_oracle(dev, monkeypatch, itype, schedule):
@@ -525,11 +524,14 @@ def test_deltaA_fast_forward_matches_generic(dev, monkeypatch, itype):
 
 @pytest.mark.parametrize("itype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("with_z", [True, False])
-def test_deltaA_fast_path_matches_generic(dev, monkeypatch, itype, with_z):
-    """Event-mode fwd + bwd on the fast and on the general kernels: every
-    output and gradient, ddeltaA included (fp32 state; sums in another order)."""
+@pytest.mark.parametrize("softplus", [False, True])
+def test_deltaA_fast_path_matches_generic(dev, monkeypatch, itype, with_z, softplus):
+    """deltaA fwd + bwd on the fast and on the general kernels, without
+    softplus (event mode) and with it: every output and gradient, ddeltaA
+    included (fp32 state; sums in another order)."""
     inp = R.make_selective_inputs(2, 128, 512, 16, seed=77, itype=itype, has_bias=False, has_z=with_z)
-    inp["delta"] = (inp["delta"].float().abs() * 0.2 + 1e-3).to(itype)
+    if not softplus:
+        inp["delta"] = (inp["delta"].float().abs() * 0.2 + 1e-3).to(itype)
     g = torch.Generator().manual_seed(78)
     dA = (0.5 * torch.rand(2, 128, 512, generator=g)).to(itype)
     dout = torch.randn(2, 128, 512, generator=g).to(itype).to(dev)
@@ -541,7 +543,7 @@ def test_deltaA_fast_path_matches_generic(dev, monkeypatch, itype, with_z):
         z = d["z"].clone().requires_grad_(True) if with_z else None
         dA_dev = dA.to(dev).requires_grad_(True)
         out, last = selective_scan_fn(lv["u"], lv["delta"], lv["A"], lv["B"], lv["C"], lv["D"], z, None, dA_dev,
-                                      False, True, "mamba")
+                                      softplus, True, "mamba")
         out.backward(dout)
         torch.cuda.synchronize()
         res.append([out.detach().float(), last.detach()] + [lv[k].grad.float() for k in lv] +
