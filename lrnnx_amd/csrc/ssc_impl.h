@@ -115,6 +115,19 @@ __device__ __forceinline__ void cdisc(float dtA, float dl, cf A, cf& Ab, cf& bet
   }
 }
 
+// The input term beta u B_in of one (t, n) (B_in = 1 for a constant B, which
+// the output weight carries).  Mamba and dirac have a real beta (delta', 1):
+// the real factor delta' u or u scales B_in, two multiplies.
+template <int kMethod, bool kVarB>
+__device__ __forceinline__ cf in_term(cf beta, cf bv, float dl, float uu) {
+  if constexpr (kMethod == LRNNX_MAMBA || kMethod == LRNNX_DIRAC) {
+    const float xr = kMethod == LRNNX_MAMBA ? dl * uu : uu;
+    return kVarB ? cscale(bv, xr) : cmk(xr, 0.f);
+  } else {
+    return cmul(beta, kVarB ? cscale(bv, uu) : cmk(uu, 0.f));
+  }
+}
+
 
 struct SSCPtrs {
   int64_t b, d0;
@@ -234,12 +247,16 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_fwd_kernel(const lrnn
       for (int k = 0; k < kS; ++k) {
         cf Ab, beta;
         cdisc<kMethod>(dt, dl, Av[k], Ab, beta);
-        cf bin = cmk(uu, 0.f);
-        if constexpr (kVarB) bin = cscale(cmk(s_B[(s * NP + n0 + k) * 2], s_B[(s * NP + n0 + k) * 2 + 1]), uu);
-        h[k] = cfma(Ab, h[k], cmul(beta, bin));
+        const cf bv = kVarB ? cmk(s_B[(s * NP + n0 + k) * 2], s_B[(s * NP + n0 + k) * 2 + 1]) : cmk(1.f, 0.f);
+        h[k] = cfma(Ab, h[k], in_term<kMethod, kVarB>(beta, bv, dl, uu));
         if constexpr (kMethod == LRNNX_BILINEAR) pa[k] = cmul(pa[k], Ab);
+        // variable B and C: the output weight is C itself (cout_c is 1 on every
+        // lane that stores; padded states have C = 0)
         cf cc = cout_c[k];
-        if constexpr (kVarC) cc = cmul(cmk(s_C[(s * NP + n0 + k) * 2], s_C[(s * NP + n0 + k) * 2 + 1]), cc);
+        if constexpr (kVarC) {
+          const cf cv = cmk(s_C[(s * NP + n0 + k) * 2], s_C[(s * NP + n0 + k) * 2 + 1]);
+          cc = kVarB ? cv : cmul(cv, cc);
+        }
         y += cc.r * h[k].r - cc.i * h[k].i;
       }
       if constexpr (kMethod != LRNNX_BILINEAR) sumdt += dt;
@@ -435,9 +452,8 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
             for (int k = 0; k < kS; ++k) {
               cf ab, beta;
               cdisc<kMethod>(dt, dl, Av[k], ab, beta);
-              cf bin = cmk(uu, 0.f);
-              if constexpr (kVarB) bin = cscale(cmk(s_B[(t * NP + n0 + k) * 2], s_B[(t * NP + n0 + k) * 2 + 1]), uu);
-              hc[k] = cfma(ab, hc[k], cmul(beta, bin));
+              const cf bv = kVarB ? cmk(s_B[(t * NP + n0 + k) * 2], s_B[(t * NP + n0 + k) * 2 + 1]) : cmk(1.f, 0.f);
+              hc[k] = cfma(ab, hc[k], in_term<kMethod, kVarB>(beta, bv, dl, uu));
               Ab[j][k] = ab;
               H[j][k] = hc[k];
             }
@@ -453,18 +469,19 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
           const int t = ts + j;
           const float dl = s_dl[t * kPad + lane], uu = s_u[t * kPad + lane];
           const float dt = kDA ? s_dt[t * kPad + lane] : dl;
-          const float dy = s_dy[t * kPad + lane];
+          const float dy = s_dy[t * kPad + lane], dy2 = 2.f * dy;
           float p1 = 0.f, p2 = 0.f, p3 = 0.f;
 #pragma unroll
           for (int k = 0; k < kS; ++k) {
+            // C_eff = C_var C_const; variable B and C: C itself (as the forward)
             cf cvar = cmk(1.f, 0.f), cc = cout_c[k], bvar = cmk(1.f, 0.f);
             if constexpr (kVarC) {
               cvar = cmk(s_C[(t * NP + n0 + k) * 2], s_C[(t * NP + n0 + k) * 2 + 1]);
-              cc = cmul(cvar, cout_c[k]);
+              cc = kVarB ? cvar : cmul(cvar, cout_c[k]);
             }
             if constexpr (kVarB) bvar = cmk(s_B[(t * NP + n0 + k) * 2], s_B[(t * NP + n0 + k) * 2 + 1]);
             // dh_t = conj(A_bar_{t+1}) dh_{t+1} + 2 dy conj(C_eff)
-            const cf dh = cadd(gn[k], cscale(cconj(cc), 2.f * dy));
+            const cf dh = cadd(gn[k], cscale(cconj(cc), dy2));
             const cf ab = Ab[j][k];
             const cf hp = j > 0 ? H[j - 1][k] : h0[k];
             const cf hcur = H[j][k];
@@ -478,9 +495,14 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
               dA_acc[k] = cadd(dA_acc[k], cmul(cconj(cscale(inv2, dt)), g));
               p2 += cdotr(g, cmul(Av[k], inv2));
             } else {
+              // A_bar h_{t-1} as a product (exactly 0 when h_{t-1} = 0, unlike
+              // h_t minus the input term, which the compiler fuses into one FMA)
               const cf abhp = cmul(ab, hp);
-              dA_acc[k] = cadd(dA_acc[k], cscale(cmul(cconj(abhp), dh), dt));
-              p2 += cdotr(dh, cmul(Av[k], abhp));
+              // w = conj(A_bar h_{t-1}) dh: dA += dt w, and
+              // Re(conj(dh) A A_bar h_{t-1}) = Re(A conj(w)) = A.r w.r + A.i w.i
+              const cf wv = cmul(cconj(abhp), dh);
+              dA_acc[k] = cadd(dA_acc[k], cscale(wv, dt));
+              p2 += fmaf(Av[k].r, wv.r, Av[k].i * wv.i);
             }
             // through the input term beta u B_in
             if constexpr (kMethod == LRNNX_MAMBA || kMethod == LRNNX_DIRAC) {
@@ -514,7 +536,7 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
               v[(k * kCk + j) * 2 + 1] = gB.i;
             }
             // output side y = 2 Re(C_eff h): dL/dC_eff = 2 dy conj(h)
-            const cf gCe = cscale(cconj(hcur), 2.f * dy);
+            const cf gCe = cscale(cconj(hcur), dy2);
             if constexpr (kVarC) {
               const cf gC = kVarB ? gCe : cmul(cconj(bcst[k]), gCe);
               v[32 + (k * kCk + j) * 2] = gC.r;
