@@ -72,6 +72,16 @@ constexpr int kPad = kWave + 1; // LDS row pitch of [kTc][64] tiles (conflict-fr
 
 __host__ __device__ constexpr int ck_c(int kS) { return 16 / kS; }  // kS * kCk = 16 complex values
 
+constexpr int kMinW = 4;  // fewest waves per workgroup
+// Up to 2 states per wave the next tile's values (and in the backward the
+// next interval's checkpoint) load while the current one computes; above,
+// whose state arrays fill the VGPRs, a tile's values load in one batch
+// right before it is staged (no registers held across the state steps).
+__host__ __device__ constexpr bool pf_ahead(int kS) { return kS <= 2; }
+// a thread's share of one tile: [64][kTc] sequence values, [NP][kTc] complex B or C
+__host__ __device__ constexpr int pf_seq_n(int kS) { return kWave * tile_c(kS) / (kMinW * kWave); }
+__host__ __device__ constexpr int pf_bc_n(int kS) { return kS * tile_c(kS) / 32 > 1 ? kS * tile_c(kS) / 32 : 1; }
+
 // states per wave: up to 8 waves per workgroup below N = 16, so that a grid
 // of B * D / 64 workgroups still gives the SIMDs more than one wave each
 inline int pick_kS_c(int64_t N) { return N <= 8 ? 1 : (N <= 16 ? 2 : (N <= 32 ? 4 : (N <= 64 ? 8 : 16))); }
@@ -93,7 +103,10 @@ inline SSCGeom ssc_geom(const lrnnx_selective_scan_args& a) {
   }
   g.n_cb = (int)((a.dim + g.CB - 1) / g.CB);
   g.kS = pick_kS_c(a.dstate);
-  g.nW = (int)((a.dstate + g.kS - 1) / g.kS);
+  // at least kMinW waves (waves past the last state carry zero B and C), so
+  // that a thread's share of a tile is at most kTc / 4 sequence values
+  const int nw = (int)((a.dstate + g.kS - 1) / g.kS);
+  g.nW = nw > kMinW ? nw : kMinW;
   g.ck = ck_c(g.kS);
   g.n_ck = (a.seqlen + g.ck - 1) / g.ck;
   return g;
@@ -129,34 +142,51 @@ __device__ __forceinline__ cf in_term(cf beta, cf bv, float dl, float uu) {
 }
 
 
-struct SSCPtrs {
-  int64_t b, d0;
-  int rows, NP;
-};
-
-// Stage one tile of (b, d0 .. d0 + 63, t0 .. t0 + kTc) sequence values in LDS
-// ([kTc][kPad], zero outside the valid rows / steps).
-template <int kTc, typename F>
-__device__ __forceinline__ void load_tile(const float* __restrict__ base, int64_t row_stride, int rows, int nt,
-                                          float* dst, int tid, int nth, F&& f) {
-  for (int j = tid; j < kWave * kTc; j += nth) {
-    const int r = j / kTc, t = j % kTc;
-    float v = 0.f;
-    if (r < rows && t < nt) v = f(base[r * row_stride + t], r);
-    dst[t * kPad + r] = v;
-  }
+// x, opaque to the optimiser: per-element offsets derived from it are
+// recomputed in each tile's phase instead of being hoisted out of the tile
+// loop and held in VGPRs across the state steps
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
 }
 
-// Variable complex B or C rows of the group: s[t][n] (re, im), zero for padded states.
-template <int kTc>
-__device__ __forceinline__ void load_bc(const float* __restrict__ base, int64_t s_n, int N, int NP, int nt,
-                                        float* dst, int tid, int nth) {
-  for (int j = tid; j < NP * kTc * 2; j += nth) {
-    const int n = j / (kTc * 2), e = j % (kTc * 2);
-    const int t = e / 2;
-    float v = 0.f;
-    if (n < N && t < nt) v = base[n * s_n + e];
-    dst[(t * NP + n) * 2 + (e & 1)] = v;
+// Register staging of a tile, issued one tile ahead of its use: thread tid
+// holds elements j = tid + i * nth of the row-major [64][kTc] tile (row r =
+// j / kTc, step t = j % kTc; the same rows in every tile), zero outside the
+// valid rows / steps; pf_put writes them to the [kTc][kPad] LDS tile.
+template <int kTc, int kP>
+__device__ __forceinline__ void pf_get(const float* __restrict__ base, int64_t row_stride, int rows, int nt, int tid,
+                                       int nth, float (&v)[kP]) {
+#pragma unroll
+  for (int i = 0; i < kP; ++i) {
+    const int j = tid + i * nth, r = j / kTc, t = j % kTc;
+    v[i] = (j < kWave * kTc && r < rows && t < nt) ? base[r * row_stride + t] : 0.f;
+  }
+}
+template <int kTc, int kP>
+__device__ __forceinline__ void pf_put(const float (&v)[kP], float* dst, int tid, int nth) {
+#pragma unroll
+  for (int i = 0; i < kP; ++i) {
+    const int j = tid + i * nth;
+    if (j < kWave * kTc) dst[(j % kTc) * kPad + j / kTc] = v[i];
+  }
+}
+// variable B or C rows: element j of the [NP][kTc][2] tile (zero for padded states)
+template <int kTc, int kP>
+__device__ __forceinline__ void pf_get_bc(const float* __restrict__ base, int64_t s_n, int N, int NP, int nt, int tid,
+                                          int nth, float (&v)[kP]) {
+#pragma unroll
+  for (int i = 0; i < kP; ++i) {
+    const int j = tid + i * nth, n = j / (kTc * 2), e = j % (kTc * 2);
+    v[i] = (j < NP * kTc * 2 && n < N && e / 2 < nt) ? base[n * s_n + e] : 0.f;
+  }
+}
+template <int kTc, int kP>
+__device__ __forceinline__ void pf_put_bc(const float (&v)[kP], float* dst, int NP, int tid, int nth) {
+#pragma unroll
+  for (int i = 0; i < kP; ++i) {
+    const int j = tid + i * nth, n = j / (kTc * 2), e = j % (kTc * 2);
+    if (j < NP * kTc * 2) dst[((e / 2) * NP + n) * 2 + (e & 1)] = v[i];
   }
 }
 
@@ -225,18 +255,57 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_fwd_kernel(const lrnn
   float* xp = static_cast<float*>(a.x);
   const int64_t n_xc = (L + kXChunk - 1) / kXChunk;
 
+  // the next tile's values in registers (pf_get), issued after the current
+  // tile's steps; per-row constants of this thread's staged elements
+  constexpr int kPS = pf_seq_n(kS), kPB = pf_bc_n(kS);
+  const int nth = blockDim.x;
+  // (held for the whole kernel with the look-ahead, else loaded in the phase that uses them)
+  float e_bias[kPS], e_D[kPS];
+  auto ld_rowc = [&](float (&o)[kPS], const float* p, int64_t st) __attribute__((always_inline)) {
+    const int tq = opaque(tid);
+#pragma unroll
+    for (int i = 0; i < kPS; ++i) {
+      const int j = tq + i * nth, r = j / kTc;
+      o[i] = (j < kWave * kTc && r < rows && p) ? p[(d0 + r) * st] : 0.f;
+    }
+  };
+  if constexpr (pf_ahead(kS)) {
+    ld_rowc(e_bias, bias, a.delta_bias.s0);
+    ld_rowc(e_D, Dp, a.D.s0);
+  }
+  float p_dl[kPS], p_u[kPS], p_da[kDA ? kPS : 1], p_z[kPS], p_B[kPB], p_C[kPB];
+  auto fetch = [&](int64_t t0, int nt) __attribute__((always_inline)) {
+    const int tq = opaque(tid);
+    if constexpr (!pf_ahead(kS)) ld_rowc(e_bias, bias, a.delta_bias.s0);
+    pf_get<kTc>(gd + t0, a.delta.s1, rows, nt, tq, nth, p_dl);
+    pf_get<kTc>(gu + t0, a.u.s1, rows, nt, tq, nth, p_u);
+    if constexpr (kDA) pf_get<kTc>(gdA + t0, a.deltaA.s1, rows, nt, tq, nth, p_da);
+    if (has_z) pf_get<kTc>(gz + t0, a.z.s1, rows, nt, tq, nth, p_z);
+    if constexpr (kVarB) pf_get_bc<kTc>(gB + 2 * t0, a.B.s2, N, NP, nt, tq, nth, p_B);
+    if constexpr (kVarC) pf_get_bc<kTc>(gC + 2 * t0, a.C.s2, N, NP, nt, tq, nth, p_C);
+  };
+  if constexpr (pf_ahead(kS)) fetch(0, (int)(L < kTc ? L : kTc));
+
   for (int64_t t0 = 0; t0 < L; t0 += kTc) {
     const int nt = (int)((L - t0) < kTc ? (L - t0) : kTc);
     __syncthreads();
-    load_tile<kTc>(gd + t0, a.delta.s1, rows, nt, s_dl, tid, blockDim.x, [&](float x, int r) {
-      x += bias ? bias[(d0 + r) * a.delta_bias.s0] : 0.f;
-      return a.delta_softplus ? softplus_fast(x) : x;
-    });
-    load_tile<kTc>(gu + t0, a.u.s1, rows, nt, s_u, tid, blockDim.x, [](float x, int) { return x; });
-    if constexpr (kDA) load_tile<kTc>(gdA + t0, a.deltaA.s1, rows, nt, s_dt, tid, blockDim.x, [](float x, int) { return x; });
-    if (has_z) load_tile<kTc>(gz + t0, a.z.s1, rows, nt, s_z, tid, blockDim.x, [](float x, int) { return x; });
-    if constexpr (kVarB) load_bc<kTc>(gB + 2 * t0, a.B.s2, N, NP, nt, s_B, tid, blockDim.x);
-    if constexpr (kVarC) load_bc<kTc>(gC + 2 * t0, a.C.s2, N, NP, nt, s_C, tid, blockDim.x);
+    if constexpr (!pf_ahead(kS)) fetch(t0, nt);
+    // delta' = softplus(delta + bias), zero outside the valid rows / steps
+    const int tq = opaque(tid);
+#pragma unroll
+    for (int i = 0; i < kPS; ++i) {
+      const int j = tq + i * nth, r = j / kTc, t = j % kTc;
+      if (j < kWave * kTc) {
+        float x = p_dl[i] + e_bias[i];
+        if (a.delta_softplus) x = softplus_fast(x);
+        s_dl[t * kPad + r] = (r < rows && t < nt) ? x : 0.f;
+      }
+    }
+    pf_put<kTc>(p_u, s_u, tq, nth);
+    if constexpr (kDA) pf_put<kTc>(p_da, s_dt, tq, nth);
+    if (has_z) pf_put<kTc>(p_z, s_z, tq, nth);
+    if constexpr (kVarB) pf_put_bc<kTc>(p_B, s_B, NP, tq, nth);
+    if constexpr (kVarC) pf_put_bc<kTc>(p_C, s_C, NP, tq, nth);
     __syncthreads();
 
     for (int s = 0; s < nt; ++s) {
@@ -287,13 +356,19 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_fwd_kernel(const lrnn
           }
       }
     }
+    // the next tile's values: in flight during the per-element phase
+    if constexpr (pf_ahead(kS))
+      if (t0 + kTc < L) fetch(t0 + kTc, (int)((L - t0 - kTc) < kTc ? (L - t0 - kTc) : kTc));
     __syncthreads();
-    for (int j = tid; j < kWave * kTc; j += blockDim.x) {
-      const int r = j / kTc, t = j % kTc;
-      if (r >= rows || t >= nt) continue;
+    if constexpr (!pf_ahead(kS)) ld_rowc(e_D, Dp, a.D.s0);
+    const int tq2 = opaque(tid);
+#pragma unroll
+    for (int i = 0; i < kPS; ++i) {
+      const int j = tq2 + i * nth, r = j / kTc, t = j % kTc;
+      if (j >= kWave * kTc || r >= rows || t >= nt) continue;
       float y = 0.f;
       for (int ww = 0; ww < nW; ++ww) y += s_Y[(ww * kTc + t) * kPad + r];
-      if (Dp) y = fmaf(Dp[(d0 + r) * a.D.s0], s_u[t * kPad + r], y);
+      if (Dp) y = fmaf(e_D[i], s_u[t * kPad + r], y);
       if (go) go[r * a.out.s1 + t0 + t] = y;
       if (has_z && goz) {
         const float zz = s_z[t * kPad + r];
@@ -394,34 +469,90 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
   }
   float dD_acc = 0.f, dbias_acc = 0.f;
 
+  // the next tile's values in registers (pf_get), issued after the current
+  // tile's intervals; per-row constants of this thread's staged elements
+  constexpr int kPS = pf_seq_n(kS), kPB = pf_bc_n(kS);
+  const int nth = blockDim.x;
+  // (held for the whole kernel with the look-ahead, else loaded in the phase that uses them)
+  float e_bias[kPS], e_D[kPS];
+  auto ld_rowc = [&](float (&o)[kPS], const float* p, int64_t st) __attribute__((always_inline)) {
+    const int tq = opaque(tid);
+#pragma unroll
+    for (int i = 0; i < kPS; ++i) {
+      const int j = tq + i * nth, r = j / kTc;
+      o[i] = (j < kWave * kTc && r < rows && p) ? p[(d0 + r) * st] : 0.f;
+    }
+  };
+  if constexpr (pf_ahead(kS)) {
+    ld_rowc(e_bias, bias, a.delta_bias.s0);
+    ld_rowc(e_D, Dp, a.D.s0);
+  }
+  float p_dl[kPS], p_u[kPS], p_da[kDA ? kPS : 1], p_do[kPS], p_z[kPS], p_os[kPS], p_B[kPB], p_C[kPB];
+  auto fetch = [&](int64_t t0, int nt) __attribute__((always_inline)) {
+    const int tq = opaque(tid);
+    if constexpr (!pf_ahead(kS)) ld_rowc(e_bias, bias, a.delta_bias.s0);
+    pf_get<kTc>(gd + t0, a.delta.s1, rows, nt, tq, nth, p_dl);
+    pf_get<kTc>(gu + t0, a.u.s1, rows, nt, tq, nth, p_u);
+    if constexpr (kDA) pf_get<kTc>(gdA + t0, a.deltaA.s1, rows, nt, tq, nth, p_da);
+    pf_get<kTc>(gdo + t0, a.dout.s1, rows, nt, tq, nth, p_do);
+    if (has_z) {
+      pf_get<kTc>(gz + t0, a.z.s1, rows, nt, tq, nth, p_z);
+      pf_get<kTc>(gos + t0, a.out_saved.s1, rows, nt, tq, nth, p_os);
+    }
+    if constexpr (kVarB) pf_get_bc<kTc>(gB + 2 * t0, a.B.s2, N, NP, nt, tq, nth, p_B);
+    if constexpr (kVarC) pf_get_bc<kTc>(gC + 2 * t0, a.C.s2, N, NP, nt, tq, nth, p_C);
+  };
+  // the state at the start of interval kk (checkpoint kk - 1), loaded one
+  // interval ahead of its use (intervals run in decreasing order)
+  auto ld_ck = [&](int64_t kk, cf (&o)[kS]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < kS; ++k) {
+      o[k] = cmk(0.f, 0.f);
+      if (kk > 0 && lane_ok && n0 + k < N) {
+        const float* p = ckp + (((b * n_ck + kk - 1) * N + n0 + k) * D + d) * 2;
+        o[k] = cmk(p[0], p[1]);
+      }
+    }
+  };
+
   const int64_t n_tiles = (L + kTc - 1) / kTc;
+  cf h0n[pf_ahead(kS) ? kS : 1];
+  if constexpr (pf_ahead(kS)) {
+    if (n_tiles > 0) {
+      ld_ck((L - 1) / kCk, h0n);
+      fetch((n_tiles - 1) * kTc, (int)(L - (n_tiles - 1) * kTc));
+    }
+  }
   for (int64_t tile = n_tiles - 1; tile >= 0; --tile) {
     const int64_t t0 = tile * kTc;
     const int nt = (int)((L - t0) < kTc ? (L - t0) : kTc);
     __syncthreads();
-    load_tile<kTc>(gd + t0, a.delta.s1, rows, nt, s_dl, tid, blockDim.x, [&](float x, int r) {
-      x += bias ? bias[(d0 + r) * a.delta_bias.s0] : 0.f;
-      return a.delta_softplus ? softplus_fast(x) : x;
-    });
-    load_tile<kTc>(gu + t0, a.u.s1, rows, nt, s_u, tid, blockDim.x, [](float x, int) { return x; });
-    if constexpr (kDA) load_tile<kTc>(gdA + t0, a.deltaA.s1, rows, nt, s_dt, tid, blockDim.x, [](float x, int) { return x; });
-    // dy = dout * silu(z); dz = dout * out * sigma(z) (1 + z (1 - sigma(z))) (selective_scan_backward.cuh:218-219)
-    for (int j = tid; j < kWave * kTc; j += blockDim.x) {
-      const int r = j / kTc, t = j % kTc;
-      float dy = 0.f;
-      if (r < rows && t < nt) {
-        dy = gdo[r * a.dout.s1 + t0 + t];
-        if (has_z) {
-          const float zz = gz[r * a.z.s1 + t0 + t];
+    if constexpr (!pf_ahead(kS)) fetch(t0, nt);
+    // delta' = softplus(delta + bias); dy = dout * silu(z);
+    // dz = dout * out * sigma(z) (1 + z (1 - sigma(z))) (selective_scan_backward.cuh:218-219)
+    const int tq = opaque(tid);
+#pragma unroll
+    for (int i = 0; i < kPS; ++i) {
+      const int j = tq + i * nth, r = j / kTc, t = j % kTc;
+      if (j < kWave * kTc) {
+        const bool ok = r < rows && t < nt;
+        float x = p_dl[i] + e_bias[i];
+        if (a.delta_softplus) x = softplus_fast(x);
+        s_dl[t * kPad + r] = ok ? x : 0.f;
+        float dy = p_do[i];
+        if (has_z && ok) {
+          const float zz = p_z[i];
           const float sg = sigmoid_fast(zz);
-          gdz[r * a.dz.s1 + t0 + t] = dy * gos[r * a.out_saved.s1 + t0 + t] * sg * (1.f + zz * (1.f - sg));
+          gdz[r * a.dz.s1 + t0 + t] = dy * p_os[i] * sg * (1.f + zz * (1.f - sg));
           dy *= zz * sg;
         }
+        s_dy[t * kPad + r] = dy;
       }
-      s_dy[t * kPad + r] = dy;
     }
-    if constexpr (kVarB) load_bc<kTc>(gB + 2 * t0, a.B.s2, N, NP, nt, s_B, tid, blockDim.x);
-    if constexpr (kVarC) load_bc<kTc>(gC + 2 * t0, a.C.s2, N, NP, nt, s_C, tid, blockDim.x);
+    pf_put<kTc>(p_u, s_u, tq, nth);
+    if constexpr (kDA) pf_put<kTc>(p_da, s_dt, tq, nth);
+    if constexpr (kVarB) pf_put_bc<kTc>(p_B, s_B, NP, tq, nth);
+    if constexpr (kVarC) pf_put_bc<kTc>(p_C, s_C, NP, tq, nth);
     __syncthreads();
 
     for (int s = (nt + kCk - 1) / kCk - 1; s >= 0; --s) {
@@ -429,13 +560,12 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
       const int Ls = (nt - ts) < kCk ? (nt - ts) : kCk;
       const int64_t kk = (t0 + ts) / kCk;
       cf h0[kS];
+      if constexpr (pf_ahead(kS)) {
 #pragma unroll
-      for (int k = 0; k < kS; ++k) {
-        h0[k] = cmk(0.f, 0.f);
-        if (kk > 0 && lane_ok && n0 + k < N) {
-          const float* p = ckp + (((b * n_ck + kk - 1) * N + n0 + k) * D + d) * 2;
-          h0[k] = cmk(p[0], p[1]);
-        }
+        for (int k = 0; k < kS; ++k) h0[k] = h0n[k];
+        ld_ck(kk - 1, h0n);
+      } else {
+        ld_ck(kk, h0);
       }
       cf Ab[kCk][kS], H[kCk][kS];
       {
@@ -563,11 +693,17 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
         }
       }
     }
+    // the next tile's values: in flight during the epilogue
+    if constexpr (pf_ahead(kS))
+      if (tile > 0) fetch(t0 - kTc, kTc);
     __syncthreads();
     // epilogue: du, ddelta, ddeltaA; dD / ddelta_bias terms
-    for (int j = tid; j < kWave * kTc; j += blockDim.x) {
-      const int r = j / kTc, t = j % kTc;
-      if (r >= rows || t >= nt) continue;
+    if constexpr (!pf_ahead(kS)) ld_rowc(e_D, Dp, a.D.s0);
+    const int tq2 = opaque(tid);
+#pragma unroll
+    for (int i = 0; i < kPS; ++i) {
+      const int j = tq2 + i * nth, r = j / kTc, t = j % kTc;
+      if (j >= kWave * kTc || r >= rows || t >= nt) continue;
       float P1 = 0.f, P2 = 0.f, P3 = 0.f;
       for (int ww = 0; ww < nW; ++ww) {
         P1 += s_P1[(ww * kTc + t) * kPad + r];
@@ -575,7 +711,7 @@ __global__ void __launch_bounds__(ssc_max_threads(kS)) ssc_bwd_kernel(const lrnn
         if constexpr (kP3) P3 += s_P3[(ww * kTc + t) * kPad + r];
       }
       const float dl = s_dl[t * kPad + r], uu = s_u[t * kPad + r], dy = s_dy[t * kPad + r];
-      const float Dv = Dp ? Dp[(d0 + r) * a.D.s0] : 0.f;
+      const float Dv = e_D[i];
       float du, ddl;
       if constexpr (kMethod == LRNNX_MAMBA) {
         du = fmaf(dl, P1, Dv * dy);
