@@ -71,7 +71,6 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   __shared__ __attribute__((aligned(16))) float s_Y[kNWmax * kWave * kT];         // [nW][kG][64][4]
   __shared__ __attribute__((aligned(16))) char s_raw_dA[kDA ? kRawArr : 16];    // deltaA (consumed by the conversion)
   __shared__ __attribute__((aligned(16))) float s_dt[kDA ? kWave * kT : 4];      // [kG][64][4] deltaA
-  __shared__ float s_Dv[kWave], s_bias[kWave];  // D and delta_bias of the block's channels
 
   const int nW = blockDim.x / kWave;
   const int tid = threadIdx.x;
@@ -132,6 +131,11 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
       prodA[k] = 1.f;
     }
   }
+  // D and delta_bias of channel `lane` in a VGPR; the per-element phases take
+  // their row's value with a cross-lane read (ds_bpermute: no LDS allocated,
+  // which keeps the 4-wave d_state 17..32 forward at two workgroups per CU)
+  const float lane_D = (has_D && lane_ok) ? static_cast<const float*>(a.D.ptr)[d * a.D.s0] : 0.f;
+  const float lane_bias = (has_bias && lane_ok) ? static_cast<const float*>(a.delta_bias.ptr)[d * a.delta_bias.s0] : 0.f;
   float sumdt = 0.f;  // running sum of the A step (exp-family chunk products)
   float* ckp = static_cast<float*>(a.ckpt);
   float* xp = static_cast<float*>(a.x);
@@ -190,7 +194,7 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
       float vu[kEl], vd[kEl];
       raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_u[buf] + 16 * j), vu);
       raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_d + 16 * j), vd);
-      const float bias = s_bias[r];
+      const float bias = __shfl(lane_bias, r);
       float vdt[kEl];
       if constexpr (kDA) raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_dA + 16 * j), vdt);
 #pragma unroll
@@ -240,6 +244,7 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
     const int nt = (int)((L - t0) < kT ? (L - t0) : kT);
     for (int j = tid; j < kWave * kQ; j += blockDim.x) {
       const int r = j / kQ, q = j % kQ;
+      const float Dv = __shfl(lane_D, r);   // before the divergent exits: every lane of the wave
       if (!kFull && r >= rows) continue;
       if (gyp) {  // state block: its partial y, fp32 (D u and the gate come in the combine)
         float y[kEl];
@@ -263,7 +268,6 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
         }
         continue;
       }
-      const float Dv = s_Dv[r];
       float vu[kEl], y[kEl];
       raw_to_f32<IT>(*reinterpret_cast<const uint4*>(s_raw_u[buf] + 16 * j), vu);
 #pragma unroll
@@ -341,11 +345,6 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
   };
 
   // ---- prologue: per-channel constants, tile 0
-  if (tid < kWave) {
-    s_Dv[tid] = (has_D && tid < rows) ? static_cast<const float*>(a.D.ptr)[(d0 + tid) * a.D.s0] : 0.f;
-    s_bias[tid] = (has_bias && tid < rows) ? static_cast<const float*>(a.delta_bias.ptr)[(d0 + tid) * a.delta_bias.s0]
-                                           : 0.f;
-  }
   if (async_tile(0)) fetch_async(0, 0);
   else fetch_sync(0, 0);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
@@ -515,7 +514,7 @@ static hipError_t launch_fwd_s(const lrnnx_selective_scan_args& a, const SSGeom&
   switch (g.kS) {
     case 1: return launch_fwd_bc<IT, 1, kMethod>(a, g, st);
     case 4: return launch_fwd_bc<IT, 4, kMethod>(a, g, st);
-    case 8:   // d_state 17..32: at most 4 waves, half the LDS (two workgroups per CU)
+    case 8:   // d_state 17..32: at most 4 waves, 80 KB of LDS without deltaA (two workgroups per CU)
       return g.nW <= 4 ? launch_fwd_bc<IT, 8, kMethod, 4>(a, g, st) : launch_fwd_bc<IT, 8, kMethod>(a, g, st);
     case 32: return launch_fwd_bc<IT, 32, kMethod>(a, g, st);
   }
