@@ -321,11 +321,23 @@ ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_c
     return y;
   };
 
+  // this lane's real states (0 past the last channel): one per-lane bound
+  // instead of a predicate per state, and one row address per checkpoint
+  // (the lane's states are D apart), keep the stores' index math out of SGPRs
+  const int n_real = lane_ok ? (Nb - n0 < kS ? Nb - n0 : kS) : 0;
   auto store_ckpt = [&](int64_t tg) __attribute__((always_inline)) {  // state after step tg
-    const int64_t kk = tg / kCk;
+    float* p = ckp + ((b * n_ck + tg / kCk) * N + nb + n0) * D + d;
+    // bound and stride opaque here: compared and stepped at each store, not
+    // hoisted out of the tile loop as per-state masks and offsets (SGPRs the
+    // loop cannot keep: they spill to VGPR lanes)
+    int nr = n_real;
+    int64_t ds = D;
+    asm volatile("" : "+v"(nr), "+s"(ds));
 #pragma unroll
-    for (int k = 0; k < kS; ++k)
-      if (lane_ok && n0 + k < Nb) ckp[((b * n_ck + kk) * N + nb + n0 + k) * D + d] = h[k];
+    for (int k = 0; k < kS; ++k) {
+      if (k < nr) *p = h[k];
+      p += ds;
+    }
   };
   auto store_x = [&](int64_t tg) __attribute__((always_inline)) {  // reference chunk carry at step tg
     const int64_t c = tg / kXChunk;
