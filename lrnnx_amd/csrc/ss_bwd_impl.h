@@ -127,7 +127,10 @@ __global__ void __launch_bounds__(512)
 ss_bwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_ck, float* __restrict__ ws,
               const SSBwdWs wo, const float* __restrict__ ckp, const int flags, const int nsb) {
   constexpr int kCk = ck_for(kS);
-  constexpr int kTB = (kS >= 8 && (kNWm > 4 || sizeof(IT) == 4)) ? 8 : 16;   // steps per tile: 16 for the 4-wave d_state 17..32 form with 16-bit I/O (fits 80 KB; fp32 tiles would not)
+  // steps per tile: 16, or 8 at 8 states per wave with fp32 I/O where 16 would not fit: two
+  // 4-wave workgroups per CU need 80 KB, and one 8-wave workgroup of zoh / bilinear (their
+  // third partial sum) more than 160 KB
+  constexpr int kTB = (kS >= 8 && sizeof(IT) == 4 && (kNWm <= 4 || needs_p3_m(kMethod))) ? 8 : 16;
   constexpr int kEl = 16 / sizeof(IT);  // elements per 16-byte block
   constexpr int kQ = kTB / kEl;         // 16-byte blocks per raw row
   constexpr int kG = kTB / 4;           // groups of 4 steps

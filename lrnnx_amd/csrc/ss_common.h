@@ -22,9 +22,8 @@ namespace lrnnx {
 // the forward's fallback for d_state > 64 without a workspace (ss_geom); it
 // writes the interval of the state-block backward (kS = 8) that reads them.
 __host__ __device__ constexpr int ck_for(int kS) { return kS == 1 ? 16 : (kS == 32 ? 8 : 64 / kS); }
-// backward tile length along L (a whole number of checkpoint intervals) and
 // forward tile length, sized so that every instantiation fits 160 KB of LDS
-__host__ __device__ constexpr int tb_for(int kS) { return kS >= 8 ? 8 : 16; }
+// (the backward's, a whole number of checkpoint intervals, is set in ss_bwd_kernel)
 __host__ __device__ constexpr int tf_for(int kS) { return kS >= 32 ? 16 : 32; }
 constexpr size_t kMaxLds = 160 * 1024;
 
