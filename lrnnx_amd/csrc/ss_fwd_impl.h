@@ -48,7 +48,9 @@ __global__ void __launch_bounds__(512)
 ss_fwd_kernel(const lrnnx_selective_scan_args a, const int CB, const int64_t n_ck, const int flags,
               float* __restrict__ ypart) {
   constexpr int kCk = ck_for(kS);
-  constexpr int kT = fwd_tile<IT, kS>();
+  // fp32 8-wave workgroups (one per CU) of the exp-family methods without deltaA have the LDS
+  // for 32-step tiles: fewer barriers per step (bilinear and rglru would spill more)
+  constexpr int kT = (sizeof(IT) == 4 && kS == 8 && kNWm == 8 && !kDA && exp_family<kMethod>()) ? 32 : fwd_tile<IT, kS>();
   constexpr int kEl = 16 / sizeof(IT);   // elements per 16-byte block
   constexpr int kQ = kT / kEl;           // blocks per row
   constexpr int kG = kT / 4;             // groups of 4 steps
