@@ -8,8 +8,8 @@ autograd of the restated selective_scan_ref, lrnnx/ops/selective_scan.py:
   gradient of ``selective_scan_fn`` on every element.
 * Grids just above the 128-workgroup split limit (unsplit fast kernels at
   moderate L): bf16 B=3 D=2816 L=1024 and fp32 B=2 D=4160 L=512.
-* d_state 24 (bf16) and 32 (fp32) on the general kernels at 512 workgroups
-  (B=8 D=4096 L=256).
+* d_state 24 / 64 (bf16) and 32 / 48 (fp32) on the general kernels at 512
+  workgroups (B=8 D=4096 L=256).
 * The small-grid split of L against the unsplit schedule
   (LRNNX_SCAN_NO_SPLIT=1) at B=1 D=64 L=4160, both against the oracle.
 * 64 and 32 channels per workgroup (LRNNX_SCAN_CHANNELS) on one unsplit grid, both forms
@@ -115,11 +115,12 @@ def test_full_grid_vs_oracle(dev, case):
     _full_grid(dev, case)
 
 
-@pytest.mark.parametrize("N,itype", [(24, torch.bfloat16), (32, torch.float32)], ids=["n24_bf16", "n32_f32"])
-def test_general_dstate_17_to_32_large_grid_vs_oracle(dev, N, itype):
-    """d_state 17..32 on the general kernels (8 states per wave, at most 4
-    waves, LDS for two workgroups per CU) on a 512-workgroup grid, every
-    element."""
+@pytest.mark.parametrize("N,itype", [(24, torch.bfloat16), (32, torch.float32), (48, torch.float32), (64, torch.bfloat16)],
+                         ids=["n24_bf16", "n32_f32", "n48_f32", "n64_bf16"])
+def test_general_dstate_large_grid_vs_oracle(dev, N, itype):
+    """d_state 17..64 on the general kernels on a 512-workgroup grid, every
+    element: 17..32 in 4-wave workgroups (two per CU), 33..64 in 8-wave ones
+    (fp32: 32-step forward and 16-step backward tiles)."""
     _full_grid(dev, (f"general_n{N}", 8, 4096, 256, 11, itype), N=N)
 
 
