@@ -1,7 +1,20 @@
-// Selective scan with complex weights: backward (instantiation unit; kernels in ssc_impl.h).
+// Selective scan with complex weights: backward entry (workspace, checkpoint rebuild); the
+// kernels for each number of states per wave are instantiated in ssc_bwd_s<kS>.hip, which
+// compile in parallel.
 #include "ssc_impl.h"
 
 namespace lrnnx {
+namespace ssc {
+#define LRNNX_SSC_BWD_DECL(K)                                                                                   \
+  hipError_t ssc_bwd_s##K(const lrnnx_selective_scan_args& a, const SSCGeom& g, float* ws, const SSCBwdWs* wo, \
+                          const float* ckp, hipStream_t st);
+LRNNX_SSC_BWD_DECL(1)
+LRNNX_SSC_BWD_DECL(2)
+LRNNX_SSC_BWD_DECL(4)
+LRNNX_SSC_BWD_DECL(8)
+LRNNX_SSC_BWD_DECL(16)
+#undef LRNNX_SSC_BWD_DECL
+}  // namespace ssc
 
 hipError_t ssc_fwd_launch(const lrnnx_selective_scan_args& a, hipStream_t st);
 
@@ -23,7 +36,14 @@ hipError_t ssc_bwd_launch(const lrnnx_selective_scan_args& a, float* ws, const f
     if (e != hipSuccess) return e;
     ckp = ws + wo.ckpt;
   }
-  return ssc::ssc_dispatch<true>(a, g, ws, &wo, ckp, st);
+  switch (g.kS) {
+    case 1: return ssc::ssc_bwd_s1(a, g, ws, &wo, ckp, st);
+    case 2: return ssc::ssc_bwd_s2(a, g, ws, &wo, ckp, st);
+    case 4: return ssc::ssc_bwd_s4(a, g, ws, &wo, ckp, st);
+    case 8: return ssc::ssc_bwd_s8(a, g, ws, &wo, ckp, st);
+    case 16: return ssc::ssc_bwd_s16(a, g, ws, &wo, ckp, st);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace lrnnx
